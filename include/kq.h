@@ -1,0 +1,157 @@
+/*
+ * kq.h — C ABI of the MI355X (gfx950) quantized linear layer: Kidi's PACKED_LINEAR operator.
+ *
+ * This is the drop-in boundary. Kidi's C++ plugin contract for the operator is
+ *   runtime::OperatorBackend::prepare(const OperatorSpec&, TensorInputs) -> unique_ptr<Operator>
+ *                                                   (kidi: src/kidi/runtime/operator.h:120-136)
+ *   runtime::Operator::run(TensorInputs) / run_into(TensorInputs, span<Tensor>)   (operator.h:106-119)
+ * with spec {PACKED_LINEAR, attributes = [bits, group, bit_cast<int32>(output_scale)], epsilon = input_scale}
+ * and inputs {x F32 [..., K], W U8 [N, K/(8/bits)], S F32|F16 [N, K/g], (Z F32|F16 [N, K/g])}
+ * (src/kidi/ops/context.cpp:933-938, validation :207-218). The entry points below split that contract into
+ * load-time weight preparation (kq_weight_pack ~ the CPU backend's one-time tile packing,
+ * runtime/ynn/operators.cpp:1061-1089, :2761-2784) and the per-call projection (kq_packed_linear ~
+ * Operator::run_into, operators.cpp:1114). No function throws; every one returns a kq_status whose values map
+ * 1:1 onto kidi::core::ErrorCode (src/kidi/core/error.h:8-14), with a thread-local message in kq_last_error().
+ *
+ * Pointers named "device" are HBM addresses on the current HIP device; `stream` is a hipStream_t (NULL = the
+ * null stream). Calls are stream-ordered and asynchronous unless stated otherwise.
+ */
+#ifndef KIDI_AMD_KQ_H
+#define KIDI_AMD_KQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* kidi::core::ErrorCode + 1 (src/kidi/core/error.h:8-14); KQ_OK has no counterpart (a Result holding a value). */
+typedef enum kq_status {
+    KQ_OK = 0,
+    KQ_INVALID_ARGUMENT = 1,
+    KQ_IO = 2,
+    KQ_INVALID_MANIFEST = 3,
+    KQ_UNSUPPORTED = 4,
+    KQ_RUNTIME = 5
+} kq_status;
+
+/* Element types at the boundary (subset of kidi::tensor::DType, src/kidi/tensor/dtype.h:10-26), plus
+ * KQ_ZP_U8: one unsigned zero-point byte (0..15) per group, meaning the additive zero (8 - zp) * scale that
+ * ops::pack_weight stores (src/kidi/ops/quantization.cpp:85). */
+typedef enum kq_dtype {
+    KQ_NONE = -1,
+    KQ_F32 = 0,
+    KQ_F16 = 1,
+    KQ_BF16 = 2,
+    KQ_U8 = 3,
+    KQ_I8 = 4,
+    KQ_ZP_U8 = 5
+} kq_dtype;
+
+typedef enum kq_memory { KQ_HOST = 0, KQ_DEVICE = 1 } kq_memory;
+
+/* Which of Kidi's CPU operators defines the numerics of a call (runtime/ynn/operators.cpp:2739-2900):
+ *   KQ_PATH_BLOCKWISE  BlockwiseLinear (:1036-1181): dynamic per-(row, group) int8 activations;
+ *   KQ_PATH_SYMMETRIC  SymmetricPackedLinear (:1183-1319): calibrated activations q = rint(x / input_scale);
+ *   KQ_PATH_PORTABLE   PortablePackedLinearOp (:2639-2713): float activations, dequantized weights. */
+typedef enum kq_path { KQ_PATH_BLOCKWISE = 0, KQ_PATH_SYMMETRIC = 1, KQ_PATH_PORTABLE = 2 } kq_path;
+
+/* A packed weight resident in HBM, re-laid out once for gfx950 (1 KiB tiles of 16 output rows, lane-ordered
+ * so one wavefront load instruction moves a whole tile with 16-byte accesses). Immutable after packing. */
+typedef struct kq_weight kq_weight;
+
+typedef struct kq_pack_desc {
+    int32_t bits;          /* 2, 4 or 8 */
+    int32_t group_size;    /* g: cols % g == 0 and g % (8 / bits) == 0 */
+    int64_t rows;          /* N (output features) */
+    int64_t cols;          /* K (input features) */
+    const void* values;    /* Kidi layout: U8 [N, K/(8/bits)], element k in bits (k % (8/bits)) * bits of byte
+                              k / (8/bits), two's complement (I8 also accepted for 8-bit) */
+    kq_dtype values_dtype; /* KQ_U8 or KQ_I8 */
+    const void* scales;    /* [N, K/g] */
+    kq_dtype scales_dtype; /* KQ_F32 or KQ_F16 */
+    const void* zeros;     /* NULL, or [N, K/g] */
+    kq_dtype zeros_dtype;  /* KQ_NONE, KQ_F32 / KQ_F16 (additive zero), or KQ_ZP_U8 (zero-point) */
+    kq_memory memory;      /* where values / scales / zeros live */
+} kq_pack_desc;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* kq_last_error(void);
+
+/* Library/ABI version and the device architecture it was built for ("gfx950"). */
+int32_t kq_version(void);
+const char* kq_arch(void);
+
+/* Load-time packing: validate (Context::Impl::run PACKED_LINEAR checks, ops/context.cpp:207-218), re-lay out
+ * into the gfx950 tile format on the host and upload to the current device. Synchronous. The source buffers are
+ * not retained. Replaces BlockwiseLinear::pack_tiles / SymmetricPackedLinear::pack_tiles
+ * (runtime/ynn/operators.cpp:1061-1089, :1206-1231). */
+kq_status kq_weight_pack(const kq_pack_desc* desc, void* stream, kq_weight** out);
+
+/* Release a packed weight (device memory is freed after the device finishes queued work). */
+void kq_weight_free(kq_weight* weight);
+
+/* Shape of a packed weight. */
+kq_status kq_weight_info(const kq_weight* weight, int32_t* bits, int32_t* group_size, int64_t* rows,
+                         int64_t* cols, int32_t* has_zeros, size_t* device_bytes);
+
+/* Operator selection for a call (CpuBackend::prepare order, runtime/ynn/operators.cpp:2739-2900;
+ * BlockwiseLinear::supports :1038-1059; SymmetricPackedLinear::supports :1185-1204). */
+int32_t kq_select_path(int32_t bits, int64_t group_size, int64_t cols, int64_t rows, int32_t has_zeros,
+                       float input_scale);
+
+typedef struct kq_linear_args {
+    const void* x;          /* device [M, K], row-major */
+    kq_dtype x_dtype;       /* KQ_F32 (Kidi's contract, context.cpp:210) or KQ_BF16 */
+    int64_t m;              /* M (rows of x); 0 is a no-op */
+    float input_scale;      /* OperatorSpec::epsilon: 0 = dynamic activations, > 0 = calibrated */
+    float output_scale;     /* bit_cast of attributes[2]: > 0 rounds y to int8 steps of this size */
+    float* y;               /* device [M, N] F32 */
+    void* workspace;        /* device scratch of kq_linear_workspace_size() bytes, or NULL to use a grow-only
+                               per-device buffer owned by the library */
+    size_t workspace_bytes;
+} kq_linear_args;
+
+/* Device bytes of scratch kq_packed_linear needs for M rows (activation codes, block scales and sums). */
+size_t kq_linear_workspace_size(const kq_weight* weight, int64_t m);
+
+/* y = PACKED_LINEAR(x; weight) with Kidi's numerics for the selected path: Context::packed_linear
+ * (src/kidi/ops/context.cpp:821-939) -> Operator::run_into (runtime/ynn/operators.cpp:1114, :1250, :2667).
+ * Asynchronous on `stream`. */
+kq_status kq_packed_linear(const kq_weight* weight, const kq_linear_args* args, void* stream);
+
+/* Fused projections that share one activation read (Kidi fuses gate+up and k+v by concatenating rows,
+ * model/gemma4.cpp:308-322; its CUDA backend groups projections with one input, runtime/cuda/operators.cpp:366-437):
+ * kq_weight_pack_concat packs `count` weights with equal bits, group and K into one weight whose rows are the
+ * concatenation in order (e.g. fused QKV). Synchronous. */
+kq_status kq_weight_pack_concat(const kq_pack_desc* descs, int32_t count, void* stream, kq_weight** out);
+
+/* Gate/up projection fused with GELU-tanh gating: `weight` holds [gate rows; up rows] (2*I rows, as Kidi's
+ * gate_up_proj, model/gemma4.cpp:308-316); y [M, I] = gelu_tanh(x W_gate^T) * (x W_up^T)
+ * (Context::gelu_gate, ops/context.cpp:957-963; formula eager_test.cpp:444-452). */
+kq_status kq_packed_linear_gelu_gate(const kq_weight* weight, const kq_linear_args* args, void* stream);
+
+/* ---- parity instrumentation (same kernels as kq_packed_linear, with an extra store) --------------------- */
+
+/* Activation quantization exactly as the projection performs it: codes int8 [M, K] (natural k order),
+ * scales f32 [M, K/g], sums int32 [M, K/g] (sum of codes per block), zero_points int32 [M, K/g] (0 unless the
+ * 8-bit dynamic form). All outputs are device pointers. */
+kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_dtype, int64_t m, float input_scale,
+                            int8_t* codes, float* scales, int32_t* sums, int32_t* zero_points, void* stream);
+
+/* Runs the projection kernel that kq_packed_linear would run for these arguments and also writes its int32
+ * per-group partials [M, N, K/g]: sum over the group of x_code * w_code, where w_code = c (symmetric), u - zp
+ * (ZP_U8 zero-points, u = c + 8) or c (additive float zeros), and x_code = q - zp_a for 8-bit dynamic. */
+kq_status kq_debug_partials(const kq_weight* weight, const kq_linear_args* args, int32_t* partials, void* stream);
+
+/* Host-only (no GPU): the gfx950 tile layout of a Kidi-layout weight and its inverse, for layout tests. */
+size_t kq_layout_bytes(int32_t bits, int32_t group_size, int64_t rows, int64_t cols);
+kq_status kq_layout_encode_host(int32_t bits, int64_t rows, int64_t cols, const uint8_t* values, uint8_t* tiles);
+kq_status kq_layout_decode_host(int32_t bits, int64_t rows, int64_t cols, const uint8_t* tiles, int8_t* codes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KIDI_AMD_KQ_H */

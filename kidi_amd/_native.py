@@ -1,0 +1,116 @@
+"""ctypes binding of the C ABI in include/kq.h (kidi_amd/lib/libkq_hip.so).
+
+Importing this module fails loudly (ImportError) when the HIP library has not been built: there is no fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libkq_hip.so")
+
+# kq_status (kidi::core::ErrorCode + 1)
+KQ_OK, KQ_INVALID_ARGUMENT, KQ_IO, KQ_INVALID_MANIFEST, KQ_UNSUPPORTED, KQ_RUNTIME = range(6)
+STATUS_NAMES = {1: "INVALID_ARGUMENT", 2: "IO", 3: "INVALID_MANIFEST", 4: "UNSUPPORTED", 5: "RUNTIME"}
+# kq_dtype
+KQ_NONE, KQ_F32, KQ_F16, KQ_BF16, KQ_U8, KQ_I8, KQ_ZP_U8 = -1, 0, 1, 2, 3, 4, 5
+KQ_HOST, KQ_DEVICE = 0, 1
+PATH_BLOCKWISE, PATH_SYMMETRIC, PATH_PORTABLE = 0, 1, 2
+
+# Every symbol include/kq.h declares.
+EXPORTS = (
+    "kq_last_error", "kq_version", "kq_arch", "kq_weight_pack", "kq_weight_free", "kq_weight_info",
+    "kq_select_path", "kq_linear_workspace_size", "kq_packed_linear", "kq_weight_pack_concat",
+    "kq_packed_linear_gelu_gate", "kq_debug_quantize", "kq_debug_partials", "kq_layout_bytes",
+    "kq_layout_encode_host", "kq_layout_decode_host",
+)
+
+
+class PackDesc(ctypes.Structure):
+    _fields_ = [
+        ("bits", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+        ("values", ctypes.c_void_p),
+        ("values_dtype", ctypes.c_int),
+        ("scales", ctypes.c_void_p),
+        ("scales_dtype", ctypes.c_int),
+        ("zeros", ctypes.c_void_p),
+        ("zeros_dtype", ctypes.c_int),
+        ("memory", ctypes.c_int),
+    ]
+
+
+class LinearArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("x_dtype", ctypes.c_int),
+        ("m", ctypes.c_int64),
+        ("input_scale", ctypes.c_float),
+        ("output_scale", ctypes.c_float),
+        ("y", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class KqError(RuntimeError):
+    """A non-OK kq_status; ``code`` is the kidi::core::ErrorCode name."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.code = STATUS_NAMES.get(status, str(status))
+        super().__init__(f"{self.code}: {message}")
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"kidi_amd HIP library not built: {LIB_PATH} is missing (run __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i32, i64, f32, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
+    L.kq_last_error.restype = ctypes.c_char_p
+    L.kq_version.restype = i32
+    L.kq_arch.restype = ctypes.c_char_p
+    L.kq_weight_pack.argtypes = [ctypes.POINTER(PackDesc), vp, ctypes.POINTER(vp)]
+    L.kq_weight_pack.restype = ctypes.c_int
+    L.kq_weight_pack_concat.argtypes = [ctypes.POINTER(PackDesc), i32, vp, ctypes.POINTER(vp)]
+    L.kq_weight_pack_concat.restype = ctypes.c_int
+    L.kq_weight_free.argtypes = [vp]
+    L.kq_weight_free.restype = None
+    L.kq_weight_info.argtypes = [vp, ctypes.POINTER(i32), ctypes.POINTER(i32), ctypes.POINTER(i64),
+                                 ctypes.POINTER(i64), ctypes.POINTER(i32), ctypes.POINTER(sz)]
+    L.kq_weight_info.restype = ctypes.c_int
+    L.kq_select_path.argtypes = [i32, i64, i64, i64, i32, f32]
+    L.kq_select_path.restype = i32
+    L.kq_linear_workspace_size.argtypes = [vp, i64]
+    L.kq_linear_workspace_size.restype = sz
+    L.kq_packed_linear.argtypes = [vp, ctypes.POINTER(LinearArgs), vp]
+    L.kq_packed_linear.restype = ctypes.c_int
+    L.kq_packed_linear_gelu_gate.argtypes = [vp, ctypes.POINTER(LinearArgs), vp]
+    L.kq_packed_linear_gelu_gate.restype = ctypes.c_int
+    L.kq_debug_quantize.argtypes = [vp, vp, ctypes.c_int, i64, f32, vp, vp, vp, vp, vp]
+    L.kq_debug_quantize.restype = ctypes.c_int
+    L.kq_debug_partials.argtypes = [vp, ctypes.POINTER(LinearArgs), vp, vp]
+    L.kq_debug_partials.restype = ctypes.c_int
+    L.kq_layout_bytes.argtypes = [i32, i32, i64, i64]
+    L.kq_layout_bytes.restype = sz
+    L.kq_layout_encode_host.argtypes = [i32, i64, i64, vp, vp]
+    L.kq_layout_encode_host.restype = ctypes.c_int
+    L.kq_layout_decode_host.argtypes = [i32, i64, i64, vp, vp]
+    L.kq_layout_decode_host.restype = ctypes.c_int
+    _lib = L
+    return L
+
+
+def check(status: int) -> None:
+    if status != KQ_OK:
+        raise KqError(status, load().kq_last_error().decode())

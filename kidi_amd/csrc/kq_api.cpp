@@ -1,0 +1,544 @@
+// C ABI of the quantized linear layer (include/kq.h): validation, operator selection, load-time packing and
+// kernel dispatch. Mirrors Kidi's contract for PACKED_LINEAR: Context::Impl::run validation
+// (src/kidi/ops/context.cpp:207-218), Context::packed_linear scale checks (:821-825), the CPU backend's operator
+// selection (runtime/ynn/operators.cpp:2739-2900) and its errors (core/error.h:8-14). No function throws.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/kq.h"
+#include "kq_internal.hpp"
+
+namespace {
+
+thread_local std::string g_error;
+
+kq_status fail(kq_status code, const std::string& message) {
+    g_error = message;
+    return code;
+}
+
+kq_status hip_fail(hipError_t e, const char* what) {
+    return fail(KQ_RUNTIME, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+float half_bits_to_float(std::uint16_t h) {
+    // exact binary16 -> binary32 via the hardware-independent definition
+    const std::uint32_t sign = static_cast<std::uint32_t>(h & 0x8000u) << 16;
+    const std::uint32_t exponent = (h >> 10) & 0x1fu;
+    std::uint32_t mantissa = h & 0x3ffu;
+    std::uint32_t bits;
+    if (exponent == 0x1fu) bits = sign | 0x7f800000u | (mantissa << 13);
+    else if (exponent != 0) bits = sign | ((exponent + 112u) << 23) | (mantissa << 13);
+    else if (mantissa == 0) bits = sign;
+    else {
+        int shift = 0;
+        while ((mantissa & 0x400u) == 0) {
+            mantissa <<= 1;
+            ++shift;
+        }
+        bits = sign | (static_cast<std::uint32_t>(113 - shift) << 23) | ((mantissa & 0x3ffu) << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+std::size_t dtype_size(kq_dtype t) {
+    switch (t) {
+    case KQ_F32: return 4;
+    case KQ_F16:
+    case KQ_BF16: return 2;
+    case KQ_U8:
+    case KQ_I8:
+    case KQ_ZP_U8: return 1;
+    default: return 0;
+    }
+}
+
+int select_path(int bits, std::int64_t group, std::int64_t K, std::int64_t N, bool has_zero, float input_scale) {
+    if (input_scale <= 0.F) {
+        bool blockwise = group >= 32 && K % group == 0;
+        if (blockwise && bits == 4) blockwise = group % 32 == 0 && (has_zero || (group < K && N >= 256));
+        else if (blockwise && bits == 8) blockwise = group % 16 == 0 && !has_zero && N >= 64;
+        else blockwise = false;
+        if (blockwise) return kq::PATH_BLOCKWISE;
+    } else if (!has_zero && group > 0 && K % group == 0 && group % (8 / bits) == 0) {
+        return kq::PATH_SYMMETRIC;
+    }
+    return kq::PATH_PORTABLE;
+}
+
+std::int64_t act_rows(const kq::Weight& w, std::int64_t M) {
+    if (!w.tiled) return M;
+    if (M <= 4) return M;
+    if (M <= 8) return 8;
+    return kq::round_up(M, 128);
+}
+
+constexpr std::size_t kAlign = 256;
+std::size_t align_up(std::size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+// Grow-only per-device scratch used when the caller passes no workspace.
+struct Scratch {
+    void* ptr = nullptr;
+    std::size_t bytes = 0;
+};
+std::mutex g_scratch_mutex;
+std::map<int, Scratch> g_scratch;
+std::map<int, Scratch> g_gelu_scratch;
+
+kq_status device_scratch(std::map<int, Scratch>& pool, std::size_t bytes, void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    Scratch& s = pool[dev];
+    if (s.bytes < bytes) {
+        if (s.ptr) {
+            e = hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+            (void)hipFree(s.ptr);
+            s.ptr = nullptr;
+            s.bytes = 0;
+        }
+        e = hipMalloc(&s.ptr, bytes);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
+        s.bytes = bytes;
+    }
+    *out = s.ptr;
+    return KQ_OK;
+}
+
+kq_status validate_desc(const kq_pack_desc* d) {
+    if (!d) return fail(KQ_INVALID_ARGUMENT, "null pack descriptor");
+    const int bits = d->bits;
+    if ((bits != 2 && bits != 4 && bits != 8) || d->group_size <= 0)
+        return fail(KQ_INVALID_ARGUMENT, "invalid packed linear precision or group");
+    if (d->rows <= 0 || d->cols <= 0 || d->cols % d->group_size || d->group_size % (8 / bits))
+        return fail(KQ_INVALID_ARGUMENT, "packed linear shape or dtype mismatch");
+    if (!d->values || !(d->values_dtype == KQ_U8 || (bits == 8 && d->values_dtype == KQ_I8)))
+        return fail(KQ_INVALID_ARGUMENT, "packed linear shape or dtype mismatch");
+    if (!d->scales || (d->scales_dtype != KQ_F32 && d->scales_dtype != KQ_F16))
+        return fail(KQ_INVALID_ARGUMENT, "packed linear shape or dtype mismatch");
+    if (d->zeros && d->zeros_dtype != KQ_F32 && d->zeros_dtype != KQ_F16 && d->zeros_dtype != KQ_ZP_U8)
+        return fail(KQ_INVALID_ARGUMENT, "packed linear zero dtype must be F32, F16 or ZP_U8");
+    if (d->memory != KQ_HOST && d->memory != KQ_DEVICE) return fail(KQ_INVALID_ARGUMENT, "invalid memory kind");
+    return KQ_OK;
+}
+
+// Copy a descriptor's buffer to host memory (it may live on the device).
+kq_status fetch(const void* src, std::size_t bytes, kq_memory memory, std::vector<std::uint8_t>& out) {
+    out.resize(bytes);
+    if (memory == KQ_HOST) {
+        std::memcpy(out.data(), src, bytes);
+        return KQ_OK;
+    }
+    const hipError_t e = hipMemcpy(out.data(), src, bytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy(weight source)");
+    return KQ_OK;
+}
+
+struct HostWeight {
+    std::vector<std::uint8_t> values;  // Kidi layout, all descriptors concatenated by rows
+    std::vector<std::uint8_t> scales;  // [N][B] of the scale dtype
+    std::vector<std::uint8_t> zeros;   // [N][B] zero dtype, empty if none
+};
+
+kq_status pack_impl(const kq_pack_desc* descs, int count, void* stream, kq_weight** out) {
+    if (!out) return fail(KQ_INVALID_ARGUMENT, "null output handle");
+    *out = nullptr;
+    if (!descs || count <= 0) return fail(KQ_INVALID_ARGUMENT, "no weights to pack");
+    for (int i = 0; i < count; ++i)
+        if (kq_status s = validate_desc(&descs[i]); s != KQ_OK) return s;
+    const kq_pack_desc& d0 = descs[0];
+    std::int64_t N = 0;
+    for (int i = 0; i < count; ++i) {
+        const kq_pack_desc& d = descs[i];
+        if (d.bits != d0.bits || d.group_size != d0.group_size || d.cols != d0.cols || d.scales_dtype != d0.scales_dtype ||
+            (d.zeros == nullptr) != (d0.zeros == nullptr) || (d.zeros && d.zeros_dtype != d0.zeros_dtype))
+            return fail(KQ_INVALID_ARGUMENT, "concatenated weights must share bits, group, K and metadata types");
+        N += d.rows;
+    }
+    const int bits = d0.bits;
+    const int group = d0.group_size;
+    const std::int64_t K = d0.cols;
+    const std::int64_t B = K / group;
+    const std::int64_t row_bytes = K / (8 / bits);
+    const std::size_t ssz = dtype_size(d0.scales_dtype);
+    const bool has_zero = d0.zeros != nullptr;
+    const std::size_t zsz = has_zero ? dtype_size(d0.zeros_dtype) : 0;
+
+    HostWeight hw;
+    hw.values.resize(static_cast<std::size_t>(N * row_bytes));
+    hw.scales.resize(static_cast<std::size_t>(N * B) * ssz);
+    if (has_zero) hw.zeros.resize(static_cast<std::size_t>(N * B) * zsz);
+    std::int64_t r0 = 0;
+    for (int i = 0; i < count; ++i) {
+        const kq_pack_desc& d = descs[i];
+        std::vector<std::uint8_t> tmp;
+        if (kq_status s = fetch(d.values, static_cast<std::size_t>(d.rows * row_bytes), d.memory, tmp); s != KQ_OK) return s;
+        std::memcpy(hw.values.data() + r0 * row_bytes, tmp.data(), tmp.size());
+        if (kq_status s = fetch(d.scales, static_cast<std::size_t>(d.rows * B) * ssz, d.memory, tmp); s != KQ_OK) return s;
+        std::memcpy(hw.scales.data() + static_cast<std::size_t>(r0 * B) * ssz, tmp.data(), tmp.size());
+        if (has_zero) {
+            if (kq_status s = fetch(d.zeros, static_cast<std::size_t>(d.rows * B) * zsz, d.memory, tmp); s != KQ_OK) return s;
+            std::memcpy(hw.zeros.data() + static_cast<std::size_t>(r0 * B) * zsz, tmp.data(), tmp.size());
+        }
+        r0 += d.rows;
+    }
+
+    auto scale_at = [&](std::int64_t i) {
+        if (d0.scales_dtype == KQ_F32) {
+            float f;
+            std::memcpy(&f, hw.scales.data() + 4 * i, 4);
+            return f;
+        }
+        std::uint16_t h;
+        std::memcpy(&h, hw.scales.data() + 2 * i, 2);
+        return half_bits_to_float(h);
+    };
+    auto zero_at = [&](std::int64_t i) {
+        if (d0.zeros_dtype == KQ_F32) {
+            float f;
+            std::memcpy(&f, hw.zeros.data() + 4 * i, 4);
+            return f;
+        }
+        std::uint16_t h;
+        std::memcpy(&h, hw.zeros.data() + 2 * i, 2);
+        return half_bits_to_float(h);
+    };
+
+    auto* w = new (std::nothrow) kq::Weight();
+    if (!w) return fail(KQ_RUNTIME, "out of host memory");
+    w->geo = kq::Geometry::make(bits, group, N, K);
+    w->tiled = kq::tiled_group_ok(bits, group);
+    w->scale_type = d0.scales_dtype == KQ_F16 ? kq::META_F16 : kq::META_F32;
+    w->zero_mode = kq::ZERO_NONE;
+    std::vector<std::uint8_t> zp(static_cast<std::size_t>(N * B), 8);
+    if (has_zero) {
+        if (d0.zeros_dtype == KQ_ZP_U8) {
+            for (std::int64_t i = 0; i < N * B; ++i) {
+                if (hw.zeros[static_cast<std::size_t>(i)] > 15) {
+                    delete w;
+                    return fail(KQ_INVALID_ARGUMENT, "zero points must be in [0, 15]");
+                }
+                zp[static_cast<std::size_t>(i)] = hw.zeros[static_cast<std::size_t>(i)];
+            }
+            w->zero_mode = kq::ZERO_POINT;
+        } else {
+            // An additive zero of the form (8 - zp) * scale (ops::pack_weight, quantization.cpp:85) is carried as a
+            // 4-bit zero point and folded into the integer partial; anything else stays a float zero.
+            bool exact = bits == 4;
+            for (std::int64_t i = 0; exact && i < N * B; ++i) {
+                const float s = scale_at(i), z = zero_at(i);
+                if (!(s != 0.F) || !std::isfinite(s) || !std::isfinite(z)) {
+                    exact = false;
+                    break;
+                }
+                const float r = 8.0F - z / s;
+                const float zr = std::nearbyint(r);
+                if (zr < 0.F || zr > 15.F || (8.0F - zr) * s != z) {
+                    exact = false;
+                    break;
+                }
+                zp[static_cast<std::size_t>(i)] = static_cast<std::uint8_t>(zr);
+            }
+            if (exact) {
+                w->zero_mode = kq::ZERO_POINT;
+            } else {
+                w->zero_mode = kq::ZERO_FLOAT;
+                w->zero_type = d0.zeros_dtype == KQ_F16 ? kq::META_F16 : kq::META_F32;
+            }
+        }
+    }
+
+    // sizes
+    const kq::Geometry& g = w->geo;
+    std::size_t off = 0;
+    const std::size_t tiles_off = off;
+    off = align_up(off + static_cast<std::size_t>(w->tiled ? g.tile_bytes_total() : N * row_bytes));
+    const std::int64_t meta_n = w->tiled ? g.meta_count() : N * B;
+    const std::size_t scales_off = off;
+    off = align_up(off + static_cast<std::size_t>(meta_n) * ssz);
+    std::size_t zp_off = 0, zeros_off = 0, cs_off = 0;
+    if (w->zero_mode == kq::ZERO_POINT) {
+        zp_off = off;
+        off = align_up(off + static_cast<std::size_t>(w->tiled ? meta_n / 2 : meta_n));
+    }
+    if (w->zero_mode == kq::ZERO_FLOAT) {
+        zeros_off = off;
+        off = align_up(off + static_cast<std::size_t>(meta_n) * zsz);
+    }
+    if (w->tiled && bits == 8) {
+        cs_off = off;
+        off = align_up(off + static_cast<std::size_t>(meta_n) * 4);
+    }
+    std::vector<std::uint8_t> image(off, 0);
+    if (w->tiled) {
+        kq::encode_tiles(bits, N, K, hw.values.data(), image.data() + tiles_off);
+        for (std::int64_t n = 0; n < N; ++n)
+            for (std::int64_t b = 0; b < B; ++b) {
+                const std::int64_t mi = g.meta_index(n, b), si = n * B + b;
+                std::memcpy(image.data() + scales_off + static_cast<std::size_t>(mi) * ssz,
+                            hw.scales.data() + static_cast<std::size_t>(si) * ssz, ssz);
+                if (w->zero_mode == kq::ZERO_POINT) {
+                    std::uint8_t& byte = image[zp_off + static_cast<std::size_t>((mi - n % kq::kTileRows) / 2 + (n % kq::kTileRows) / 2)];
+                    byte = static_cast<std::uint8_t>(byte | (zp[static_cast<std::size_t>(si)] << (4 * (n & 1))));
+                }
+                if (w->zero_mode == kq::ZERO_FLOAT)
+                    std::memcpy(image.data() + zeros_off + static_cast<std::size_t>(mi) * zsz,
+                                hw.zeros.data() + static_cast<std::size_t>(si) * zsz, zsz);
+                if (bits == 8) {
+                    std::int32_t sum = 0;
+                    for (std::int64_t c = 0; c < group; ++c)
+                        sum += static_cast<std::int8_t>(hw.values[static_cast<std::size_t>(n * row_bytes + b * group + c)]);
+                    std::memcpy(image.data() + cs_off + static_cast<std::size_t>(mi) * 4, &sum, 4);
+                }
+            }
+    } else {
+        std::memcpy(image.data() + tiles_off, hw.values.data(), hw.values.size());
+        std::memcpy(image.data() + scales_off, hw.scales.data(), hw.scales.size());
+        if (w->zero_mode == kq::ZERO_POINT) std::memcpy(image.data() + zp_off, zp.data(), zp.size());
+        if (w->zero_mode == kq::ZERO_FLOAT) std::memcpy(image.data() + zeros_off, hw.zeros.data(), hw.zeros.size());
+    }
+
+    hipError_t e = hipGetDevice(&w->device);
+    if (e != hipSuccess) {
+        delete w;
+        return hip_fail(e, "hipGetDevice");
+    }
+    e = hipMalloc(&w->allocation, off);
+    if (e != hipSuccess) {
+        delete w;
+        return hip_fail(e, "hipMalloc(weight)");
+    }
+    auto* base = static_cast<std::uint8_t*>(w->allocation);
+    e = hipMemcpyAsync(base, image.data(), off, hipMemcpyHostToDevice, static_cast<hipStream_t>(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+        (void)hipFree(w->allocation);
+        delete w;
+        return hip_fail(e, "upload weight");
+    }
+    w->bytes = off;
+    w->tiles = base + tiles_off;
+    w->scales = base + scales_off;
+    if (w->zero_mode == kq::ZERO_POINT) w->zero_points = base + zp_off;
+    if (w->zero_mode == kq::ZERO_FLOAT) w->zeros = base + zeros_off;
+    if (w->tiled && bits == 8) w->code_sums = reinterpret_cast<std::int32_t*>(base + cs_off);
+    *out = reinterpret_cast<kq_weight*>(w);
+    return KQ_OK;
+}
+
+const kq::Weight* as_weight(const kq_weight* w) { return reinterpret_cast<const kq::Weight*>(w); }
+
+kq_status prepare_call(const kq_weight* weight, const kq_linear_args* args, bool gelu, kq::LinearCall& c,
+                       std::size_t* ws_needed) {
+    if (!weight || !args) return fail(KQ_INVALID_ARGUMENT, "null weight or arguments");
+    const kq::Weight& w = *as_weight(weight);
+    if (!std::isfinite(args->input_scale) || args->input_scale < 0 || !std::isfinite(args->output_scale) ||
+        args->output_scale < 0)
+        return fail(KQ_INVALID_ARGUMENT, "invalid calibrated projection scales");
+    if (args->m < 0) return fail(KQ_INVALID_ARGUMENT, "negative row count");
+    if (args->x_dtype != KQ_F32 && args->x_dtype != KQ_BF16)
+        return fail(KQ_INVALID_ARGUMENT, "packed linear input must be F32 or BF16");
+    if (args->m > 0 && (!args->x || !args->y)) return fail(KQ_INVALID_ARGUMENT, "null input or output");
+    if (gelu && (w.geo.rows % 2)) return fail(KQ_INVALID_ARGUMENT, "GELU gate requires an even number of rows");
+    c = kq::LinearCall{};
+    c.w = &w;
+    c.x = args->x;
+    c.x_type = args->x_dtype == KQ_BF16 ? kq::ACT_BF16 : kq::ACT_F32;
+    c.M = args->m;
+    c.input_scale = args->input_scale;
+    c.output_scale = args->output_scale;
+    c.y = args->y;
+    c.path = select_path(w.geo.bits, w.geo.group, w.geo.cols, w.geo.rows, w.zero_mode != kq::ZERO_NONE, args->input_scale);
+    c.gelu_gate = gelu;
+    *ws_needed = c.path == kq::PATH_PORTABLE ? 0 : kq::workspace_bytes(w, c.M);
+    return KQ_OK;
+}
+
+kq_status run_call(kq::LinearCall& c, const kq_linear_args* args, std::size_t ws_needed, hipStream_t stream) {
+    if (c.M == 0) return KQ_OK;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev != c.w->device) return fail(KQ_INVALID_ARGUMENT, "weight was packed on another device");
+    void* ws = args->workspace;
+    if (ws_needed) {
+        if (ws) {
+            if (args->workspace_bytes < ws_needed) return fail(KQ_INVALID_ARGUMENT, "workspace too small");
+        } else if (kq_status s = device_scratch(g_scratch, ws_needed, &ws); s != KQ_OK) {
+            return s;
+        }
+        c.act = kq::carve_workspace(*c.w, c.M, ws);
+    }
+    // GELU gating is fused into the tiled GEMV/GEMM when the gate and up halves are whole tiles; otherwise the
+    // full projection goes to a scratch buffer and a gating kernel follows.
+    const bool fused_gelu = c.gelu_gate && c.path != kq::PATH_PORTABLE && c.w->tiled && (c.w->geo.rows / 2) % kq::kTileRows == 0;
+    float* final_y = c.y;
+    if (c.gelu_gate && !fused_gelu) {
+        void* tmp = nullptr;
+        if (kq_status s = device_scratch(g_gelu_scratch, static_cast<std::size_t>(c.M * c.w->geo.rows) * 4, &tmp); s != KQ_OK)
+            return s;
+        c.y = static_cast<float*>(tmp);
+        c.gelu_gate = false;
+    }
+    e = kq::launch_quantize(c, stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize launch");
+    e = kq::launch_linear(c, stream);
+    if (e != hipSuccess) return hip_fail(e, "projection launch");
+    if (c.y != final_y) {
+        e = kq::launch_gelu_gate(c.y, c.M, c.w->geo.rows / 2, final_y, stream);
+        if (e != hipSuccess) return hip_fail(e, "gelu gate launch");
+    }
+    return KQ_OK;
+}
+
+}  // namespace
+
+namespace kq {
+
+std::size_t workspace_bytes(const Weight& w, std::int64_t M) {
+    const std::int64_t rows = act_rows(w, M);
+    const std::int64_t cols = w.tiled ? w.geo.cols_p : w.geo.cols;
+    const std::int64_t groups = w.tiled ? w.geo.groups_p : w.geo.cols / w.geo.group;
+    return align_up(static_cast<std::size_t>(rows * cols)) + 3 * align_up(static_cast<std::size_t>(rows * groups) * 4);
+}
+
+ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base) {
+    ActBuffers a;
+    a.rows_p = act_rows(w, M);
+    const std::int64_t cols = w.tiled ? w.geo.cols_p : w.geo.cols;
+    const std::int64_t groups = w.tiled ? w.geo.groups_p : w.geo.cols / w.geo.group;
+    auto* p = static_cast<std::uint8_t*>(base);
+    a.q = reinterpret_cast<std::int8_t*>(p);
+    p += align_up(static_cast<std::size_t>(a.rows_p * cols));
+    a.scale = reinterpret_cast<float*>(p);
+    p += align_up(static_cast<std::size_t>(a.rows_p * groups) * 4);
+    a.sum = reinterpret_cast<std::int32_t*>(p);
+    p += align_up(static_cast<std::size_t>(a.rows_p * groups) * 4);
+    a.zero = reinterpret_cast<std::int32_t*>(p);
+    return a;
+}
+
+}  // namespace kq
+
+extern "C" {
+
+const char* kq_last_error(void) { return g_error.c_str(); }
+
+int32_t kq_version(void) { return 1; }
+
+const char* kq_arch(void) { return "gfx950"; }
+
+kq_status kq_weight_pack(const kq_pack_desc* desc, void* stream, kq_weight** out) { return pack_impl(desc, 1, stream, out); }
+
+kq_status kq_weight_pack_concat(const kq_pack_desc* descs, int32_t count, void* stream, kq_weight** out) {
+    return pack_impl(descs, count, stream, out);
+}
+
+void kq_weight_free(kq_weight* weight) {
+    if (!weight) return;
+    auto* w = reinterpret_cast<kq::Weight*>(weight);
+    if (w->allocation) (void)hipFree(w->allocation);
+    delete w;
+}
+
+kq_status kq_weight_info(const kq_weight* weight, int32_t* bits, int32_t* group_size, int64_t* rows, int64_t* cols,
+                         int32_t* has_zeros, size_t* device_bytes) {
+    if (!weight) return fail(KQ_INVALID_ARGUMENT, "null weight");
+    const kq::Weight& w = *as_weight(weight);
+    if (bits) *bits = w.geo.bits;
+    if (group_size) *group_size = w.geo.group;
+    if (rows) *rows = w.geo.rows;
+    if (cols) *cols = w.geo.cols;
+    if (has_zeros) *has_zeros = w.zero_mode != kq::ZERO_NONE;
+    if (device_bytes) *device_bytes = w.bytes;
+    return KQ_OK;
+}
+
+int32_t kq_select_path(int32_t bits, int64_t group_size, int64_t cols, int64_t rows, int32_t has_zeros, float input_scale) {
+    if ((bits != 2 && bits != 4 && bits != 8) || group_size <= 0) return -1;
+    return select_path(bits, group_size, cols, rows, has_zeros != 0, input_scale);
+}
+
+size_t kq_linear_workspace_size(const kq_weight* weight, int64_t m) {
+    if (!weight || m < 0) return 0;
+    return kq::workspace_bytes(*as_weight(weight), m);
+}
+
+kq_status kq_packed_linear(const kq_weight* weight, const kq_linear_args* args, void* stream) {
+    kq::LinearCall c;
+    std::size_t ws = 0;
+    if (kq_status s = prepare_call(weight, args, false, c, &ws); s != KQ_OK) return s;
+    return run_call(c, args, ws, static_cast<hipStream_t>(stream));
+}
+
+kq_status kq_packed_linear_gelu_gate(const kq_weight* weight, const kq_linear_args* args, void* stream) {
+    kq::LinearCall c;
+    std::size_t ws = 0;
+    if (kq_status s = prepare_call(weight, args, true, c, &ws); s != KQ_OK) return s;
+    return run_call(c, args, ws, static_cast<hipStream_t>(stream));
+}
+
+kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_dtype, int64_t m, float input_scale,
+                            int8_t* codes, float* scales, int32_t* sums, int32_t* zero_points, void* stream) {
+    kq_linear_args args{};
+    args.x = x;
+    args.x_dtype = x_dtype;
+    args.m = m;
+    args.input_scale = input_scale;
+    args.y = reinterpret_cast<float*>(codes);  // unused, must be non-null
+    kq::LinearCall c;
+    std::size_t ws_bytes = 0;
+    if (kq_status s = prepare_call(weight, &args, false, c, &ws_bytes); s != KQ_OK) return s;
+    if (c.path == kq::PATH_PORTABLE) return fail(KQ_UNSUPPORTED, "the portable path does not quantize activations");
+    if (m == 0) return KQ_OK;
+    void* ws = nullptr;
+    if (kq_status s = device_scratch(g_scratch, ws_bytes, &ws); s != KQ_OK) return s;
+    c.act = kq::carve_workspace(*c.w, m, ws);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = kq::launch_quantize(c, st);
+    if (e == hipSuccess && codes) e = kq::launch_unpermute_codes(*c.w, c.act, m, codes, st);
+    if (e == hipSuccess) e = kq::launch_copy_block_stats(*c.w, c.act, m, scales, sums, zero_points, st);
+    if (e != hipSuccess) return hip_fail(e, "debug quantize");
+    return KQ_OK;
+}
+
+kq_status kq_debug_partials(const kq_weight* weight, const kq_linear_args* args, int32_t* partials, void* stream) {
+    kq::LinearCall c;
+    std::size_t ws = 0;
+    if (kq_status s = prepare_call(weight, args, false, c, &ws); s != KQ_OK) return s;
+    if (c.path == kq::PATH_PORTABLE) return fail(KQ_UNSUPPORTED, "the portable path has no integer partials");
+    c.dump = partials;
+    return run_call(c, args, ws, static_cast<hipStream_t>(stream));
+}
+
+size_t kq_layout_bytes(int32_t bits, int32_t group_size, int64_t rows, int64_t cols) {
+    if ((bits != 2 && bits != 4 && bits != 8) || rows <= 0 || cols <= 0) return 0;
+    return static_cast<size_t>(kq::Geometry::make(bits, group_size, rows, cols).tile_bytes_total());
+}
+
+kq_status kq_layout_encode_host(int32_t bits, int64_t rows, int64_t cols, const uint8_t* values, uint8_t* tiles) {
+    if ((bits != 2 && bits != 4 && bits != 8) || rows <= 0 || cols <= 0 || cols % (8 / bits) || !values || !tiles)
+        return fail(KQ_INVALID_ARGUMENT, "invalid layout arguments");
+    kq::encode_tiles(bits, rows, cols, values, tiles);
+    return KQ_OK;
+}
+
+kq_status kq_layout_decode_host(int32_t bits, int64_t rows, int64_t cols, const uint8_t* tiles, int8_t* codes) {
+    if ((bits != 2 && bits != 4 && bits != 8) || rows <= 0 || cols <= 0 || !tiles || !codes)
+        return fail(KQ_INVALID_ARGUMENT, "invalid layout arguments");
+    kq::decode_tiles(bits, rows, cols, tiles, codes);
+    return KQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,74 @@
+// Internal types shared by the C ABI (kq_api.cpp) and the kernels (kq_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "kq_layout.hpp"
+
+namespace kq {
+
+enum MetaType : int { META_F32 = 0, META_F16 = 1 };
+enum ZeroMode : int { ZERO_NONE = 0, ZERO_POINT = 1, ZERO_FLOAT = 2 };
+enum ActType : int { ACT_F32 = 0, ACT_BF16 = 1 };
+enum Path : int { PATH_BLOCKWISE = 0, PATH_SYMMETRIC = 1, PATH_PORTABLE = 2 };
+
+// Device-resident packed weight. Either the tiled layout (kq_layout.hpp) or, for group sizes the tiles cannot
+// carry, Kidi's own row-major layout.
+struct Weight {
+    Geometry geo;
+    bool tiled = true;
+    int scale_type = META_F32;
+    int zero_mode = ZERO_NONE;
+    int zero_type = META_F32;       // for ZERO_FLOAT
+    std::uint8_t* tiles = nullptr;  // tiled codes, or Kidi-layout values [N, K/(8/bits)]
+    void* scales = nullptr;         // tiled: [n_tiles][groups_p][16]; row-major: [N][K/g]
+    std::uint8_t* zero_points = nullptr;  // ZERO_POINT: tiled [n_tiles][groups_p][8] nibbles; row-major [N][K/g] bytes
+    void* zeros = nullptr;          // ZERO_FLOAT: same indexing as scales
+    std::int32_t* code_sums = nullptr;  // 8-bit tiled: sum of codes per (row, group), [n_tiles][groups_p][16]
+    void* allocation = nullptr;     // one hipMalloc holding all of the above
+    std::size_t bytes = 0;
+    int device = 0;
+};
+
+// Activation workspace carved out of one device buffer.
+struct ActBuffers {
+    std::int8_t* q = nullptr;       // [rows_p][cols_p] permuted (tiled) or [M][K] natural (row-major)
+    float* scale = nullptr;         // [rows_p][groups_p]
+    std::int32_t* sum = nullptr;    // [rows_p][groups_p]
+    std::int32_t* zero = nullptr;   // [rows_p][groups_p]
+    std::int64_t rows_p = 0;
+};
+
+struct LinearCall {
+    const Weight* w;
+    const void* x;
+    int x_type;
+    std::int64_t M;
+    float input_scale, output_scale;
+    float* y;
+    int path;
+    bool gelu_gate;                 // y [M, N/2] = gelu_tanh(first half) * second half
+    std::int32_t* dump;             // optional int32 partials [M][N][K/g]
+    ActBuffers act;
+};
+
+std::size_t workspace_bytes(const Weight& w, std::int64_t M);
+ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base);
+
+// Kernel launchers (kq_kernels.hip). Return hipSuccess or the launch error.
+hipError_t launch_quantize(const LinearCall& c, hipStream_t stream);
+hipError_t launch_linear(const LinearCall& c, hipStream_t stream);
+hipError_t launch_gelu_gate(const float* in, std::int64_t M, std::int64_t I, float* out, hipStream_t stream);
+hipError_t launch_unpermute_codes(const Weight& w, const ActBuffers& act, std::int64_t M, std::int8_t* codes,
+                                  hipStream_t stream);
+hipError_t launch_copy_block_stats(const Weight& w, const ActBuffers& act, std::int64_t M, float* scales,
+                                   std::int32_t* sums, std::int32_t* zero_points, hipStream_t stream);
+
+// Host-side layout (kq_layout_host.cpp).
+void encode_tiles(int bits, std::int64_t rows, std::int64_t cols, const std::uint8_t* values, std::uint8_t* tiles);
+void decode_tiles(int bits, std::int64_t rows, std::int64_t cols, const std::uint8_t* tiles, std::int8_t* codes);
+
+}  // namespace kq

@@ -1,0 +1,248 @@
+"""Host-side mirror of Kidi's packed-linear entry points, over the HIP C ABI (include/kq.h).
+
+Kidi's caller-facing interface for this path is ``ops::Context`` (src/kidi/ops/context.h:72-203):
+``packed_linear`` (context.cpp:821-939), ``bind_packed_zero`` (:813-815), ``gelu_gate`` (:957-963), and the
+dispatcher's prepared-operator cache keyed by parameter storage identity (:148-194, :366-382). This module keeps
+those names, argument meanings and error behaviour (``Failure`` carrying the ErrorCode name) for tensors that live
+in PyTorch-ROCm device memory. PyTorch is only the allocator and stream here; every projection runs in
+``libkq_hip.so``.
+"""
+
+from __future__ import annotations
+
+import collections
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _native as N
+
+
+class Failure(RuntimeError):
+    """ops::Failure (src/kidi/ops/context.h:52-59): ``code`` is the kidi::core::ErrorCode name."""
+
+    def __init__(self, code: str, message: str):
+        self.code = code
+        super().__init__(f"{code}: {message}")
+
+
+def _raise(status: int) -> None:
+    if status != N.KQ_OK:
+        raise Failure(N.STATUS_NAMES.get(status, "RUNTIME"), N.load().kq_last_error().decode())
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _meta_dtype(t: torch.Tensor, what: str) -> int:
+    if t.dtype == torch.float32:
+        return N.KQ_F32
+    if t.dtype == torch.float16:
+        return N.KQ_F16
+    if what == "zeros" and t.dtype == torch.uint8:
+        return N.KQ_ZP_U8
+    raise Failure("INVALID_ARGUMENT", "packed linear shape or dtype mismatch")
+
+
+@dataclass
+class PackedWeight:
+    """ops::PackedWeight (src/kidi/ops/quantization.h:6-11)."""
+
+    values: torch.Tensor
+    scales: torch.Tensor
+    zeros: torch.Tensor | None
+    bits: int
+    group_size: int
+
+
+class DeviceWeight:
+    """A packed weight re-laid out for gfx950 and resident in HBM (kq_weight)."""
+
+    def __init__(self, values, scales, bits: int, group_size: int, zeros=None, concat=None):
+        lib = N.load()
+        parts = concat if concat is not None else [(values, scales, zeros)]
+        descs = (N.PackDesc * len(parts))()
+        self._keep = []
+        rows = 0
+        for i, (v, s, z) in enumerate(parts):
+            if v.dim() != 2 or s.dim() != 2:
+                raise Failure("INVALID_ARGUMENT", "packed linear shape or dtype mismatch")
+            v = v.contiguous()
+            s = s.contiguous()
+            z = z.contiguous() if z is not None else None
+            dev = v.is_cuda
+            if s.is_cuda != dev or (z is not None and z.is_cuda != dev):
+                raise Failure("INVALID_ARGUMENT", "packed weight parts must share one device")
+            self._keep += [v, s, z]
+            d = descs[i]
+            d.bits = bits
+            d.group_size = group_size
+            d.rows = v.shape[0]
+            d.cols = v.shape[1] * (8 // bits) if bits in (2, 4, 8) else 0
+            d.values = v.data_ptr()
+            d.values_dtype = N.KQ_I8 if v.dtype == torch.int8 else (N.KQ_U8 if v.dtype == torch.uint8 else 99)
+            d.scales = s.data_ptr()
+            d.scales_dtype = _meta_dtype(s, "scales")
+            d.zeros = z.data_ptr() if z is not None else None
+            d.zeros_dtype = _meta_dtype(z, "zeros") if z is not None else N.KQ_NONE
+            d.memory = N.KQ_DEVICE if dev else N.KQ_HOST
+            if s.shape[0] != v.shape[0] or (group_size > 0 and s.shape[1] * group_size != d.cols):
+                raise Failure("INVALID_ARGUMENT", "packed linear shape or dtype mismatch")
+            rows += v.shape[0]
+        handle = ctypes.c_void_p()
+        if concat is None:
+            status = lib.kq_weight_pack(descs, _stream() if torch.cuda.is_available() else None, ctypes.byref(handle))
+        else:
+            status = lib.kq_weight_pack_concat(descs, len(parts), _stream() if torch.cuda.is_available() else None,
+                                               ctypes.byref(handle))
+        self._keep = None
+        _raise(status)
+        self.handle = handle
+        self.bits, self.group_size, self.rows = bits, group_size, rows
+        self.cols = descs[0].cols
+        self.has_zeros = parts[0][2] is not None
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and h.value:
+            N.load().kq_weight_free(h)
+            self.handle = None
+
+    def path(self, input_scale: float) -> int:
+        return N.load().kq_select_path(self.bits, self.group_size, self.cols, self.rows, int(self.has_zeros), input_scale)
+
+    def workspace_size(self, m: int) -> int:
+        return N.load().kq_linear_workspace_size(self.handle, m)
+
+    def _args(self, x: torch.Tensor, y: torch.Tensor, m: int, input_scale: float, output_scale: float):
+        ws_bytes = self.workspace_size(m)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+        a = N.LinearArgs()
+        a.x = x.data_ptr()
+        a.x_dtype = N.KQ_BF16 if x.dtype == torch.bfloat16 else (N.KQ_F32 if x.dtype == torch.float32 else 99)
+        a.m = m
+        a.input_scale = input_scale
+        a.output_scale = output_scale
+        a.y = y.data_ptr()
+        a.workspace = ws.data_ptr()
+        a.workspace_bytes = ws_bytes
+        return a, ws
+
+    def linear(self, x: torch.Tensor, input_scale: float = 0.0, output_scale: float = 0.0,
+               out: torch.Tensor | None = None, gelu_gate: bool = False) -> torch.Tensor:
+        """y [..., N] (or [..., N/2] with GELU gating) for x [..., K] F32/BF16 on the device."""
+        if x.dim() < 1 or x.shape[-1] != self.cols:
+            raise Failure("INVALID_ARGUMENT", "packed linear shape or dtype mismatch")
+        x2 = x.reshape(-1, self.cols).contiguous()
+        m = x2.shape[0]
+        width = self.rows // 2 if gelu_gate else self.rows
+        y = out if out is not None else torch.empty((m, width), dtype=torch.float32, device=x.device)
+        a, ws = self._args(x2, y, m, input_scale, output_scale)
+        fn = N.load().kq_packed_linear_gelu_gate if gelu_gate else N.load().kq_packed_linear
+        _raise(fn(self.handle, ctypes.byref(a), _stream()))
+        return y.reshape(*x.shape[:-1], width)
+
+    def debug_partials(self, x: torch.Tensor, input_scale: float = 0.0, output_scale: float = 0.0):
+        """(y, int32 partials [M, N, K/g]) from the same kernel as ``linear``."""
+        x2 = x.reshape(-1, self.cols).contiguous()
+        m = x2.shape[0]
+        y = torch.empty((m, self.rows), dtype=torch.float32, device=x.device)
+        P = torch.zeros((m, self.rows, self.cols // self.group_size), dtype=torch.int32, device=x.device)
+        a, ws = self._args(x2, y, m, input_scale, output_scale)
+        _raise(N.load().kq_debug_partials(self.handle, ctypes.byref(a), P.data_ptr(), _stream()))
+        return y, P
+
+    def debug_quantize(self, x: torch.Tensor, input_scale: float = 0.0):
+        """(codes int8 [M, K], scales f32 [M, B], sums int32 [M, B], zero points int32 [M, B])."""
+        x2 = x.reshape(-1, self.cols).contiguous()
+        m = x2.shape[0]
+        B = self.cols // self.group_size
+        codes = torch.zeros((m, self.cols), dtype=torch.int8, device=x.device)
+        s = torch.zeros((m, B), dtype=torch.float32, device=x.device)
+        q = torch.zeros((m, B), dtype=torch.int32, device=x.device)
+        z = torch.zeros((m, B), dtype=torch.int32, device=x.device)
+        xt = N.KQ_BF16 if x2.dtype == torch.bfloat16 else N.KQ_F32
+        _raise(N.load().kq_debug_quantize(self.handle, x2.data_ptr(), xt, m, input_scale, codes.data_ptr(),
+                                          s.data_ptr(), q.data_ptr(), z.data_ptr(), _stream()))
+        return codes, s, q, z
+
+
+def _identity(t: torch.Tensor | None):
+    if t is None:
+        return None
+    return (t.device.type, t.untyped_storage().data_ptr(), t.storage_offset(), tuple(t.shape), t.dtype)
+
+
+class Context:
+    """The packed-linear slice of ops::Context on one HIP device."""
+
+    CAPACITY = 4096  # bounded prepared-operator cache (ops/context.cpp:368-375)
+
+    def __init__(self, device: str | torch.device = "cuda"):
+        self.device = torch.device(device)
+        self._prepared: collections.OrderedDict = collections.OrderedDict()
+        self._zeros: dict = {}
+
+    def bind_packed_zero(self, scales: torch.Tensor, zeros: torch.Tensor) -> None:
+        """Context::bind_packed_zero (ops/context.cpp:813-815)."""
+        if scales is not None and zeros is not None:
+            self._zeros[_identity(scales)] = zeros
+
+    def _prepare(self, weight, scales, bits, group_size, zeros) -> DeviceWeight:
+        key = (_identity(weight), _identity(scales), _identity(zeros), bits, group_size)
+        found = self._prepared.get(key)
+        if found is not None:
+            self._prepared.move_to_end(key)
+            return found[0]
+        dw = DeviceWeight(weight, scales, bits, group_size, zeros)
+        self._prepared[key] = (dw, weight, scales, zeros)
+        if len(self._prepared) > self.CAPACITY:
+            self._prepared.popitem(last=False)
+        return dw
+
+    @staticmethod
+    def _validate(input, weight, scales, bits, group_size, input_scale, output_scale):
+        # Context::packed_linear (ops/context.cpp:824-825) then Impl::run validation (:207-218)
+        if not math.isfinite(input_scale) or input_scale < 0 or not math.isfinite(output_scale) or output_scale < 0:
+            raise Failure("INVALID_ARGUMENT", "invalid calibrated projection scales")
+        if bits not in (2, 4, 8) or group_size <= 0:
+            raise Failure("INVALID_ARGUMENT", "invalid packed linear precision or group")
+        per = 8 // bits
+        K = input.shape[-1] if input.dim() else 0
+        if (input.dtype not in (torch.float32, torch.bfloat16) or input.dim() < 2 or not K or K % group_size
+                or group_size % per or weight.dtype != torch.uint8 or weight.dim() != 2 or not weight.shape[0]
+                or weight.shape[1] != K // per or scales.dtype not in (torch.float32, torch.float16)
+                or scales.dim() != 2 or scales.shape[0] != weight.shape[0] or scales.shape[1] != K // group_size):
+            raise Failure("INVALID_ARGUMENT", "packed linear shape or dtype mismatch")
+
+    def packed_linear(self, input: torch.Tensor, weight: torch.Tensor, scales: torch.Tensor, bits: int,
+                      group_size: int, input_scale: float = 0.0, output_scale: float = 0.0,
+                      zeros: torch.Tensor | None = None) -> torch.Tensor:
+        """Context::packed_linear (ops/context.cpp:821-939) for CHECKPOINT precision: F32 [..., N] output."""
+        self._validate(input, weight, scales, bits, group_size, input_scale, output_scale)
+        bound = zeros if zeros is not None else self._zeros.get(_identity(scales))
+        dw = self._prepare(weight, scales, bits, group_size, bound)
+        host = not input.is_cuda
+        x = input.to(self.device) if host else input
+        y = dw.linear(x, input_scale, output_scale)
+        if host:  # a HIP op behind a CPU tensor returns host-visible results (synchronous)
+            y = y.cpu()
+        return y
+
+    def packed_linear_gelu_gate(self, input: torch.Tensor, weight: torch.Tensor, scales: torch.Tensor, bits: int,
+                                group_size: int, input_scale: float = 0.0, output_scale: float = 0.0,
+                                zeros: torch.Tensor | None = None) -> torch.Tensor:
+        """gelu_gate(packed_linear(x, gate_up)) in one pass: Kidi's gate_up_proj followed by Context::gelu_gate
+        (ops/context.cpp:957-963, layers/gemma4.cpp:206-210)."""
+        self._validate(input, weight, scales, bits, group_size, input_scale, output_scale)
+        if weight.shape[0] % 2:
+            raise Failure("INVALID_ARGUMENT", "GELU gate requires floating [..., 2 * intermediate] input")
+        bound = zeros if zeros is not None else self._zeros.get(_identity(scales))
+        dw = self._prepare(weight, scales, bits, group_size, bound)
+        host = not input.is_cuda
+        x = input.to(self.device) if host else input
+        y = dw.linear(x, input_scale, output_scale, gelu_gate=True)
+        return y.cpu() if host else y

@@ -1,0 +1,339 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C ABI (ctypes) on the same seeded inputs.
+
+Bar: int8 activation codes, block sums and int32 per-group partials bit-exact; fp32 outputs within
+max|dy| <= 2e-3 * max|y_ref|; exact equality where the reference pins exact values (calibrated KATs)."""
+
+import numpy as np
+import pytest
+
+from tests.cases import activations, pack_codes, weights
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from kidi_amd import _native
+
+    _native.load()
+    return torch.device("cuda:0")
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def device_weight(values, scales, bits, group, dev, zeros=None, zero_points=None, on_device=True):
+    from kidi_amd.ops import DeviceWeight
+
+    conv = (lambda a: to_dev(a, dev)) if on_device else (lambda a: torch.from_numpy(np.ascontiguousarray(a)))
+    z = zeros if zeros is not None else zero_points
+    return DeviceWeight(conv(values), conv(scales), bits, group, conv(z) if z is not None else None)
+
+
+def expected_partials(ref, q, codes, zpa, bits, group, zero_points=None, dynamic=True):
+    """P' as the kernels define it: sum q*c, plus (8 - zp) * Q for uint4 zero points, minus zp_a * C for 8-bit."""
+    P, C = ref.partials(q, codes, group)
+    P = P.astype(np.int64)
+    M, K = q.shape
+    B = K // group
+    Q = q.astype(np.int64).reshape(M, B, group).sum(axis=2)
+    if zero_points is not None:
+        P = P + (8 - zero_points.astype(np.int64))[None, :, :] * Q[:, None, :]
+    if bits == 8 and dynamic:
+        P = P - zpa.astype(np.int64)[:, None, :] * C.astype(np.int64)[None, :, :]
+    return P
+
+
+def check_close(y, y_ref, tol=TOL):
+    y = y.detach().cpu().numpy() if hasattr(y, "detach") else y
+    scale = max(float(np.max(np.abs(y_ref))), 1e-30)
+    err = float(np.max(np.abs(y - y_ref))) if y.size else 0.0
+    assert err <= tol * scale, f"max|dy| = {err:.3g} > {tol} * {scale:.3g}"
+
+
+CASES = [
+    # (bits, group, M, K, N, zeros, input_scale, x_bf16, outliers)
+    (4, 32, 1, 256, 512, None, 0.0, False, 0.0),
+    (4, 32, 3, 512, 256, None, 0.0, True, 0.0),
+    (4, 128, 1, 512, 272, "zp", 0.0, True, 0.001),
+    (4, 128, 4, 1024, 256, "zp", 0.0, True, 0.001),
+    (4, 64, 2, 512, 320, "zp", 0.0, False, 0.0),
+    (4, 256, 1, 1024, 256, None, 0.0, False, 0.0),
+    (4, 128, 5, 512, 256, "f16", 0.0, False, 0.0),
+    (8, 32, 1, 256, 128, None, 0.0, True, 0.0),
+    (8, 32, 8, 512, 192, None, 0.0, False, 0.001),
+    (8, 128, 3, 512, 64, None, 0.0, False, 0.0),
+    (2, 32, 1, 512, 256, None, 0.05, False, 0.0),
+    (2, 128, 6, 512, 128, None, 0.05, True, 0.0),
+    (4, 32, 2, 256, 256, None, 0.05, False, 0.0),
+    (8, 64, 1, 256, 128, None, 0.03, False, 0.0),
+    # prefill GEMM shapes (M > 8, ragged M and N)
+    (4, 128, 130, 512, 272, "zp", 0.0, True, 0.001),
+    (4, 32, 129, 256, 256, None, 0.0, False, 0.0),
+    (4, 64, 200, 256, 384, "zp", 0.0, False, 0.0),
+    (4, 256, 64, 512, 256, None, 0.0, False, 0.0),
+    (4, 128, 40, 256, 256, "f16", 0.0, False, 0.0),
+    (8, 32, 150, 256, 200, None, 0.0, False, 0.001),
+    (8, 128, 17, 256, 64, None, 0.0, True, 0.0),
+    (2, 32, 140, 512, 144, None, 0.05, False, 0.0),
+    (2, 128, 33, 512, 128, None, 0.05, False, 0.0),
+    (4, 32, 257, 256, 128, None, 0.05, False, 0.0),
+    # group sizes the tiles cannot carry (row-major integer path)
+    (4, 96, 3, 384, 256, "zp", 0.0, False, 0.0),
+    (8, 48, 2, 288, 96, None, 0.0, False, 0.0),
+    (8, 48, 20, 192, 64, None, 0.0, False, 0.0),
+]
+
+
+def _make(ref, case, seed):
+    bits, group, M, K, N, zeros, input_scale, x_bf16, outliers = case
+    rng = np.random.default_rng(seed)
+    values, scales, zp, codes = weights(rng, N, K, bits, group, zero_points=zeros in ("zp", "f16"))
+    zf = None
+    if zeros == "f16":
+        # an additive F16 zero that is not (8 - zp) * scale: stays a float zero on the device
+        zf = rng.uniform(-0.05, 0.05, size=scales.shape).astype(np.float16)
+        zp = None
+    x = activations(rng, M, K, outliers)
+    return bits, group, M, K, N, values, scales, zp, zf, codes, x, input_scale, x_bf16
+
+
+@pytest.mark.parametrize("index", range(len(CASES)),
+                         ids=[f"b{c[0]}g{c[1]}m{c[2]}k{c[3]}n{c[4]}{c[5] or ''}s{c[6]}" for c in CASES])
+def test_projection_parity(dev, ref, index):
+    case = CASES[index]
+    print(f"case {case}", flush=True)
+    bits, group, M, K, N, values, scales, zp, zf, codes, x, in_s, x_bf16 = _make(ref, case, 1000 + index)
+    y_ref, path = ref.packed_linear(x, values, scales, bits, group, in_s, 0.0, zeros=zf, zero_points=zp)
+    assert path != ref.PATH_PORTABLE
+    dw = device_weight(values, scales, bits, group, dev, zeros=zf, zero_points=zp)
+    xt = to_dev(x, dev)
+    if x_bf16:
+        xt = xt.to(torch.bfloat16)
+    # activation codes and block statistics: bit-exact
+    if in_s == 0:
+        q_ref, s_ref, Q_ref, zpa_ref = ref.quantize_dynamic(x, group, bits)
+    else:
+        (q_ref, Q_ref), s_ref, zpa_ref = ref.quantize_static(x, group, in_s), None, None
+    codes_d, s_d, Q_d, z_d = dw.debug_quantize(xt, in_s)
+    np.testing.assert_array_equal(codes_d.cpu().numpy(), q_ref)
+    np.testing.assert_array_equal(Q_d.cpu().numpy(), Q_ref)
+    if in_s == 0:
+        np.testing.assert_array_equal(s_d.cpu().numpy(), s_ref)
+        np.testing.assert_array_equal(z_d.cpu().numpy(), zpa_ref)
+    # int32 per-group partials: bit-exact
+    y_d, P_d = dw.debug_partials(xt, in_s)
+    P_ref = expected_partials(ref, q_ref, codes, zpa_ref, bits, group, zero_points=zp, dynamic=in_s == 0)
+    np.testing.assert_array_equal(P_d.cpu().numpy().astype(np.int64), P_ref)
+    # fp32 outputs
+    check_close(y_d, y_ref)
+    y = dw.linear(xt, in_s)
+    torch.cuda.synchronize()
+    check_close(y, y_ref)
+    np.testing.assert_array_equal(y.cpu().numpy(), y_d.cpu().numpy())  # the dump variant computes the same y
+
+
+def test_eager_calibrated_projection_exact_gpu(dev, ref):
+    """tests/kidi/layers/eager_test.cpp:64-111 through the HIP path: exact equality, bits 2/4/8, g = K = 256."""
+    WIDTH = 256
+    for bits in (2, 4, 8):
+        per = 8 // bits
+        for columns in (3, 35, 67, 257, 513):
+            idx = np.arange(columns * WIDTH, dtype=np.int64)
+            integers = ((idx * 13 + idx // WIDTH * 7 + idx // (WIDTH * 3) + 3) % (1 << bits)) - (1 << (bits - 1))
+            weight = pack_codes(integers.reshape(columns, WIDTH), bits)
+            factors = np.full((columns, 1), 0.001953125, np.float32)
+            values = ((np.arange(WIDTH) % 17) - 8).astype(np.float32) * np.float32(0.125)
+            values[0], values[1] = -1000.0, 1000.0
+            y_ref, _ = ref.packed_linear(values[None, :], weight, factors, bits, WIDTH, 0.25, 0.125)
+            dw = device_weight(weight, factors, bits, WIDTH, dev)
+            y = dw.linear(to_dev(values[None, :], dev), 0.25, 0.125).cpu().numpy()
+            np.testing.assert_array_equal(y, y_ref)
+
+
+def test_cuda_kat_gpu(dev):
+    """tests/kidi/runtime/cuda/operators_test.cpp:815-831 bytes, g=2 (row-major path); hand-worked values."""
+    w = np.array([[0xE1, 0xC3], [0x54, 0x7A]], np.uint8)
+    s = np.array([[0.25, 0.5], [0.125, 0.25]], np.float32)
+    x = np.array([[0.25, -0.5, 0.75, -1], [-0.25, 0.5, -0.75, 1]], np.float32)
+    dw = device_weight(w, s, 4, 2, dev)
+    y = dw.linear(to_dev(x, dev), 0.25, 0.125).cpu().numpy()
+    np.testing.assert_array_equal(y, np.array([[3.5, -3.0], [-3.5, 3.0]], np.float32))
+
+
+@pytest.mark.parametrize("bits,group,N,M,in_s", [(4, 128, 35, 3, 0.0), (4, 4, 2, 1, 0.0), (2, 32, 256, 2, 0.0),
+                                                 (8, 32, 63, 2, 0.0), (4, 128, 256, 2, 0.5)])
+def test_portable_path(dev, ref, bits, group, N, M, in_s):
+    """Float path (PortablePackedLinearOp) domains: N < 256 without zeros, g < 32, dynamic 2-bit, 8-bit N < 64,
+    calibrated with zeros. The GPU sums k in the oracle's order without contraction: equal to the last bit."""
+    rng = np.random.default_rng(N * 7 + bits)
+    K = 256
+    values, scales, zp, _ = weights(rng, N, K, bits, group, zero_points=in_s > 0)
+    x = activations(rng, M, K)
+    y_ref, path = ref.packed_linear(x, values, scales, bits, group, in_s, 0.0, zero_points=zp)
+    assert path == ref.PATH_PORTABLE
+    dw = device_weight(values, scales, bits, group, dev, zero_points=zp)
+    y = dw.linear(to_dev(x, dev), in_s).cpu().numpy()
+    np.testing.assert_array_equal(y, y_ref)
+
+
+def test_eager_pack_weight_group4_gpu(dev, ref):
+    """eager_test.cpp:300-345 on the device: pack_weight g=4, portable projection within 1e-3, 33 rows."""
+    weights_ = np.array([0, -7, 7, 1, 0, 14, -14, 2, 0, 0, 0, 0, 7, -7, 1, -1], np.float32).reshape(2, 8)
+    act = np.array([0, 1, 2, 3, 4, 5, 6, 255], np.float32)
+    for bits in (2, 4, 8):
+        v, s, _ = ref.pack_weight(weights_, bits, 4)
+        y_ref, _ = ref.packed_linear(act[None, :], v, s, bits, 4)
+        dw = device_weight(v, s, bits, 4, dev)
+        y = dw.linear(to_dev(np.tile(act, (33, 1)), dev)).cpu().numpy()
+        assert np.all(np.abs(y - y_ref[0][None, :]) <= 1e-3)
+
+
+def test_output_calibration(dev, ref):
+    """output_scale > 0 rounds y to int8 steps: codes agree except where y_ref sits within fp32 noise of a
+    rounding boundary, and then by one step."""
+    rng = np.random.default_rng(9)
+    values, scales, zp, _ = weights(rng, 512, 1024, 4, 128, zero_points=True)
+    x = activations(rng, 2, 1024)
+    out_s = 0.01
+    y_ref, _ = ref.packed_linear(x, values, scales, 4, 128, 0.0, out_s, zero_points=zp)
+    y = device_weight(values, scales, 4, 128, dev, zero_points=zp).linear(to_dev(x, dev), 0.0, out_s).cpu().numpy()
+    steps = np.rint((y - y_ref) / out_s)
+    assert np.all(np.abs(steps) <= 1)
+    assert np.mean(steps == 0) > 0.99
+
+
+def test_host_source_and_repeat(dev, ref):
+    """Weights packed from host memory equal weights packed from device memory; repeated calls are identical."""
+    rng = np.random.default_rng(4)
+    values, scales, zp, _ = weights(rng, 256, 512, 4, 128, zero_points=True)
+    x = to_dev(activations(rng, 1, 512), dev)
+    a = device_weight(values, scales, 4, 128, dev, zero_points=zp, on_device=False).linear(x)
+    b = device_weight(values, scales, 4, 128, dev, zero_points=zp, on_device=True)
+    y1, y2 = b.linear(x), b.linear(x)
+    torch.cuda.synchronize()
+    assert torch.equal(a, y1) and torch.equal(y1, y2)
+
+
+def test_pack_weight_asymmetric_zeros_become_zero_points(dev, ref):
+    """ops::pack_weight asymmetric output (F32 zeros = (8 - zp) * scale) runs the integer zero-point fold."""
+    rng = np.random.default_rng(21)
+    w = (rng.standard_normal((256, 512)) * 0.05).astype(np.float32)
+    v, s, z = ref.pack_weight(w, 4, 128, asymmetric_clip=True)
+    x = activations(rng, 3, 512)
+    y_ref, path = ref.packed_linear(x, v, s, 4, 128, zeros=z)
+    assert path == ref.PATH_BLOCKWISE
+    dw = device_weight(v, s, 4, 128, dev, zeros=z)
+    check_close(dw.linear(to_dev(x, dev)), y_ref)
+    zp = np.rint(8 - z / s).astype(np.uint8)
+    _, P = dw.debug_partials(to_dev(x, dev))
+    q, _, _, _ = ref.quantize_dynamic(x, 128, 4)
+    np.testing.assert_array_equal(P.cpu().numpy(), expected_partials(ref, q, ref.unpack_codes(v, 512, 4), None, 4, 128,
+                                                                      zero_points=zp))
+
+
+def test_zero_block_and_empty(dev, ref):
+    """An all-zero activation block quantizes to codes 0 / scale 0 and contributes nothing; M = 0 is a no-op."""
+    rng = np.random.default_rng(5)
+    values, scales, zp, _ = weights(rng, 256, 256, 4, 32, zero_points=True)
+    x = activations(rng, 2, 256)
+    x[0, 32:64] = 0.0
+    x[1, :] = 0.0
+    y_ref, _ = ref.packed_linear(x, values, scales, 4, 32, zero_points=zp)
+    dw = device_weight(values, scales, 4, 32, dev, zero_points=zp)
+    y = dw.linear(to_dev(x, dev)).cpu().numpy()
+    check_close(y, y_ref)
+    assert np.all(y[1] == 0)
+    empty = dw.linear(torch.zeros((0, 256), device=dev))
+    assert tuple(empty.shape) == (0, 256)
+
+
+@pytest.mark.parametrize("M", [1, 4, 200])
+def test_gelu_gate_fused(dev, ref, M):
+    """gate/up projection + GELU-tanh in one pass equals the oracle's projection followed by gelu_gate."""
+    rng = np.random.default_rng(M)
+    I, K = 256, 512
+    values, scales, zp, _ = weights(rng, 2 * I, K, 4, 128, zero_points=True)
+    x = activations(rng, M, K)
+    y_full, _ = ref.packed_linear(x, values, scales, 4, 128, zero_points=zp)
+    h_ref = ref.gelu_gate(y_full)
+    from kidi_amd.ops import Context
+
+    ctx = Context(dev)
+    h = ctx.packed_linear_gelu_gate(to_dev(x, dev), to_dev(values, dev), to_dev(scales, dev), 4, 128,
+                                    zeros=to_dev(zp, dev))
+    check_close(h, h_ref, tol=5e-3)
+
+
+def test_fused_qkv_concat(dev, ref):
+    """Fused QKV (one weight of N = 2048 + 256 + 256 rows, g = 32) equals the three projections side by side."""
+    rng = np.random.default_rng(31)
+    K = 2048
+    parts = [weights(rng, n, K, 4, 32) for n in (2048, 256, 256)]
+    x = activations(rng, 1, K)
+    from kidi_amd.ops import DeviceWeight
+
+    fused = DeviceWeight(None, None, 4, 32, concat=[(to_dev(v, dev), to_dev(s, dev), None) for v, s, _, _ in parts])
+    y = fused.linear(to_dev(x, dev)).cpu().numpy()
+    y_ref = np.concatenate([ref.packed_linear(x, v, s, 4, 32)[0] for v, s, _, _ in parts], axis=1)
+    check_close(y, y_ref)
+
+
+def test_context_mirror(dev, ref):
+    """Context.packed_linear: host tensors in, host tensors out; validation errors carry Kidi's error codes."""
+    from kidi_amd.ops import Context, Failure
+
+    rng = np.random.default_rng(8)
+    values, scales, zp, _ = weights(rng, 256, 256, 4, 128, zero_points=True)
+    x = activations(rng, 2, 256)
+    ctx = Context(dev)
+    v, s, z = torch.from_numpy(values), torch.from_numpy(scales), torch.from_numpy(zp)
+    ctx.bind_packed_zero(s, z)
+    y = ctx.packed_linear(torch.from_numpy(x), v, s, 4, 128)
+    y_ref, _ = ref.packed_linear(x, values, scales, 4, 128, zero_points=zp)
+    check_close(y.numpy(), y_ref)
+    with pytest.raises(Failure) as e:
+        ctx.packed_linear(torch.from_numpy(x), v, s, 4, 96)
+    assert e.value.code == "INVALID_ARGUMENT"
+    with pytest.raises(Failure) as e:
+        ctx.packed_linear(torch.from_numpy(x), v, s, 4, 128, input_scale=-1.0)
+    assert e.value.code == "INVALID_ARGUMENT"
+
+
+@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("shape", [(2048, 8192), (8192, 2048)])
+def test_baseline_decode_shapes(dev, ref, M, shape):
+    """Config 2 at full size: asymmetric int4 g=128, bf16 activations with 0.1% outliers x20."""
+    K, N = shape
+    rng = np.random.default_rng(2)
+    values, scales, zp, codes = weights(rng, N, K, 4, 128, zero_points=True)
+    x = activations(rng, M, K, outliers=0.001)
+    y_ref, _ = ref.packed_linear(x, values, scales, 4, 128, zero_points=zp, threads=8)
+    dw = device_weight(values, scales, 4, 128, dev, zero_points=zp)
+    xt = to_dev(x, dev).to(torch.bfloat16)
+    y_d, P_d = dw.debug_partials(xt)
+    q, _, _, _ = ref.quantize_dynamic(x, 128, 4)
+    np.testing.assert_array_equal(P_d.cpu().numpy().astype(np.int64),
+                                  expected_partials(ref, q, codes, None, 4, 128, zero_points=zp))
+    check_close(dw.linear(xt), y_ref)
+
+
+def test_baseline_prefill_rows(dev, ref):
+    """Config 3 (M=2048, K=2048, N=8192, asymmetric g=128): rows are independent, so a sample of 16 rows of the
+    full GEMM output is checked against the oracle on those rows; all rows are finite."""
+    M, K, N = 2048, 2048, 8192
+    rng = np.random.default_rng(3)
+    values, scales, zp, _ = weights(rng, N, K, 4, 128, zero_points=True)
+    x = activations(rng, M, K)
+    dw = device_weight(values, scales, 4, 128, dev, zero_points=zp)
+    y = dw.linear(to_dev(x, dev).to(torch.bfloat16)).cpu().numpy()
+    assert np.all(np.isfinite(y))
+    rows = np.sort(rng.choice(M, size=16, replace=False))
+    y_ref, _ = ref.packed_linear(x[rows], values, scales, 4, 128, zero_points=zp, threads=8)
+    check_close(y[rows], y_ref)
