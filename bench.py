@@ -228,6 +228,13 @@ def main():
     ms_per_step = dev_ms / args.steps
     bytes_step = gemv_bytes(M_DEC, K_DEC, N_DEC, G_DEC)
     value = bytes_step / (ms_per_step * 1e-3) / 1e9
+    # The decode step is one kernel launch (kq_packed_linear -> skinny_kernel: activation quantization fused), so the
+    # per-launch device time over the timed region is the kernel's average launch duration including the launch
+    # gap between back-to-back kernels on the stream.
+    roofline = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "skinny_kernel (fused quantize + int8 MFMA GEMV)", "bytes_per_launch": bytes_step,
+                "us_per_launch": round(ms_per_step * 1e3, 3)}
 
     # MALL-resident figure (one weight, repeated): reported separately, never as HBM %
     g1 = capture(torch, [projs[0]] * 64, stream_ptr)
@@ -298,7 +305,7 @@ def main():
         "config": {"workload": "decode GEMV, asymmetric int4 g=128, M=1, K=2048, N=8192 (configs[1] up-proj)",
                    "rotated_weights": R, "weight_working_set_MB": round(R * projs_bytes(N_DEC, K_DEC, G_DEC) / 1e6, 1),
                    "launch": "HIP graph replay, one stream"},
-        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "roofline": roofline,
         "wall_s": round(wall, 4),
         "parity": parity,
         "mall_resident_gbs": round(bytes_step / (mall_ms * 1e-3) / 1e9, 1),

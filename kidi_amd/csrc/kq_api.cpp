@@ -371,6 +371,13 @@ kq_status run_call(kq::LinearCall& c, const kq_linear_args* args, std::size_t ws
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     if (dev != c.w->device) return fail(KQ_INVALID_ARGUMENT, "weight was packed on another device");
+    // Decode (M <= 16): one fused launch, no workspace.
+    kq::SkinnyPlan plan;
+    if (kq::skinny_plan(c, plan)) {
+        e = kq::launch_skinny(c, plan, stream);
+        if (e != hipSuccess) return hip_fail(e, "skinny projection launch");
+        return KQ_OK;
+    }
     void* ws = args->workspace;
     if (ws_needed) {
         if (ws) {
@@ -502,10 +509,25 @@ kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_d
     if (kq_status s = prepare_call(weight, &args, false, c, &ws_bytes); s != KQ_OK) return s;
     if (c.path == kq::PATH_PORTABLE) return fail(KQ_UNSUPPORTED, "the portable path does not quantize activations");
     if (m == 0) return KQ_OK;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    kq::SkinnyPlan plan;
+    if (kq::skinny_plan(c, plan)) {
+        // the fused quantizer of the decode projection reports what it computed
+        void* ybuf = nullptr;
+        if (kq_status s = device_scratch(g_gelu_scratch, static_cast<std::size_t>(m * c.w->geo.rows) * 4, &ybuf); s != KQ_OK)
+            return s;
+        c.y = static_cast<float*>(ybuf);
+        c.dq_codes = codes;
+        c.dq_scales = scales;
+        c.dq_sums = sums;
+        c.dq_zeros = zero_points;
+        const hipError_t e = kq::launch_skinny(c, plan, st);
+        if (e != hipSuccess) return hip_fail(e, "debug quantize");
+        return KQ_OK;
+    }
     void* ws = nullptr;
     if (kq_status s = device_scratch(g_scratch, ws_bytes, &ws); s != KQ_OK) return s;
     c.act = kq::carve_workspace(*c.w, m, ws);
-    const hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e = kq::launch_quantize(c, st);
     if (e == hipSuccess && codes) e = kq::launch_unpermute_codes(*c.w, c.act, m, codes, st);
     if (e == hipSuccess) e = kq::launch_copy_block_stats(*c.w, c.act, m, scales, sums, zero_points, st);

@@ -53,7 +53,23 @@ struct LinearCall {
     bool gelu_gate;                 // y [M, N/2] = gelu_tanh(first half) * second half
     std::int32_t* dump;             // optional int32 partials [M][N][K/g]
     ActBuffers act;
+    // optional dumps of the fused (skinny) quantizer: codes [M][K] natural order, block stats [M][K/g]
+    std::int8_t* dq_codes = nullptr;
+    float* dq_scales = nullptr;
+    std::int32_t* dq_sums = nullptr;
+    std::int32_t* dq_zeros = nullptr;
 };
+
+// Launch plan of the skinny (decode, M <= 16) projection with fused activation quantization (kq_skinny.hip).
+struct SkinnyPlan {
+    int R = 1, W = 1, T = 4;
+    int chunk_tiles = 1;
+    int wave_lds = 0, off_stats = 0, off_meta = 0, red_off = 0, lds_bytes = 0;
+    std::int64_t blocks = 0;
+};
+
+bool skinny_plan(const LinearCall& c, SkinnyPlan& p);
+hipError_t launch_skinny(const LinearCall& c, const SkinnyPlan& p, hipStream_t stream);
 
 std::size_t workspace_bytes(const Weight& w, std::int64_t M);
 ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base);

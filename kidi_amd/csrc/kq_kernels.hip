@@ -17,45 +17,19 @@
 
 #include <cstdint>
 
+#include "kq_device.hpp"
 #include "kq_internal.hpp"
 
 namespace kq {
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
+using namespace dev;
 
-__device__ __forceinline__ float meta_load(const float* p, std::int64_t i) { return p[i]; }
-__device__ __forceinline__ float meta_load(const __half* p, std::int64_t i) { return __half2float(p[i]); }
-
-__device__ __forceinline__ float load_act(const void* x, int type, std::int64_t i) {
-    if (type == ACT_BF16) return __uint_as_float(static_cast<std::uint32_t>(static_cast<const std::uint16_t*>(x)[i]) << 16);
-    return static_cast<const float*>(x)[i];
-}
-
-__device__ __forceinline__ float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
-
-// Static output rounding (eager_test.cpp:100-102): clamp(rint(y / out), -128, 127) * out when out > 0.
-__device__ __forceinline__ float calibrate_output(float v, float out) {
-    return out > 0.F ? clampf(__builtin_rintf(v / out), -128.F, 127.F) * out : v;
-}
-
-__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
-
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
-
-// Streaming 16-byte weight load (each weight byte is read once per projection).
-__device__ __forceinline__ uint4 load_stream(const uint4* p) {
-    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 // ---------------------------------------------------------------------------------------------------------------
-// Activation quantization (tiled order). One group of g columns is handled by T = g/8 lanes (T a power of two up
-// to 64; larger groups loop), each lane owning 8-column chunks whose codes land at act_position(k0).
-//   dynamic symmetric (2/4-bit weights), hnsw_test.cpp:513-520: s = max/127, q = clamp(rint(x * (127/max)), +-127);
-//     an all-zero block gives codes 0 and s = 0.
-//   dynamic asymmetric (8-bit weights), hnsw_test.cpp:492-511: XNNPACK-style zero point, std::round ties away.
-//   calibrated, eager_test.cpp:97-98: q = clamp(rint(x / input_scale), -128, 127).
+// Activation quantization into a workspace (used ahead of the prefill GEMM, M > 16). One group of g columns is
+// handled by T = g/8 lanes (T a power of two up to 64; larger groups loop), each lane owning 8-column chunks whose
+// codes land at act_position(k0). Arithmetic: quant_block / quant_code (kq_device.hpp).
 // Rows >= M and columns >= K (tile padding) get codes 0, scale 0, sum 0, zero point 0.
 struct QuantArgs {
     const void* x;
@@ -89,44 +63,14 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantArgs a) {
         const std::int64_t k0 = static_cast<std::int64_t>(b) * a.group + 8 * c;
         if (!live_row || k0 >= a.K) continue;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float v = load_act(a.x, a.x_type, m * a.K + k0 + i);
-            if (MODE == 1) {
-                mn = fminf(mn, v);
-                mx = fmaxf(mx, v);
-            } else {
-                mx = fmaxf(mx, fabsf(v));
-            }
-        }
+        for (int i = 0; i < 8; ++i) quant_stat(MODE, load_act(a.x, a.x_type, m * a.K + k0 + i), mx, mn);
     }
     for (int off = T / 2; off >= 1; off >>= 1) {
         mx = fmaxf(mx, __shfl_xor(mx, off));
-        if (MODE == 1) mn = fminf(mn, __shfl_xor(mn, off));
+        if (MODE == QUANT_DYN_ASYM) mn = fminf(mn, __shfl_xor(mn, off));
     }
     const bool live_block = live_row && static_cast<std::int64_t>(b) * a.group < a.K;
-
-    float s = 0.F, inverse = 0.F;
-    int zp = 0;
-    if (MODE == 0) {
-        if (mx > 0.F) {
-            inverse = 127.F / mx;
-            s = mx / 127.F;
-        }
-    } else if (MODE == 1) {
-        const float rdiff = mx - mn;
-        inverse = rdiff > 0.F ? 255.F / rdiff : 0.F;
-        s = rdiff > 0.F ? rdiff / 255.F : 1.F;
-        const float min_error = -128.F + mn * inverse;
-        const float max_error = 127.F + mx * inverse;
-        const float fzp = min_error + max_error > 0.F ? -128.F - mn * inverse : 127.F - mx * inverse;
-        zp = rdiff > 0.F ? static_cast<int>(__builtin_rintf(clampf(fzp, -128.F, 127.F))) : -128;
-        if (!live_block) {
-            s = 0.F;
-            zp = 0;
-        }
-    } else {
-        s = a.input_scale;
-    }
+    const QuantBlock p = quant_block(MODE, mx, mn, a.input_scale, live_block);
 
     // pass 2: codes
     int total = 0;
@@ -137,16 +81,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantArgs a) {
         if (live_row && k0 < a.K) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float v = load_act(a.x, a.x_type, m * a.K + k0 + i);
-                int code;
-                if (MODE == 0) {
-                    code = mx > 0.F ? static_cast<int>(clampf(__builtin_rintf(v * inverse), -127.F, 127.F)) : 0;
-                } else if (MODE == 1) {
-                    code = static_cast<int>(roundf(v * inverse)) + zp;
-                    code = code < -128 ? -128 : (code > 127 ? 127 : code);
-                } else {
-                    code = static_cast<int>(clampf(__builtin_rintf(v / a.input_scale), -128.F, 127.F));
-                }
+                const int code = quant_code(MODE, load_act(a.x, a.x_type, m * a.K + k0 + i), p, a.input_scale);
                 total += code;
                 const std::uint32_t byte = static_cast<std::uint32_t>(code) & 0xFFu;
                 if (i < 4) lo |= byte << (8 * i);
@@ -164,9 +99,9 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantArgs a) {
     for (int off = T / 2; off >= 1; off >>= 1) total += __shfl_xor(total, off);
     if (valid && sub == 0) {
         const std::int64_t o = m * a.groups_p + b;
-        a.scale[o] = live_block ? s : 0.F;
+        a.scale[o] = p.s;
         a.sum[o] = total;
-        a.zero[o] = live_block ? zp : 0;
+        a.zero[o] = p.zp;
     }
 }
 
@@ -179,107 +114,18 @@ __global__ __launch_bounds__(256) void quantize_rowmajor_kernel(QuantArgs a) {
     const std::int64_t m = gid / blocks, b = gid % blocks;
     const std::int64_t base = m * a.K + b * a.group;
     float mx = 0.F, mn = 0.F;
-    for (int c = 0; c < a.group; ++c) {
-        const float v = load_act(a.x, a.x_type, base + c);
-        if (MODE == 1) {
-            mn = fminf(mn, v);
-            mx = fmaxf(mx, v);
-        } else {
-            mx = fmaxf(mx, fabsf(v));
-        }
-    }
-    float s = 0.F, inverse = 0.F;
-    int zp = 0;
-    if (MODE == 0) {
-        if (mx > 0.F) {
-            inverse = 127.F / mx;
-            s = mx / 127.F;
-        }
-    } else if (MODE == 1) {
-        const float rdiff = mx - mn;
-        inverse = rdiff > 0.F ? 255.F / rdiff : 0.F;
-        s = rdiff > 0.F ? rdiff / 255.F : 1.F;
-        const float min_error = -128.F + mn * inverse;
-        const float max_error = 127.F + mx * inverse;
-        const float fzp = min_error + max_error > 0.F ? -128.F - mn * inverse : 127.F - mx * inverse;
-        zp = rdiff > 0.F ? static_cast<int>(__builtin_rintf(clampf(fzp, -128.F, 127.F))) : -128;
-    } else {
-        s = a.input_scale;
-    }
+    for (int c = 0; c < a.group; ++c) quant_stat(MODE, load_act(a.x, a.x_type, base + c), mx, mn);
+    const QuantBlock p = quant_block(MODE, mx, mn, a.input_scale, true);
     int total = 0;
     for (int c = 0; c < a.group; ++c) {
-        const float v = load_act(a.x, a.x_type, base + c);
-        int code;
-        if (MODE == 0) {
-            code = mx > 0.F ? static_cast<int>(clampf(__builtin_rintf(v * inverse), -127.F, 127.F)) : 0;
-        } else if (MODE == 1) {
-            code = static_cast<int>(roundf(v * inverse)) + zp;
-            code = code < -128 ? -128 : (code > 127 ? 127 : code);
-        } else {
-            code = static_cast<int>(clampf(__builtin_rintf(v / a.input_scale), -128.F, 127.F));
-        }
+        const int code = quant_code(MODE, load_act(a.x, a.x_type, base + c), p, a.input_scale);
         a.q[base + c] = static_cast<std::int8_t>(code);
         total += code;
     }
-    a.scale[gid] = s;
+    a.scale[gid] = p.s;
     a.sum[gid] = total;
-    a.zero[gid] = zp;
+    a.zero[gid] = p.zp;
 }
-
-// ---------------------------------------------------------------------------------------------------------------
-// Shared pieces of the tiled projections.
-
-template <int BITS>
-struct TileShape {
-    static constexpr int KT = 512 / BITS;  // columns per tile
-    static constexpr int J = KT / 64;      // 64-column blocks per tile
-    static constexpr int CH = 2 * J;       // 32-column chunks per tile
-};
-
-// Codes of 64-column block j of a lane's 16-byte slot, as 4 dwords of int8 lanes in activation order.
-template <int BITS, int j>
-__device__ __forceinline__ void unpack_block(const uint4 w, int (&o)[4]) {
-    if constexpr (BITS == 8) {
-        o[0] = static_cast<int>(w.x);
-        o[1] = static_cast<int>(w.y);
-        o[2] = static_cast<int>(w.z);
-        o[3] = static_cast<int>(w.w);
-    } else if constexpr (BITS == 4) {
-        const std::uint32_t a = j == 0 ? w.x : w.z;
-        const std::uint32_t b = j == 0 ? w.y : w.w;
-        o[0] = static_cast<int>(a & 0x0F0F0F0Fu);
-        o[1] = static_cast<int>((a >> 4) & 0x0F0F0F0Fu);
-        o[2] = static_cast<int>(b & 0x0F0F0F0Fu);
-        o[3] = static_cast<int>((b >> 4) & 0x0F0F0F0Fu);
-    } else {
-        const std::uint32_t a = j == 0 ? w.x : (j == 1 ? w.y : (j == 2 ? w.z : w.w));
-        o[0] = static_cast<int>(a & 0x03030303u);
-        o[1] = static_cast<int>((a >> 2) & 0x03030303u);
-        o[2] = static_cast<int>((a >> 4) & 0x03030303u);
-        o[3] = static_cast<int>((a >> 6) & 0x03030303u);
-    }
-}
-
-struct LinearArgs {
-    const void* x;                // raw activations (portable path)
-    int x_type;
-    const std::uint8_t* tiles;
-    const void* scales;
-    const std::uint8_t* zero_points;
-    const void* zeros;
-    const std::int32_t* code_sums;
-    const std::int8_t* q;
-    const float* a_scale;
-    const std::int32_t* a_sum;
-    const std::int32_t* a_zero;
-    float* y;
-    std::int32_t* dump;
-    std::int64_t M, N, K, cols_p, k_tiles, n_tiles;
-    int group, groups_p, groups;  // groups = K / g (real)
-    int zero_mode, zero_half, is_static, gelu;
-    float input_scale, output_scale;
-    int units, tiles_per_unit;    // GEMV split of the K range across waves
-};
 
 // Integer partial of one finished group -> exact int32 partial P' and its fp32 contribution.
 //   2/4-bit:   P' = sum q*u - zp*Q  (u = c + 2^(b-1); zp = 2^(b-1) symmetric / additive zeros, zero point else)
@@ -312,10 +158,6 @@ __device__ __forceinline__ float group_term(const LinearArgs& a, std::int64_t me
     return a.is_static ? acc + t : acc + a.a_scale[ab] * t;
 }
 
-__device__ __forceinline__ float gelu_tanh(float g) {
-    const float inner = 0.7978845608028654F * (g + 0.044715F * g * g * g);
-    return 0.5F * g * (1.F + tanhf(inner));
-}
 
 // ---------------------------------------------------------------------------------------------------------------
 // Decode GEMV (M <= 8). Grid: one workgroup per 16-row tile (two with gelu gating: gate tile and its up tile);
@@ -945,39 +787,6 @@ int pow2_floor(int v) {
     return p;
 }
 
-LinearArgs make_args(const LinearCall& c) {
-    const Weight& w = *c.w;
-    LinearArgs a{};
-    a.x = c.x;
-    a.x_type = c.x_type;
-    a.tiles = w.tiles;
-    a.scales = w.scales;
-    a.zero_points = w.zero_points;
-    a.zeros = w.zeros;
-    a.code_sums = w.code_sums;
-    a.q = c.act.q;
-    a.a_scale = c.act.scale;
-    a.a_sum = c.act.sum;
-    a.a_zero = c.act.zero;
-    a.y = c.y;
-    a.dump = c.dump;
-    a.M = c.M;
-    a.N = w.geo.rows;
-    a.K = w.geo.cols;
-    a.cols_p = w.geo.cols_p;
-    a.k_tiles = w.geo.k_tiles;
-    a.n_tiles = w.geo.n_tiles;
-    a.group = w.geo.group;
-    a.groups_p = static_cast<int>(w.geo.groups_p);
-    a.groups = static_cast<int>(w.geo.cols / w.geo.group);
-    a.zero_mode = w.zero_mode;
-    a.zero_half = w.zero_type == META_F16;
-    a.is_static = c.path == PATH_SYMMETRIC;
-    a.gelu = c.gelu_gate;
-    a.input_scale = c.input_scale;
-    a.output_scale = c.output_scale;
-    return a;
-}
 
 template <int BITS, typename ST>
 hipError_t launch_gemv_bits(const LinearCall& c, LinearArgs a, hipStream_t stream) {
@@ -1009,7 +818,7 @@ hipError_t launch_gemv_bits(const LinearCall& c, LinearArgs a, hipStream_t strea
 
 template <int BITS, typename ST>
 hipError_t launch_tiled(const LinearCall& c, hipStream_t stream) {
-    LinearArgs a = make_args(c);
+    LinearArgs a = make_linear_args(c);
     if (c.M <= 8) return launch_gemv_bits<BITS, ST>(c, a, stream);
     const std::int64_t m_blocks = (c.M + GM - 1) / GM;
     const std::int64_t n_blocks = c.gelu_gate ? (c.w->geo.n_tiles / 2 + 3) / 4 : (c.w->geo.n_tiles + 7) / 8;
@@ -1019,7 +828,7 @@ hipError_t launch_tiled(const LinearCall& c, hipStream_t stream) {
 
 template <int BITS, typename ST>
 hipError_t launch_rowmajor(const LinearCall& c, hipStream_t stream) {
-    LinearArgs a = make_args(c);
+    LinearArgs a = make_linear_args(c);
     const std::int64_t total = c.M * c.w->geo.rows;
     hipLaunchKernelGGL((rowmajor_kernel<BITS, ST>), dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, a);
     return hipGetLastError();
@@ -1027,7 +836,7 @@ hipError_t launch_rowmajor(const LinearCall& c, hipStream_t stream) {
 
 template <int BITS, typename ST>
 hipError_t launch_portable(const LinearCall& c, hipStream_t stream) {
-    LinearArgs a = make_args(c);
+    LinearArgs a = make_linear_args(c);
     const std::int64_t total = c.M * c.w->geo.rows;
     hipLaunchKernelGGL((portable_kernel<BITS, ST>), dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, a,
                        c.w->tiled ? 1 : 0);
@@ -1118,5 +927,47 @@ hipError_t launch_copy_block_stats(const Weight& w, const ActBuffers& act, std::
                        act.sum, act.zero, M, groups, groups_p, scales, sums, zero_points);
     return hipGetLastError();
 }
+
+namespace dev {
+
+LinearArgs make_linear_args(const LinearCall& c) {
+    const Weight& w = *c.w;
+    LinearArgs a{};
+    a.x = c.x;
+    a.x_type = c.x_type;
+    a.tiles = w.tiles;
+    a.scales = w.scales;
+    a.zero_points = w.zero_points;
+    a.zeros = w.zeros;
+    a.code_sums = w.code_sums;
+    a.q = c.act.q;
+    a.a_scale = c.act.scale;
+    a.a_sum = c.act.sum;
+    a.a_zero = c.act.zero;
+    a.y = c.y;
+    a.dump = c.dump;
+    a.M = c.M;
+    a.N = w.geo.rows;
+    a.K = w.geo.cols;
+    a.cols_p = w.geo.cols_p;
+    a.k_tiles = w.geo.k_tiles;
+    a.n_tiles = w.geo.n_tiles;
+    a.group = w.geo.group;
+    a.groups_p = static_cast<int>(w.geo.groups_p);
+    a.groups = static_cast<int>(w.geo.cols / w.geo.group);
+    a.zero_mode = w.zero_mode;
+    a.zero_half = w.zero_type == META_F16;
+    a.is_static = c.path == PATH_SYMMETRIC;
+    a.gelu = c.gelu_gate;
+    a.input_scale = c.input_scale;
+    a.output_scale = c.output_scale;
+    a.dq_codes = c.dq_codes;
+    a.dq_scales = c.dq_scales;
+    a.dq_sums = c.dq_sums;
+    a.dq_zeros = c.dq_zeros;
+    return a;
+}
+
+}  // namespace dev
 
 }  // namespace kq

@@ -70,6 +70,14 @@ CASES = [
     (8, 32, 8, 512, 192, None, 0.0, False, 0.001),
     (8, 128, 3, 512, 64, None, 0.0, False, 0.0),
     (2, 32, 1, 512, 256, None, 0.05, False, 0.0),
+    # decode rows 9..16 (skinny kernel), groups spanning tiles, large groups (whole-wave quantizer)
+    (4, 128, 16, 512, 256, "zp", 0.0, True, 0.001),
+    (8, 32, 12, 256, 128, None, 0.0, False, 0.0),
+    (2, 32, 16, 512, 256, None, 0.05, False, 0.0),
+    (4, 256, 9, 1024, 256, None, 0.0, False, 0.0),
+    (4, 512, 2, 1024, 256, "zp", 0.0, True, 0.0),
+    (8, 192, 3, 384, 128, None, 0.0, False, 0.0),
+    (4, 128, 7, 512, 256, "f16", 0.0, True, 0.0),
     (2, 128, 6, 512, 128, None, 0.05, True, 0.0),
     (4, 32, 2, 256, 256, None, 0.05, False, 0.0),
     (8, 64, 1, 256, 128, None, 0.03, False, 0.0),
@@ -254,7 +262,7 @@ def test_zero_block_and_empty(dev, ref):
     assert tuple(empty.shape) == (0, 256)
 
 
-@pytest.mark.parametrize("M", [1, 4, 200])
+@pytest.mark.parametrize("M", [1, 4, 16, 200])
 def test_gelu_gate_fused(dev, ref, M):
     """gate/up projection + GELU-tanh in one pass equals the oracle's projection followed by gelu_gate."""
     rng = np.random.default_rng(M)
