@@ -372,6 +372,11 @@ kq_status run_call(kq::LinearCall& c, const kq_linear_args* args, std::size_t ws
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     if (dev != c.w->device) return fail(KQ_INVALID_ARGUMENT, "weight was packed on another device");
     // Decode (M <= 16): one fused launch, no workspace.
+    if (kq::decode_fits(c)) {
+        e = kq::launch_decode(c, stream);
+        if (e != hipSuccess) return hip_fail(e, "decode projection launch");
+        return KQ_OK;
+    }
     kq::SkinnyPlan plan;
     if (kq::skinny_plan(c, plan)) {
         e = kq::launch_skinny(c, plan, stream);
@@ -511,7 +516,8 @@ kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_d
     if (m == 0) return KQ_OK;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     kq::SkinnyPlan plan;
-    if (kq::skinny_plan(c, plan)) {
+    const bool fused = kq::decode_fits(c);
+    if (fused || kq::skinny_plan(c, plan)) {
         // the fused quantizer of the decode projection reports what it computed
         void* ybuf = nullptr;
         if (kq_status s = device_scratch(g_gelu_scratch, static_cast<std::size_t>(m * c.w->geo.rows) * 4, &ybuf); s != KQ_OK)
@@ -521,7 +527,7 @@ kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_d
         c.dq_scales = scales;
         c.dq_sums = sums;
         c.dq_zeros = zero_points;
-        const hipError_t e = kq::launch_skinny(c, plan, st);
+        const hipError_t e = fused ? kq::launch_decode(c, st) : kq::launch_skinny(c, plan, st);
         if (e != hipSuccess) return hip_fail(e, "debug quantize");
         return KQ_OK;
     }

@@ -1,0 +1,426 @@
+// Decode projection of the MI355X quantized linear layer for M <= 4 rows and K a multiple of 512: one launch per
+// call, activation quantization fused in, every shape parameter that the inner loop touches fixed at compile time.
+//
+// Grid: one workgroup per pair of row tiles (16 output rows each; with GELU gating a gate tile and its up tile,
+// Kidi's gate_up_proj row order, model/gemma4.cpp:308-316). Block: W = K/512 waves; wave w owns columns
+// [512 w, 512 w + 512) of both row tiles, i.e. NT = 512/KT weight tiles per row tile. A wave
+//   1. loads its activation pieces (8 columns per lane and row), the group metadata its epilogue lanes need, and
+//      its 2 x NT weight tiles (one 16-byte load per tile per lane), all up front into registers;
+//   2. quantizes its columns of the M rows into its LDS region (codes in the tiles' permuted order, per-group
+//      scale, code sum, zero point), with the arithmetic of kq_device.hpp;
+//   3. runs one v_mfma_i32_16x16x64_i8 per 64-column block and row tile. A row nn of the MFMA is activation row
+//      m = nn & 3 restricted to the groups whose index is nn >> 2 (mod 4), so the accumulator of lane (n, L)
+//      collects, in register i, the exact int32 partial of group slot L and row i; one epilogue per four groups
+//      folds them into fp32;
+//   4. sums its four group slots across lanes and hands 16 x M sums per row tile to the cross-wave reduction.
+//
+// Numerics: BlockwiseLinear / SymmetricPackedLinear closed forms (runtime/ynn/operators.cpp:1118-1169,
+// :1250-1308): P' = sum q*u - zw*Q (2/4-bit, u = c + 2^(b-1), zw = zero point or 2^(b-1)), P' = sum q*c - zp_a*C
+// (8-bit dynamic), t = s*P' (+ z*Q for additive float zeros), acc += a_s*t (dynamic) or t (calibrated).
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "kq_device.hpp"
+#include "kq_internal.hpp"
+
+namespace kq {
+namespace {
+
+using namespace dev;
+
+constexpr std::uint32_t kOob = 0x80000000u;  // buffer offset past every resource: the load returns zeros
+constexpr int kRsrcWord3 = 0x00020000;       // raw (unformatted) buffer resource, gfx9-family word 3
+constexpr int kMaxRows = 4;
+
+struct DecodeArgs {
+    const void* x;  // activations [M][K]
+    const std::uint8_t* tiles;
+    const void* scales;  // [n_tiles][groups_p][16] F16|F32
+    const void* aux;     // zero points [n_tiles][groups_p][8 B] | code sums [..][16] I32 | float zeros [..][16] F16|F32
+    float* y;
+    std::int32_t* dump;  // optional int32 partials [M][N][K/g]
+    std::int8_t* dq_codes;
+    float* dq_scales;
+    std::int32_t* dq_sums;
+    std::int32_t* dq_zeros;
+    int M, K, N, k_tiles, n_tiles, groups_p, groups;
+    int x_f32, scale_half, aux_half;
+    float input_scale, output_scale;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, std::uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kRsrcWord3);
+}
+__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, std::uint32_t off) {
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+
+// Max / min / sum over aligned blocks of 2^LG lanes (LG <= 4: inside one 16-lane row, all DPP).
+template <int LG, typename Op>
+__device__ __forceinline__ int row_reduce(int v, Op op) {
+    if (LG >= 1) v = op(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]
+    if (LG >= 2) v = op(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]
+    if (LG >= 3) v = op(v, dpp<0x141>(v));  // row_half_mirror
+    if (LG >= 4) v = op(v, dpp<0x140>(v));  // row_mirror
+    return v;
+}
+
+// Codes of 64-column block j of a 16-byte weight slot as 16 int8 in activation order (see kq_layout.hpp).
+template <int BITS, int j>
+__device__ __forceinline__ v4i block_codes(const uint4 w) {
+    int o[4];
+    unpack_block<BITS, j>(w, o);
+    return v4i{o[0], o[1], o[2], o[3]};
+}
+
+template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG>
+__global__ __launch_bounds__(1024) void decode_kernel(DecodeArgs a) {
+    constexpr int KT = 512 / BITS;       // columns per weight tile
+    constexpr int J = KT / 64;           // 64-column blocks per tile
+    constexpr int NT = 512 / KT;         // tiles per wave and row tile
+    constexpr int NG = 512 / G;          // groups per wave
+    constexpr int NQ = NG / 4;           // quads of groups per wave
+    constexpr int LGC = G == 32 ? 2 : (G == 64 ? 3 : 4);  // log2 of 8-column pieces per group
+    constexpr int WAVE_BYTES = kMaxRows * 512 + 3 * 4 * kMaxRows * NG + 16;
+    static_assert(G == 32 || G == 64 || G == 128, "group size");
+    extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int W = blockDim.x >> 6;
+    const int nn = lane & 15, L = lane >> 4;
+    const int M = a.M;
+    const int am = nn & 3, aslot = nn >> 2;  // A-operand row of this lane: activation row, group slot
+
+    int nts[2];
+    if constexpr (GELU) {
+        nts[0] = blockIdx.x;
+        nts[1] = blockIdx.x + (a.n_tiles >> 1);
+    } else {
+        nts[0] = 2 * blockIdx.x;
+        nts[1] = 2 * blockIdx.x + 1;
+    }
+    const bool live1 = nts[1] < a.n_tiles;
+    const int nt1 = live1 ? nts[1] : nts[0];
+
+    std::uint8_t* wl = lds + wave * WAVE_BYTES;
+    std::int8_t* codes = reinterpret_cast<std::int8_t*>(wl);                     // [M][512]
+    float* st_s = reinterpret_cast<float*>(wl + kMaxRows * 512);                  // [M][NG]
+    int* st_q = reinterpret_cast<int*>(st_s + kMaxRows * NG);
+    int* st_z = st_q + kMaxRows * NG;
+    const int zero_slot = WAVE_BYTES - 16;
+    if (lane == 0) *reinterpret_cast<uint4*>(wl + zero_slot) = make_uint4(0, 0, 0, 0);
+
+    // ---- 1. loads: activations, metadata, weights (in this order) ----
+    const __amdgpu_buffer_rsrc_t xres = rsrc(a.x, static_cast<std::uint32_t>(M * a.K * (a.x_f32 ? 4 : 2)));
+    const int kb = wave * 512;  // first column of this wave
+    uint4 xr[kMaxRows][2];
+#pragma unroll
+    for (int m = 0; m < kMaxRows; ++m) {
+        if (m < M) {
+            const std::uint32_t e = static_cast<std::uint32_t>(m * a.K + kb + 8 * lane);
+            const std::uint32_t off = a.x_f32 ? 4 * e : 2 * e;
+            xr[m][0] = ld16(xres, off);
+            xr[m][1] = ld16(xres, a.x_f32 ? off + 16 : off);
+        }
+    }
+    // metadata entry of quad q for this lane: group 4q + L of the wave, row nn
+    const std::uint32_t meta_n = static_cast<std::uint32_t>(a.n_tiles * a.groups_p * kTileRows);
+    const __amdgpu_buffer_rsrc_t sres = rsrc(a.scales, meta_n * (a.scale_half ? 2 : 4));
+    std::uint32_t s_raw[2][NQ], x_raw[2][NQ];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int nt = r == 0 ? nts[0] : nt1;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const std::uint32_t mi = static_cast<std::uint32_t>((nt * a.groups_p + wave * NG + 4 * q + L) * kTileRows + nn);
+            s_raw[r][q] = a.scale_half ? __builtin_amdgcn_raw_buffer_load_b16(sres, 2 * mi, 0, 0)
+                                       : __builtin_amdgcn_raw_buffer_load_b32(sres, 4 * mi, 0, 0);
+            x_raw[r][q] = 0;
+            if constexpr (BITS == 8 && QM == QUANT_DYN_ASYM)
+                x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b32(rsrc(a.aux, meta_n * 4), 4 * mi, 0, 0);
+            if constexpr (BITS != 8 && ZM == ZERO_POINT)
+                x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b8(rsrc(a.aux, meta_n / 2), (mi - nn) / 2 + nn / 2, 0, 0);
+            if constexpr (BITS != 8 && ZM == ZERO_FLOAT)
+                x_raw[r][q] = a.aux_half ? __builtin_amdgcn_raw_buffer_load_b16(rsrc(a.aux, meta_n * 2), 2 * mi, 0, 0)
+                                         : __builtin_amdgcn_raw_buffer_load_b32(rsrc(a.aux, meta_n * 4), 4 * mi, 0, 0);
+        }
+    }
+    const __amdgpu_buffer_rsrc_t w0 = rsrc(a.tiles + static_cast<std::int64_t>(nts[0]) * a.k_tiles * kTileBytes,
+                                           static_cast<std::uint32_t>(a.k_tiles * kTileBytes));
+    const __amdgpu_buffer_rsrc_t w1 = rsrc(a.tiles + static_cast<std::int64_t>(nt1) * a.k_tiles * kTileBytes,
+                                           static_cast<std::uint32_t>(a.k_tiles * kTileBytes));
+    uint4 wv[2][NT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+        const std::uint32_t off = static_cast<std::uint32_t>((wave * NT + u) * kTileBytes + 16 * lane);
+        wv[0][u] = ld16(w0, off);
+        wv[1][u] = ld16(w1, off);
+    }
+
+    // ---- 2. quantize this wave's 512 columns of each row: lane = 8-column piece, 2^LGC lanes = one group ----
+    const bool dump_block = DBG && blockIdx.x == 0;
+#pragma unroll
+    for (int m = 0; m < kMaxRows; ++m) {
+        if (m < M) {
+            float v[8];
+            if (a.x_f32) {
+                const std::uint32_t w8[8] = {xr[m][0].x, xr[m][0].y, xr[m][0].z, xr[m][0].w,
+                                             xr[m][1].x, xr[m][1].y, xr[m][1].z, xr[m][1].w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w8[i]);
+            } else {
+                const std::uint32_t w4[4] = {xr[m][0].x, xr[m][0].y, xr[m][0].z, xr[m][0].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[2 * i] = __uint_as_float(w4[i] << 16);
+                    v[2 * i + 1] = __uint_as_float(w4[i] & 0xFFFF0000u);
+                }
+            }
+            float mx = 0.F, mn = 0.F;
+            if constexpr (QM != QUANT_STATIC) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) quant_stat(QM, v[i], mx, mn);
+                mx = __int_as_float(row_reduce<LGC>(__float_as_int(mx), [](int p, int q) { return __float_as_int(fmaxf(__int_as_float(p), __int_as_float(q))); }));
+                if constexpr (QM == QUANT_DYN_ASYM)
+                    mn = __int_as_float(row_reduce<LGC>(__float_as_int(mn), [](int p, int q) { return __float_as_int(fminf(__int_as_float(p), __int_as_float(q))); }));
+            }
+            const QuantBlock qb = quant_block(QM, mx, mn, a.input_scale, true);
+            std::uint32_t lo = 0, hi = 0;
+            int total = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int c = quant_code(QM, v[i], qb, a.input_scale);
+                total += c;
+                if (i < 4) lo |= (static_cast<std::uint32_t>(c) & 0xFFu) << (8 * i);
+                else hi |= (static_cast<std::uint32_t>(c) & 0xFFu) << (8 * (i - 4));
+            }
+            *reinterpret_cast<uint2*>(codes + m * 512 + act_position(8 * lane)) = make_uint2(lo, hi);
+            total = row_reduce<LGC>(total, [](int p, int q) { return p + q; });
+            if ((lane & ((1 << LGC) - 1)) == 0) {
+                const int sl = m * NG + (lane >> LGC);
+                st_s[sl] = qb.s;
+                st_q[sl] = total;
+                st_z[sl] = qb.zp;
+                if (dump_block) {
+                    const int o = m * a.groups + wave * NG + (lane >> LGC);
+                    if (a.dq_scales) a.dq_scales[o] = qb.s;
+                    if (a.dq_sums) a.dq_sums[o] = total;
+                    if (a.dq_zeros) a.dq_zeros[o] = qb.zp;
+                }
+            }
+            if (dump_block && a.dq_codes) *reinterpret_cast<uint2*>(a.dq_codes + m * a.K + kb + 8 * lane) = make_uint2(lo, hi);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- 3. MFMA over the wave's blocks, one epilogue per quad of groups ----
+    float acc[2][4];
+    v4i C[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        C[r] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][i] = 0.F;
+    }
+    const int abase = am * 512 + 16 * L;
+    const bool arow = am < M;
+
+    auto flush = [&](int q) {
+        const int gi = 4 * q + L;  // this lane's group (of the wave) and the stats slot of row i
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const float s = a.scale_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(s_raw[r][q]))) : __uint_as_float(s_raw[r][q]);
+            int x2 = 0;
+            if constexpr (BITS == 8 && QM == QUANT_DYN_ASYM) x2 = static_cast<int>(x_raw[r][q]);
+            if constexpr (BITS != 8 && ZM == ZERO_POINT) x2 = static_cast<int>((x_raw[r][q] >> (4 * (nn & 1))) & 15u);
+            if constexpr (BITS != 8 && ZM == ZERO_FLOAT)
+                x2 = __float_as_int(a.aux_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(x_raw[r][q]))) : __uint_as_float(x_raw[r][q]));
+            const int n = (r == 0 ? nts[0] : nts[1]) * kTileRows + nn;
+#pragma unroll
+            for (int i = 0; i < kMaxRows; ++i) {
+                if (i < M) {
+                    const int sl = i * NG + gi;
+                    int Pp;
+                    if constexpr (BITS == 8) {
+                        Pp = QM == QUANT_STATIC ? C[r][i] : C[r][i] - st_z[sl] * x2;
+                    } else {
+                        const int zw = ZM == ZERO_POINT ? x2 : sign_offset(BITS);
+                        Pp = C[r][i] - zw * st_q[sl];
+                    }
+                    if (DBG && a.dump && n < a.N && (r == 0 || live1))
+                        a.dump[(static_cast<std::int64_t>(i) * a.N + n) * a.groups + wave * NG + gi] = Pp;
+                    float t = s * static_cast<float>(Pp);
+                    if constexpr (BITS != 8 && ZM == ZERO_FLOAT) t = t + __int_as_float(x2) * static_cast<float>(st_q[sl]);
+                    acc[r][i] = QM == QUANT_STATIC ? acc[r][i] + t : acc[r][i] + st_s[sl] * t;
+                }
+            }
+            C[r] = v4i{0, 0, 0, 0};
+        }
+    };
+
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            constexpr int dummy = 0;
+            (void)dummy;
+            const int c = u * KT + 64 * j;  // wave-local first column of the block
+            v4i A;
+            if constexpr (G == 32) {
+                // two groups per block: bytes 0-7 of a lane's 16 belong to group c/32, bytes 8-15 to c/32 + 1
+                const int s0 = (c >> 5) & 3, s1 = ((c >> 5) + 1) & 3;
+                const int o0 = (arow && aslot == s0) ? abase + act_position(c) : zero_slot;
+                const int o1 = (arow && aslot == s1) ? abase + act_position(c) + 8 : zero_slot;
+                const uint2 lo = *reinterpret_cast<const uint2*>(wl + o0);
+                const uint2 hi = *reinterpret_cast<const uint2*>(wl + o1);
+                A = v4i{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(hi.x), static_cast<int>(hi.y)};
+            } else {
+                const int sg = (c / G) & 3;
+                A = *reinterpret_cast<const v4i*>(wl + ((arow && aslot == sg) ? abase + act_position(c) : zero_slot));
+            }
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                v4i B;
+                if (j == 0) B = block_codes<BITS, 0>(wv[r][u]);
+                else if (j == 1) B = block_codes<BITS, (J > 1 ? 1 : 0)>(wv[r][u]);
+                else if (j == 2) B = block_codes<BITS, (J > 2 ? 2 : 0)>(wv[r][u]);
+                else B = block_codes<BITS, (J > 3 ? 3 : 0)>(wv[r][u]);
+                C[r] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, C[r], 0, 0, 0);
+            }
+            if (((c + 64) % (4 * G)) == 0) flush((c + 64) / (4 * G) - 1);
+        }
+    }
+
+    // ---- 4. sum the four group slots (lanes nn + 16 L) and the waves ----
+    float* red = reinterpret_cast<float*>(lds + W * WAVE_BYTES);  // [W][2][M][16]
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+#pragma unroll
+        for (int i = 0; i < kMaxRows; ++i) {
+            if (i < M) {
+                float v = acc[r][i];
+                v = v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));  // xor 16
+                v = v + __shfl_xor(v, 32);
+                if (L == 0) red[((wave * 2 + r) * kMaxRows + i) * 16 + nn] = v;
+            }
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < (GELU ? 1 : 2) * M * 16; idx += blockDim.x) {
+        const int r = idx / (M * 16), i = (idx / 16) % M, c = idx % 16;
+        float v[2] = {0.F, 0.F};
+#pragma unroll
+        for (int h = 0; h < (GELU ? 2 : 1); ++h) {
+            const int rr = GELU ? h : r;
+            for (int w = 0; w < W; ++w) v[h] = v[h] + red[((w * 2 + rr) * kMaxRows + i) * 16 + c];
+            if (QM == QUANT_STATIC) v[h] = v[h] * a.input_scale;
+            v[h] = calibrate_output(v[h], a.output_scale);
+        }
+        if constexpr (GELU) {
+            const int half_n = a.N >> 1;
+            const int n = nts[0] * kTileRows + c;
+            if (n < half_n) a.y[static_cast<std::int64_t>(i) * half_n + n] = gelu_tanh(v[0]) * v[1];
+        } else {
+            const int nt = nts[r];
+            const int n = nt * kTileRows + c;
+            if (nt < a.n_tiles && n < a.N) a.y[static_cast<std::int64_t>(i) * a.N + n] = v[0];
+        }
+    }
+}
+
+template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG>
+hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds, hipStream_t stream) {
+    hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG>), grid, block, lds, stream, a);
+    return hipGetLastError();
+}
+
+template <int BITS, int ZM, int QM>
+hipError_t launch_modes(const DecodeArgs& a, int g, bool gelu, bool dbg, dim3 grid, dim3 block, std::size_t lds, hipStream_t stream) {
+#define KQ_DEC(G)                                                                                       \
+    do {                                                                                                \
+        if (gelu) return launch_g<BITS, G, true, ZM, QM, false>(a, grid, block, lds, stream);           \
+        if (dbg) return launch_g<BITS, G, false, ZM, QM, true>(a, grid, block, lds, stream);            \
+        return launch_g<BITS, G, false, ZM, QM, false>(a, grid, block, lds, stream);                    \
+    } while (0)
+    if (g == 32) KQ_DEC(32);
+    if (g == 64) KQ_DEC(64);
+    KQ_DEC(128);
+#undef KQ_DEC
+}
+
+int wave_bytes(int g) { return kMaxRows * 512 + 3 * 4 * kMaxRows * (512 / g) + 16; }
+
+}  // namespace
+
+bool decode_fits(const LinearCall& c) {
+    const Weight& w = *c.w;
+    if (!w.tiled || c.path == PATH_PORTABLE || c.M < 1 || c.M > kMaxRows) return false;
+    const int bits = w.geo.bits, g = w.geo.group;
+    if (g != 32 && g != 64 && g != 128) return false;
+    if (w.geo.cols % 512 || w.geo.cols / 512 > 16) return false;
+    if (bits == 2 && c.path != PATH_SYMMETRIC) return false;  // dynamic 2-bit is Kidi's portable path
+    if (c.gelu_gate && ((w.geo.rows / 2) % kTileRows || w.geo.n_tiles % 2)) return false;
+    if (w.geo.k_tiles * kTileBytes >= (std::int64_t{1} << 31) || w.geo.meta_count() * 4 >= (std::int64_t{1} << 31) ||
+        c.M * w.geo.cols * 4 >= (std::int64_t{1} << 31) || w.geo.n_tiles * w.geo.k_tiles * kTileBytes >= (std::int64_t{1} << 46))
+        return false;
+    return true;
+}
+
+hipError_t launch_decode(const LinearCall& c, hipStream_t stream) {
+    const Weight& w = *c.w;
+    DecodeArgs a{};
+    a.x = c.x;
+    a.tiles = w.tiles;
+    a.scales = w.scales;
+    a.aux = w.geo.bits == 8 ? static_cast<const void*>(w.code_sums)
+                            : (w.zero_mode == ZERO_POINT ? static_cast<const void*>(w.zero_points) : w.zeros);
+    a.y = c.y;
+    a.dump = c.dump;
+    a.dq_codes = c.dq_codes;
+    a.dq_scales = c.dq_scales;
+    a.dq_sums = c.dq_sums;
+    a.dq_zeros = c.dq_zeros;
+    a.M = static_cast<int>(c.M);
+    a.K = static_cast<int>(w.geo.cols);
+    a.N = static_cast<int>(w.geo.rows);
+    a.k_tiles = static_cast<int>(w.geo.k_tiles);
+    a.n_tiles = static_cast<int>(w.geo.n_tiles);
+    a.groups_p = static_cast<int>(w.geo.groups_p);
+    a.groups = static_cast<int>(w.geo.cols / w.geo.group);
+    a.x_f32 = c.x_type == ACT_F32;
+    a.scale_half = w.scale_type == META_F16;
+    a.aux_half = w.zero_type == META_F16;
+    a.input_scale = c.input_scale;
+    a.output_scale = c.output_scale;
+    const int W = static_cast<int>(w.geo.cols / 512);
+    const int blocks = static_cast<int>(c.gelu_gate ? w.geo.n_tiles / 2 : (w.geo.n_tiles + 1) / 2);
+    const dim3 grid(static_cast<unsigned>(blocks)), block(64 * W);
+    const std::size_t lds = static_cast<std::size_t>(W * wave_bytes(w.geo.group) + W * 2 * kMaxRows * 16 * 4);
+    const bool dbg = c.dump || c.dq_codes || c.dq_scales || c.dq_sums || c.dq_zeros;
+    const bool stat = c.path == PATH_SYMMETRIC;
+    const int g = w.geo.group;
+    switch (w.geo.bits) {
+    case 2: return launch_modes<2, ZERO_NONE, dev::QUANT_STATIC>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
+    case 4:
+        if (stat) return launch_modes<4, ZERO_NONE, dev::QUANT_STATIC>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
+        if (w.zero_mode == ZERO_POINT) return launch_modes<4, ZERO_POINT, dev::QUANT_DYN_SYM>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
+        if (w.zero_mode == ZERO_FLOAT) return launch_modes<4, ZERO_FLOAT, dev::QUANT_DYN_SYM>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
+        return launch_modes<4, ZERO_NONE, dev::QUANT_DYN_SYM>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
+    default:
+        if (stat) return launch_modes<8, ZERO_NONE, dev::QUANT_STATIC>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
+        return launch_modes<8, ZERO_NONE, dev::QUANT_DYN_ASYM>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
+    }
+}
+
+}  // namespace kq

@@ -45,7 +45,8 @@ __device__ __forceinline__ void load_act4(const void* x, int type, std::int64_t 
     }
 }
 
-__device__ __forceinline__ float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
+// min(max(v, lo), hi) for finite or infinite v in one v_med3_f32 (activations are finite by contract).
+__device__ __forceinline__ float clampf(float v, float lo, float hi) { return __builtin_amdgcn_fmed3f(v, lo, hi); }
 
 // Static output rounding (eager_test.cpp:100-102): clamp(rint(y / out), -128, 127) * out when out > 0.
 __device__ __forceinline__ float calibrate_output(float v, float out) {
@@ -208,6 +209,8 @@ struct LinearArgs {
     int chunk_tiles;              // tiles quantized and staged per chunk (a multiple of the tiles per group)
     int wave_lds;                 // LDS bytes per wave
     int off_stats, off_meta;      // byte offsets inside a wave's LDS region
+    int off_x2, off_w;            // ... of the second metadata words and of the staged weight tiles
+    int scale_block, x2_block;    // LDS bytes per row tile of a chunk's raw scales / second words
     int red_off;                  // byte offset of the cross-wave reduction buffer
     int lg_group, lg_chunk_cols, lg_waves, lg_tiles_per_unit;  // log2 of g, of the chunk's columns, of W, of tiles/group
     std::int8_t* dq_codes;        // optional dumps of the fused quantizer (natural order [M][K], [M][K/g])

@@ -64,11 +64,16 @@ struct LinearCall {
 struct SkinnyPlan {
     int R = 1, W = 1, T = 4;
     int chunk_tiles = 1;
-    int wave_lds = 0, off_stats = 0, off_meta = 0, red_off = 0, lds_bytes = 0;
+    int wave_lds = 0, off_stats = 0, off_meta = 0, off_x2 = 0, off_w = 0, red_off = 0, lds_bytes = 0;
+    int scale_block = 0, x2_block = 0;  // LDS bytes per row tile of a chunk's raw scales and second words
     std::int64_t blocks = 0;
 };
 
 bool skinny_plan(const LinearCall& c, SkinnyPlan& p);
+
+// Decode projection for M <= 4 and K a multiple of 512 with g in {32, 64, 128} (kq_decode.hip).
+bool decode_fits(const LinearCall& c);
+hipError_t launch_decode(const LinearCall& c, hipStream_t stream);
 hipError_t launch_skinny(const LinearCall& c, const SkinnyPlan& p, hipStream_t stream);
 
 std::size_t workspace_bytes(const Weight& w, std::int64_t M);

@@ -78,6 +78,15 @@ CASES = [
     (4, 512, 2, 1024, 256, "zp", 0.0, True, 0.0),
     (8, 192, 3, 384, 128, None, 0.0, False, 0.0),
     (4, 128, 7, 512, 256, "f16", 0.0, True, 0.0),
+    # decode kernel (M <= 4, K a multiple of 512, g in {32, 64, 128})
+    (8, 32, 2, 1024, 192, None, 0.0, True, 0.001),
+    (8, 128, 3, 512, 128, None, 0.03, False, 0.0),
+    (8, 64, 4, 1536, 64, None, 0.0, False, 0.0),
+    (4, 32, 4, 2048, 256, None, 0.0, False, 0.0),
+    (4, 64, 1, 1024, 288, "zp", 0.0, True, 0.001),
+    (4, 128, 1, 512, 256, "f16", 0.0, False, 0.0),
+    (2, 64, 3, 1024, 128, None, 0.05, True, 0.0),
+    (2, 128, 1, 512, 48, None, 0.05, False, 0.0),
     (2, 128, 6, 512, 128, None, 0.05, True, 0.0),
     (4, 32, 2, 256, 256, None, 0.05, False, 0.0),
     (8, 64, 1, 256, 128, None, 0.03, False, 0.0),
