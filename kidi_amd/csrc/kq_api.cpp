@@ -79,7 +79,7 @@ std::int64_t act_rows(const kq::Weight& w, std::int64_t M) {
     if (!w.tiled) return M;
     if (M <= 4) return M;
     if (M <= 8) return 8;
-    return kq::round_up(M, 128);
+    return kq::round_up(M, 256);
 }
 
 constexpr std::size_t kAlign = 256;
@@ -392,6 +392,12 @@ kq_status run_call(kq::LinearCall& c, const kq_linear_args* args, std::size_t ws
         }
         c.act = kq::carve_workspace(*c.w, c.M, ws);
     }
+    // Prefill, 4-bit g = 128: quantizer + int8 MFMA GEMM (GELU gate fused).
+    if (kq::gemm_i4_fits(c)) {
+        e = kq::launch_gemm_i4(c, c.act, stream);
+        if (e != hipSuccess) return hip_fail(e, "prefill projection launch");
+        return KQ_OK;
+    }
     // GELU gating is fused into the tiled GEMV/GEMM when the gate and up halves are whole tiles; otherwise the
     // full projection goes to a scratch buffer and a gating kernel follows.
     const bool fused_gelu = c.gelu_gate && c.path != kq::PATH_PORTABLE && c.w->tiled && (c.w->geo.rows / 2) % kq::kTileRows == 0;
@@ -534,6 +540,11 @@ kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_d
     void* ws = nullptr;
     if (kq_status s = device_scratch(g_scratch, ws_bytes, &ws); s != KQ_OK) return s;
     c.act = kq::carve_workspace(*c.w, m, ws);
+    if (kq::gemm_i4_fits(c)) {
+        const hipError_t e = kq::launch_gemm_i4_quantize_dump(c, c.act, codes, scales, sums, zero_points, st);
+        if (e != hipSuccess) return hip_fail(e, "debug quantize");
+        return KQ_OK;
+    }
     hipError_t e = kq::launch_quantize(c, st);
     if (e == hipSuccess && codes) e = kq::launch_unpermute_codes(*c.w, c.act, m, codes, st);
     if (e == hipSuccess) e = kq::launch_copy_block_stats(*c.w, c.act, m, scales, sums, zero_points, st);

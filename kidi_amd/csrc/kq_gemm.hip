@@ -1,0 +1,498 @@
+// Prefill projection (M > 16) of the MI355X quantized linear layer for 4-bit weights with g = 128 (symmetric or
+// with zero points) and K a multiple of 512: an activation quantizer and an int8 MFMA GEMM.
+//
+// quantize_rows_kernel: one wave per (row, 512 columns); lane = 8-column piece, the g/8 lanes of a group reduce
+//   max |x| and the code sum with DPP; codes go to [M_p][K] in the tiles' permuted order, block scales to
+//   [groups][M_p] (transposed so a GEMM stage copies one contiguous 1 KiB row of them).
+// gemm_i4_kernel: workgroup tile 256 (rows) x 128 (output columns = 8 weight row tiles), 8 waves of 64 x 64, one
+//   128-column k-step (= one 4-bit tile = one group) per iteration, double-buffered:
+//     - activation codes: 32 direct-to-LDS copies of 1 KiB per step (buffer_load ... lds), lane addresses XOR-
+//       swizzled by row so A-operand reads spread over the LDS banks;
+//     - weights: each thread loads one 16-byte packed slot (one per tile lane) a step ahead, unpacks it to int8
+//       with the zero point folded in (u - zp per byte, SWAR), and stores both 64-column halves in B-operand order;
+//     - MFMA: per 64-column half 4 A and 4 B reads, 16 v_mfma_i32_16x16x64_i8; the int32 accumulators hold the
+//       exact per-group partials P' = sum q (u - zp);
+//     - epilogue per group: acc += a_s[row] * s[col] * P' (calibrated: s * P', input_scale applied at the end).
+// Numerics: BlockwiseLinear / SymmetricPackedLinear closed forms (runtime/ynn/operators.cpp:1118-1169,
+// :1250-1308) with the zero point folded into the integer operand: w = (u - zp) * s = c * s + (8 - zp) * s.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "kq_device.hpp"
+#include "kq_internal.hpp"
+
+namespace kq {
+namespace {
+
+using namespace dev;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kBM = 256, kBN = 128, kBK = 128;  // rows, output columns (8 row tiles), columns per step
+constexpr int kWaves = 8;                       // 4 (rows) x 2 (columns), 64 x 64 per wave
+constexpr int kABytes = kBM * kBK;              // activation codes per stage
+constexpr int kBBytes = 8 * 2 * 1024;           // unpacked weights per stage: [tile][half][lane][16 B]
+constexpr int kSBytes = kBM * 4;                // activation scales per stage
+constexpr int kLds = 2 * (kABytes + kBBytes + kSBytes);
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr std::uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, std::uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kRsrcWord3);
+}
+__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, std::uint32_t off) {
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ int row16_max(int v) {  // max over 16-lane rows (float bits)
+    auto mx = [](int p, int q) { return __float_as_int(fmaxf(__int_as_float(p), __int_as_float(q))); };
+    v = mx(v, dpp<0xB1>(v));
+    v = mx(v, dpp<0x4E>(v));
+    v = mx(v, dpp<0x141>(v));
+    return mx(v, dpp<0x140>(v));
+}
+__device__ __forceinline__ int row16_sum(int v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    return v + dpp<0x140>(v);
+}
+
+struct QRowArgs {
+    const void* x;
+    int x_f32;
+    int M, M_p, K;
+    float input_scale;
+    std::int8_t* q;      // [M_p][K] permuted
+    float* scale_t;      // [K/128][M_p]
+    std::int32_t* sum_t; // [K/128][M_p] (optional)
+};
+
+// g = 128: a group is one 16-lane row of the wave.
+template <int QM>
+__global__ __launch_bounds__(256) void quantize_rows_kernel(QRowArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wid = static_cast<int>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int chunks = a.K / 512;
+    const int m = wid / chunks, c = wid % chunks;
+    if (m >= a.M_p) return;
+    const bool live = m < a.M;
+    const __amdgpu_buffer_rsrc_t xr = rsrc(a.x, static_cast<std::uint32_t>(a.M) * a.K * (a.x_f32 ? 4 : 2));
+    const std::uint32_t e = static_cast<std::uint32_t>(m) * a.K + c * 512 + 8 * lane;
+    const std::uint32_t off = live ? (a.x_f32 ? 4 * e : 2 * e) : kOob;
+    const uint4 r0 = ld16(xr, off);
+    const uint4 r1 = ld16(xr, a.x_f32 ? off + 16 : off);
+    float v[8];
+    if (a.x_f32) {
+        const std::uint32_t w8[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w8[i]);
+    } else {
+        const std::uint32_t w4[4] = {r0.x, r0.y, r0.z, r0.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w4[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w4[i] & 0xFFFF0000u);
+        }
+    }
+    float mx = 0.F, mn = 0.F;
+    if constexpr (QM != QUANT_STATIC) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) quant_stat(QM, v[i], mx, mn);
+        mx = __int_as_float(row16_max(__float_as_int(mx)));
+    }
+    const QuantBlock qb = quant_block(QM, mx, mn, a.input_scale, live);
+    std::uint32_t lo = 0, hi = 0;
+    int total = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int code = quant_code(QM, v[i], qb, a.input_scale);
+        total += code;
+        if (i < 4) lo |= (static_cast<std::uint32_t>(code) & 0xFFu) << (8 * i);
+        else hi |= (static_cast<std::uint32_t>(code) & 0xFFu) << (8 * (i - 4));
+    }
+    *reinterpret_cast<uint2*>(a.q + static_cast<std::int64_t>(m) * a.K + c * 512 + act_position(8 * lane)) = make_uint2(lo, hi);
+    total = row16_sum(total);
+    if ((lane & 15) == 0) {
+        const std::int64_t o = static_cast<std::int64_t>(c * 4 + (lane >> 4)) * a.M_p + m;
+        a.scale_t[o] = qb.s;
+        if (a.sum_t) a.sum_t[o] = total;
+    }
+}
+
+struct GemmArgs {
+    const std::int8_t* q;       // [M_p][K]
+    const float* scale_t;       // [K/128][M_p]
+    const std::uint8_t* tiles;
+    const void* scales;         // [n_tiles][groups_p][16] F16|F32
+    const std::uint8_t* zero_points;  // [n_tiles][groups_p][8], or null (symmetric: zero point 8)
+    float* y;
+    std::int32_t* dump;
+    int M, M_p, N, K, k_tiles, n_tiles, groups_p, groups;
+    int scale_half;
+    float input_scale, output_scale;
+    int m_blocks, n_blocks;
+};
+
+// Global row tile of LDS tile slot t (0..7) of column block nb, or n_tiles when out of range. GELU: slots 0-3 are
+// gate tiles 4 nb + t, slots 4-7 the matching up tiles (gate rows [0, I), up rows [I, 2I)).
+template <bool GELU>
+__device__ __forceinline__ int slot_tile(const GemmArgs& a, int nb, int t) {
+    if constexpr (GELU) {
+        const int half = a.n_tiles >> 1;
+        const int g = nb * 4 + (t & 3);
+        return g < half ? (t < 4 ? g : half + g) : a.n_tiles;
+    }
+    const int nt = nb * 8 + t;
+    return nt < a.n_tiles ? nt : a.n_tiles;
+}
+// LDS tile slot of wave column wn, subtile ni: plain 4 wn + ni; GELU 2 wn + ni (gate) / 4 + 2 wn + ni - 2 (up).
+template <bool GELU>
+__device__ __forceinline__ constexpr int wave_slot(int wn, int ni) {
+    return GELU ? (ni < 2 ? 2 * wn + ni : 4 + 2 * wn + ni - 2) : 4 * wn + ni;
+}
+
+template <bool GELU, int QM, bool ZP, bool DBG>
+__global__ __launch_bounds__(512) void gemm_i4_kernel(GemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 3, wn = wave >> 2;
+    const int nn = lane & 15, L = lane >> 4;
+
+    // workgroup -> (row block, column block): consecutive workgroups go to different XCDs, so give each XCD a
+    // contiguous range (8 column blocks x all row blocks share its L2)
+    const int total = a.m_blocks * a.n_blocks;
+    int bid = blockIdx.x;
+    if (total % 8 == 0) bid = (bid % 8) * (total / 8) + bid / 8;
+    const int mb = bid % a.m_blocks, nb = bid / a.m_blocks;
+    const int m0 = mb * kBM;
+
+    // activation panel of this workgroup: rows [m0, m0 + 256) x K
+    const __amdgpu_buffer_rsrc_t ares = rsrc(a.q + static_cast<std::int64_t>(m0) * a.K, static_cast<std::uint32_t>(kBM) * a.K);
+    const __amdgpu_buffer_rsrc_t sres = rsrc(a.scale_t, static_cast<std::uint32_t>(a.groups_p) * a.M_p * 4);
+
+    // weight staging: thread -> (tile slot, lane of that tile)
+    const int st = tid >> 6;
+    const int my_nt = slot_tile<GELU>(a, nb, st);
+    const bool my_live = my_nt < a.n_tiles;
+    const __amdgpu_buffer_rsrc_t wres = rsrc(a.tiles + static_cast<std::int64_t>(my_live ? my_nt : 0) * a.k_tiles * kTileBytes,
+                                             my_live ? static_cast<std::uint32_t>(a.k_tiles * kTileBytes) : 0u);
+    const std::uint32_t meta_n = static_cast<std::uint32_t>(a.n_tiles * a.groups_p * kTileRows);
+    const __amdgpu_buffer_rsrc_t zres = rsrc(a.zero_points, ZP ? meta_n / 2 : 0u);
+    const __amdgpu_buffer_rsrc_t scres = rsrc(a.scales, meta_n * (a.scale_half ? 2 : 4));
+
+    // epilogue scales: this lane's 4 output columns (one per subtile), group kt
+    int col_nt[4];
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) col_nt[ni] = slot_tile<GELU>(a, nb, wave_slot<GELU>(wn, ni));
+
+    auto issue_a = [&](int kt, int stage) {
+        // 32 copies of 1 KiB per step; wave w issues copies 4w .. 4w+3. LDS byte p = 1024 i + 16 l of the stage is
+        // row r = 8 i + l / 8, 16-byte chunk c' = l % 8, holding global chunk c = c' ^ (r & 7).
+        std::uint8_t* base = lds + stage * kABytes;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int i = wave * 4 + s;
+            const int r = i * 8 + (lane >> 3);
+            const int c = (lane & 7) ^ (r & 7);
+            const std::uint32_t off = static_cast<std::uint32_t>(r) * a.K + kt * kBK + c * 16;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(base + i * 1024), 16, off, 0, 0, 0);
+        }
+        if (wave == 0) {
+            std::uint8_t* sb = lds + 2 * kABytes + 2 * kBBytes + stage * kSBytes;
+            const std::uint32_t off = (static_cast<std::uint32_t>(kt) * a.M_p + m0) * 4 + lane * 16;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sres, (lds_void*)sb, 16, off, 0, 0, 0);
+        }
+    };
+    struct Bregs {
+        uint4 w;
+        std::uint32_t zp;
+        std::uint32_t s[4];
+    };
+    auto issue_b = [&](int kt) {
+        Bregs b;
+        b.w = ld16(wres, static_cast<std::uint32_t>(kt * kTileBytes + lane * 16));
+        b.zp = 8;
+        if constexpr (ZP)
+            b.zp = __builtin_amdgcn_raw_buffer_load_b8(zres, my_live ? static_cast<std::uint32_t>((my_nt * a.groups_p + kt) * 8 + (nn >> 1)) : kOob, 0, 0);
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            const bool live = col_nt[ni] < a.n_tiles;
+            const std::uint32_t mi = static_cast<std::uint32_t>((col_nt[ni] * a.groups_p + kt) * kTileRows + nn);
+            b.s[ni] = a.scale_half ? __builtin_amdgcn_raw_buffer_load_b16(scres, live ? 2 * mi : kOob, 0, 0)
+                                   : __builtin_amdgcn_raw_buffer_load_b32(scres, live ? 4 * mi : kOob, 0, 0);
+        }
+        return b;
+    };
+    auto stage_b = [&](const Bregs& b, int stage) {
+        // unpack to int8 with the zero point folded in: byte = (u + 128 - zp) ^ 0x80 = u - zp (two's complement)
+        const std::uint32_t z = ZP ? ((b.zp >> (4 * (nn & 1))) & 15u) : 8u;
+        const std::uint32_t zz = z * 0x01010101u;
+        const std::uint32_t d[4] = {b.w.x, b.w.y, b.w.z, b.w.w};
+        std::uint8_t* bb = lds + 2 * kABytes + stage * kBBytes;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const std::uint32_t lo0 = d[2 * j] & 0x0F0F0F0Fu, hi0 = (d[2 * j] >> 4) & 0x0F0F0F0Fu;
+            const std::uint32_t lo1 = d[2 * j + 1] & 0x0F0F0F0Fu, hi1 = (d[2 * j + 1] >> 4) & 0x0F0F0F0Fu;
+            uint4 o;
+            o.x = ((lo0 | 0x80808080u) - zz) ^ 0x80808080u;
+            o.y = ((hi0 | 0x80808080u) - zz) ^ 0x80808080u;
+            o.z = ((lo1 | 0x80808080u) - zz) ^ 0x80808080u;
+            o.w = ((hi1 | 0x80808080u) - zz) ^ 0x80808080u;
+            *reinterpret_cast<uint4*>(bb + (st * 2 + j) * 1024 + lane * 16) = o;
+        }
+    };
+
+    v4i C[4][4];
+    float acc[4][4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            C[mi][ni] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[mi][ni][r] = 0.F;
+        }
+
+    // prologue: stage 0
+    issue_a(0, 0);
+    Bregs cur = issue_b(0);
+    stage_b(cur, 0);
+    float sv[4];
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+        sv[ni] = a.scale_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(cur.s[ni]))) : __uint_as_float(cur.s[ni]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    const int arow = wm * 64 + nn;  // A row of subtile 0 read by this lane
+    for (int kt = 0; kt < a.k_tiles; ++kt) {
+        const int stage = kt & 1;
+        const bool more = kt + 1 < a.k_tiles;
+        Bregs nxt;
+        if (more) {
+            issue_a(kt + 1, stage ^ 1);
+            nxt = issue_b(kt + 1);
+        }
+        const std::uint8_t* ab = lds + stage * kABytes;
+        const std::uint8_t* bb = lds + 2 * kABytes + stage * kBBytes;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            v4i A[4], B[4];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                const int r = arow + mi * 16;
+                const int c = (4 * j + L) ^ (r & 7);
+                A[mi] = *reinterpret_cast<const v4i*>(ab + r * kBK + c * 16);
+            }
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) B[ni] = *reinterpret_cast<const v4i*>(bb + (wave_slot<GELU>(wn, ni) * 2 + j) * 1024 + lane * 16);
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) C[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], B[ni], C[mi][ni], 0, 0, 0);
+        }
+        // epilogue of group kt
+        const float* sb = reinterpret_cast<const float*>(lds + 2 * kABytes + 2 * kBBytes + stage * kSBytes);
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+            const float4 as4 = *reinterpret_cast<const float4*>(sb + wm * 64 + mi * 16 + 4 * L);
+            const float as[4] = {as4.x, as4.y, as4.z, as4.w};
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int P = C[mi][ni][r];
+                    if (DBG && a.dump) {
+                        const int row = m0 + wm * 64 + mi * 16 + 4 * L + r, col = col_nt[ni] * kTileRows + nn;
+                        if (row < a.M && col_nt[ni] < a.n_tiles && col < a.N)
+                            a.dump[(static_cast<std::int64_t>(row) * a.N + col) * a.groups + kt] = P;
+                    }
+                    if constexpr (QM == QUANT_STATIC) acc[mi][ni][r] = acc[mi][ni][r] + sv[ni] * static_cast<float>(P);
+                    else acc[mi][ni][r] = acc[mi][ni][r] + (as[r] * sv[ni]) * static_cast<float>(P);
+                }
+                C[mi][ni] = v4i{0, 0, 0, 0};
+            }
+        }
+        if (more) {
+            stage_b(nxt, stage ^ 1);
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni)
+                sv[ni] = a.scale_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(nxt.s[ni]))) : __uint_as_float(nxt.s[ni]);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+
+    // store
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = m0 + wm * 64 + mi * 16 + 4 * L + r;
+            if (row >= a.M) continue;
+            if constexpr (GELU) {
+                const int half_n = a.N >> 1;
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni) {
+                    const int i = col_nt[ni] * kTileRows + nn;
+                    if (col_nt[ni] >= a.n_tiles || i >= half_n) continue;
+                    float g = acc[mi][ni][r], up = acc[mi][ni + 2][r];
+                    if (QM == QUANT_STATIC) {
+                        g = g * a.input_scale;
+                        up = up * a.input_scale;
+                    }
+                    g = calibrate_output(g, a.output_scale);
+                    up = calibrate_output(up, a.output_scale);
+                    a.y[static_cast<std::int64_t>(row) * half_n + i] = gelu_tanh(g) * up;
+                }
+            } else {
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) {
+                    const int col = col_nt[ni] * kTileRows + nn;
+                    if (col_nt[ni] >= a.n_tiles || col >= a.N) continue;
+                    float v = acc[mi][ni][r];
+                    if (QM == QUANT_STATIC) v = v * a.input_scale;
+                    a.y[static_cast<std::int64_t>(row) * a.N + col] = calibrate_output(v, a.output_scale);
+                }
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void unpermute_rows_kernel(const std::int8_t* q, int M, int K, std::int8_t* codes) {
+    const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= static_cast<std::int64_t>(M) * K) return;
+    const std::int64_t m = id / K, k = id % K;
+    codes[id] = q[m * K + act_position(k)];
+}
+
+__global__ __launch_bounds__(256) void transpose_stats_kernel(const float* s_t, const std::int32_t* q_t, int M, int M_p,
+                                                              int groups, float* s, std::int32_t* q, std::int32_t* z) {
+    const int id = blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= M * groups) return;
+    const int m = id / groups, b = id % groups;
+    if (s) s[id] = s_t[b * M_p + m];
+    if (q) q[id] = q_t[b * M_p + m];
+    if (z) z[id] = 0;
+}
+
+}  // namespace
+
+bool gemm_i4_fits(const LinearCall& c) {
+    const Weight& w = *c.w;
+    if (!w.tiled || w.geo.bits != 4 || w.geo.group != 128 || c.M <= 16) return false;
+    if (c.path != PATH_BLOCKWISE && c.path != PATH_SYMMETRIC) return false;
+    if (w.zero_mode == ZERO_FLOAT) return false;
+    if (w.geo.cols % 512 || w.geo.cols_p != w.geo.cols) return false;
+    if (c.gelu_gate && ((w.geo.rows / 2) % kTileRows || w.geo.n_tiles % 2)) return false;
+    const std::int64_t M_p = round_up(c.M, kBM);
+    if (M_p * w.geo.cols >= (std::int64_t{1} << 31) || w.geo.k_tiles * kTileBytes >= (std::int64_t{1} << 31) ||
+        w.geo.meta_count() * 4 >= (std::int64_t{1} << 31) || M_p * w.geo.groups_p * 4 >= (std::int64_t{1} << 31))
+        return false;
+    return true;
+}
+
+std::int64_t gemm_i4_rows(std::int64_t M) { return round_up(M, kBM); }
+
+hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_t stream) {
+    const Weight& w = *c.w;
+    const int M = static_cast<int>(c.M), K = static_cast<int>(w.geo.cols);
+    const int M_p = static_cast<int>(gemm_i4_rows(c.M));
+    const bool stat = c.path == PATH_SYMMETRIC;
+    QRowArgs q{};
+    q.x = c.x;
+    q.x_f32 = c.x_type == ACT_F32;
+    q.M = M;
+    q.M_p = M_p;
+    q.K = K;
+    q.input_scale = c.input_scale;
+    q.q = act.q;
+    q.scale_t = act.scale;
+    q.sum_t = nullptr;
+    const int waves = M_p * (K / 512);
+    const dim3 qgrid(static_cast<unsigned>((waves + 3) / 4)), qblock(256);
+    if (stat) hipLaunchKernelGGL(quantize_rows_kernel<dev::QUANT_STATIC>, qgrid, qblock, 0, stream, q);
+    else hipLaunchKernelGGL(quantize_rows_kernel<dev::QUANT_DYN_SYM>, qgrid, qblock, 0, stream, q);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+
+    GemmArgs a{};
+    a.q = act.q;
+    a.scale_t = act.scale;
+    a.tiles = w.tiles;
+    a.scales = w.scales;
+    a.zero_points = w.zero_mode == ZERO_POINT ? w.zero_points : nullptr;
+    a.y = c.y;
+    a.dump = c.dump;
+    a.M = M;
+    a.M_p = M_p;
+    a.N = static_cast<int>(w.geo.rows);
+    a.K = K;
+    a.k_tiles = static_cast<int>(w.geo.k_tiles);
+    a.n_tiles = static_cast<int>(w.geo.n_tiles);
+    a.groups_p = static_cast<int>(w.geo.groups_p);
+    a.groups = static_cast<int>(w.geo.cols / w.geo.group);
+    a.scale_half = w.scale_type == META_F16;
+    a.input_scale = c.input_scale;
+    a.output_scale = c.output_scale;
+    a.m_blocks = M_p / kBM;
+    a.n_blocks = c.gelu_gate ? static_cast<int>((w.geo.n_tiles / 2 + 3) / 4) : static_cast<int>((w.geo.n_tiles + 7) / 8);
+    const dim3 grid(static_cast<unsigned>(a.m_blocks * a.n_blocks)), block(64 * kWaves);
+    const bool zp = w.zero_mode == ZERO_POINT;
+    const bool dbg = c.dump != nullptr;
+#define KQ_G(GE, QM, Z, D) hipLaunchKernelGGL((gemm_i4_kernel<GE, QM, Z, D>), grid, block, kLds, stream, a)
+    if (stat) {
+        if (c.gelu_gate) KQ_G(true, dev::QUANT_STATIC, false, false);
+        else if (dbg) KQ_G(false, dev::QUANT_STATIC, false, true);
+        else KQ_G(false, dev::QUANT_STATIC, false, false);
+    } else if (zp) {
+        if (c.gelu_gate) KQ_G(true, dev::QUANT_DYN_SYM, true, false);
+        else if (dbg) KQ_G(false, dev::QUANT_DYN_SYM, true, true);
+        else KQ_G(false, dev::QUANT_DYN_SYM, true, false);
+    } else {
+        if (c.gelu_gate) KQ_G(true, dev::QUANT_DYN_SYM, false, false);
+        else if (dbg) KQ_G(false, dev::QUANT_DYN_SYM, false, true);
+        else KQ_G(false, dev::QUANT_DYN_SYM, false, false);
+    }
+#undef KQ_G
+    return hipGetLastError();
+}
+
+// Quantizer outputs of the prefill path in the debug form (natural-order codes [M][K], stats [M][K/g]).
+hipError_t launch_gemm_i4_quantize_dump(const LinearCall& c, const ActBuffers& act, std::int8_t* codes, float* scales,
+                                        std::int32_t* sums, std::int32_t* zero_points, hipStream_t stream) {
+    const Weight& w = *c.w;
+    const int M = static_cast<int>(c.M), K = static_cast<int>(w.geo.cols);
+    const int M_p = static_cast<int>(gemm_i4_rows(c.M));
+    QRowArgs q{};
+    q.x = c.x;
+    q.x_f32 = c.x_type == ACT_F32;
+    q.M = M;
+    q.M_p = M_p;
+    q.K = K;
+    q.input_scale = c.input_scale;
+    q.q = act.q;
+    q.scale_t = act.scale;
+    q.sum_t = act.sum;
+    const int waves = M_p * (K / 512);
+    const dim3 qgrid(static_cast<unsigned>((waves + 3) / 4)), qblock(256);
+    if (c.path == PATH_SYMMETRIC) hipLaunchKernelGGL(quantize_rows_kernel<dev::QUANT_STATIC>, qgrid, qblock, 0, stream, q);
+    else hipLaunchKernelGGL(quantize_rows_kernel<dev::QUANT_DYN_SYM>, qgrid, qblock, 0, stream, q);
+    const std::int64_t total = static_cast<std::int64_t>(M) * K;
+    if (codes) hipLaunchKernelGGL(unpermute_rows_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, act.q, M, K, codes);
+    const int groups = K / 128;
+    hipLaunchKernelGGL(transpose_stats_kernel, dim3(static_cast<unsigned>((M * groups + 255) / 256)), dim3(256), 0, stream,
+                       act.scale, act.sum, M, M_p, groups, scales, sums, zero_points);
+    return hipGetLastError();
+}
+
+}  // namespace kq

@@ -76,6 +76,14 @@ bool decode_fits(const LinearCall& c);
 hipError_t launch_decode(const LinearCall& c, hipStream_t stream);
 hipError_t launch_skinny(const LinearCall& c, const SkinnyPlan& p, hipStream_t stream);
 
+// Prefill projection (M > 16) for 4-bit weights with g = 128 and K a multiple of 512 (kq_gemm.hip): a row
+// quantizer writing codes [rows_p][K] and transposed block scales [K/128][rows_p] into the workspace, then the int8
+// MFMA GEMM. rows_p = round_up(M, 256).
+bool gemm_i4_fits(const LinearCall& c);
+hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_t stream);
+hipError_t launch_gemm_i4_quantize_dump(const LinearCall& c, const ActBuffers& act, std::int8_t* codes, float* scales,
+                                        std::int32_t* sums, std::int32_t* zero_points, hipStream_t stream);
+
 std::size_t workspace_bytes(const Weight& w, std::int64_t M);
 ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base);
 

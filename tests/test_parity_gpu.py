@@ -101,6 +101,12 @@ CASES = [
     (2, 32, 140, 512, 144, None, 0.05, False, 0.0),
     (2, 128, 33, 512, 128, None, 0.05, False, 0.0),
     (4, 32, 257, 256, 128, None, 0.05, False, 0.0),
+    # int8 MFMA GEMM (4-bit, g = 128, K a multiple of 512): several row blocks, ragged N, static and symmetric
+    (4, 128, 300, 1024, 400, None, 0.0, False, 0.0),
+    (4, 128, 513, 512, 256, "zp", 0.0, True, 0.001),
+    (4, 128, 17, 2048, 128, None, 0.05, False, 0.0),
+    (4, 128, 64, 512, 1040, "zp", 0.0, True, 0.0),
+    (4, 128, 260, 1536, 144, "zp", 0.0, False, 0.001),
     # group sizes the tiles cannot carry (row-major integer path)
     (4, 96, 3, 384, 256, "zp", 0.0, False, 0.0),
     (8, 48, 2, 288, 96, None, 0.0, False, 0.0),
@@ -271,11 +277,11 @@ def test_zero_block_and_empty(dev, ref):
     assert tuple(empty.shape) == (0, 256)
 
 
-@pytest.mark.parametrize("M", [1, 4, 16, 200])
-def test_gelu_gate_fused(dev, ref, M):
+@pytest.mark.parametrize("M,I", [(1, 256), (4, 256), (16, 256), (200, 256), (300, 272)])
+def test_gelu_gate_fused(dev, ref, M, I):
     """gate/up projection + GELU-tanh in one pass equals the oracle's projection followed by gelu_gate."""
     rng = np.random.default_rng(M)
-    I, K = 256, 512
+    K = 512
     values, scales, zp, _ = weights(rng, 2 * I, K, 4, 128, zero_points=True)
     x = activations(rng, M, K)
     y_full, _ = ref.packed_linear(x, values, scales, 4, 128, zero_points=zp)
@@ -339,6 +345,22 @@ def test_baseline_decode_shapes(dev, ref, M, shape):
     np.testing.assert_array_equal(P_d.cpu().numpy().astype(np.int64),
                                   expected_partials(ref, q, codes, None, 4, 128, zero_points=zp))
     check_close(dw.linear(xt), y_ref)
+
+
+def test_prefill_f32_scales(dev, ref):
+    """GEMM path with F32 scales and F32 activations: partials bit-exact, outputs within tolerance."""
+    rng = np.random.default_rng(77)
+    M, K, N = 96, 1024, 256
+    values, scales, zp, codes = weights(rng, N, K, 4, 128, zero_points=True, scale_dtype=np.float32)
+    x = activations(rng, M, K)
+    y_ref, _ = ref.packed_linear(x, values, scales, 4, 128, zero_points=zp)
+    dw = device_weight(values, scales, 4, 128, dev, zero_points=zp)
+    y_d, P_d = dw.debug_partials(to_dev(x, dev))
+    q, _, _, _ = ref.quantize_dynamic(x, 128, 4)
+    np.testing.assert_array_equal(P_d.cpu().numpy().astype(np.int64),
+                                  expected_partials(ref, q, codes, None, 4, 128, zero_points=zp))
+    check_close(y_d, y_ref)
+    check_close(dw.linear(to_dev(x, dev)), y_ref)
 
 
 def test_baseline_prefill_rows(dev, ref):
