@@ -20,6 +20,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 
 #include "kq_device.hpp"
 #include "kq_internal.hpp"
@@ -30,13 +31,21 @@ namespace {
 using namespace dev;
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 256, kBN = 128, kBK = 128;  // rows, output columns (8 row tiles), columns per step
-constexpr int kWaves = 8;                       // 4 (rows) x 2 (columns), 64 x 64 per wave
-constexpr int kABytes = kBM * kBK;              // activation codes per stage
-constexpr int kBBytes = 8 * 2 * 1024;           // unpacked weights per stage: [tile][half][lane][16 B]
-constexpr int kSBytes = kBM * 4;                // activation scales per stage
-constexpr int kLds = 2 * (kABytes + kBBytes + kSBytes);
+constexpr int kBN = 128, kBK = 128;  // output columns (8 row tiles), columns per step (one group)
+constexpr int kBBytes = 8 * 2 * 1024;   // unpacked weights per stage: [tile slot][64-column half][lane][16 B]
+constexpr int kQuantRows = 256;         // activation rows are padded to this for every tile shape
+
+// Workgroup tile: WM x 2 waves of 64 x 64 outputs; BM = 64 WM rows x 128 columns.
+template <int WM>
+struct GemmShape {
+    static constexpr int BM = 64 * WM, WAVES = 2 * WM, THREADS = 64 * WAVES;
+    static constexpr int A_BYTES = BM * kBK;  // activation codes per stage
+    static constexpr int S_BYTES = BM * 4;    // activation scales per stage
+    static constexpr int LDS = 2 * (A_BYTES + kBBytes + S_BYTES);
+    static constexpr int TPW = 8 / WAVES;     // weight tiles each wave stages per step
+};
 constexpr int kRsrcWord3 = 0x00020000;
 constexpr std::uint32_t kOob = 0x80000000u;
 
@@ -159,45 +168,54 @@ __device__ __forceinline__ constexpr int wave_slot(int wn, int ni) {
     return GELU ? (ni < 2 ? 2 * wn + ni : 4 + 2 * wn + ni - 2) : 4 * wn + ni;
 }
 
-template <bool GELU, int QM, bool ZP, bool DBG>
-__global__ __launch_bounds__(512) void gemm_i4_kernel(GemmArgs a) {
+template <int WM, bool GELU, int QM, bool ZP, bool SH, bool DBG>
+__global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArgs a) {
+    using S = GemmShape<WM>;
     extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 3, wn = wave >> 2;
+    const int wm = wave % WM, wn = wave / WM;
     const int nn = lane & 15, L = lane >> 4;
 
     // workgroup -> (row block, column block): consecutive workgroups go to different XCDs, so give each XCD a
-    // contiguous range (8 column blocks x all row blocks share its L2)
+    // contiguous range (its column blocks x all row blocks share its L2)
     const int total = a.m_blocks * a.n_blocks;
     int bid = blockIdx.x;
     if (total % 8 == 0) bid = (bid % 8) * (total / 8) + bid / 8;
     const int mb = bid % a.m_blocks, nb = bid / a.m_blocks;
-    const int m0 = mb * kBM;
+    const int m0 = mb * S::BM;
 
-    // activation panel of this workgroup: rows [m0, m0 + 256) x K
-    const __amdgpu_buffer_rsrc_t ares = rsrc(a.q + static_cast<std::int64_t>(m0) * a.K, static_cast<std::uint32_t>(kBM) * a.K);
+    std::uint8_t* const a_lds = lds;
+    std::uint8_t* const b_lds = lds + 2 * S::A_BYTES;
+    std::uint8_t* const s_lds = lds + 2 * S::A_BYTES + 2 * kBBytes;
+
+    // activation panel of this workgroup: rows [m0, m0 + BM) x K (rows are padded to a multiple of 256)
+    const __amdgpu_buffer_rsrc_t ares = rsrc(a.q + static_cast<std::int64_t>(m0) * a.K, static_cast<std::uint32_t>(S::BM) * a.K);
     const __amdgpu_buffer_rsrc_t sres = rsrc(a.scale_t, static_cast<std::uint32_t>(a.groups_p) * a.M_p * 4);
 
-    // weight staging: thread -> (tile slot, lane of that tile)
-    const int st = tid >> 6;
-    const int my_nt = slot_tile<GELU>(a, nb, st);
-    const bool my_live = my_nt < a.n_tiles;
-    const __amdgpu_buffer_rsrc_t wres = rsrc(a.tiles + static_cast<std::int64_t>(my_live ? my_nt : 0) * a.k_tiles * kTileBytes,
-                                             my_live ? static_cast<std::uint32_t>(a.k_tiles * kTileBytes) : 0u);
+    // weight staging: wave -> TPW tile slots (uniform), lane -> 16-byte slot of each tile
+    int st_nt[S::TPW];
+    __amdgpu_buffer_rsrc_t wres[S::TPW];
+#pragma unroll
+    for (int u = 0; u < S::TPW; ++u) {
+        st_nt[u] = slot_tile<GELU>(a, nb, wave * S::TPW + u);
+        const bool live = st_nt[u] < a.n_tiles;
+        wres[u] = rsrc(a.tiles + static_cast<std::int64_t>(live ? st_nt[u] : 0) * a.k_tiles * kTileBytes,
+                       live ? static_cast<std::uint32_t>(a.k_tiles * kTileBytes) : 0u);
+    }
     const std::uint32_t meta_n = static_cast<std::uint32_t>(a.n_tiles * a.groups_p * kTileRows);
     const __amdgpu_buffer_rsrc_t zres = rsrc(a.zero_points, ZP ? meta_n / 2 : 0u);
-    const __amdgpu_buffer_rsrc_t scres = rsrc(a.scales, meta_n * (a.scale_half ? 2 : 4));
+    const __amdgpu_buffer_rsrc_t scres = rsrc(a.scales, meta_n * (SH ? 2 : 4));
 
-    // epilogue scales: this lane's 4 output columns (one per subtile), group kt
+    // the wave's 4 output column tiles (uniform)
     int col_nt[4];
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) col_nt[ni] = slot_tile<GELU>(a, nb, wave_slot<GELU>(wn, ni));
 
     auto issue_a = [&](int kt, int stage) {
-        // 32 copies of 1 KiB per step; wave w issues copies 4w .. 4w+3. LDS byte p = 1024 i + 16 l of the stage is
-        // row r = 8 i + l / 8, 16-byte chunk c' = l % 8, holding global chunk c = c' ^ (r & 7).
-        std::uint8_t* base = lds + stage * kABytes;
+        // BM / 8 copies of 1 KiB per step, 4 per wave. LDS byte 1024 i + 16 l of the stage is row r = 8 i + l / 8,
+        // 16-byte chunk c' = l % 8, which holds global chunk c = c' ^ (r & 7).
+        std::uint8_t* base = a_lds + stage * S::A_BYTES;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int i = wave * 4 + s;
@@ -206,128 +224,159 @@ __global__ __launch_bounds__(512) void gemm_i4_kernel(GemmArgs a) {
             const std::uint32_t off = static_cast<std::uint32_t>(r) * a.K + kt * kBK + c * 16;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(base + i * 1024), 16, off, 0, 0, 0);
         }
-        if (wave == 0) {
-            std::uint8_t* sb = lds + 2 * kABytes + 2 * kBBytes + stage * kSBytes;
-            const std::uint32_t off = (static_cast<std::uint32_t>(kt) * a.M_p + m0) * 4 + lane * 16;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(sres, (lds_void*)sb, 16, off, 0, 0, 0);
+        if (wave < WM) {  // activation scales of rows [m0 + 64 wave, +64) for group kt
+            const std::uint32_t off = (static_cast<std::uint32_t>(kt) * a.M_p + m0 + 64 * wave + lane) * 4;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sres, (lds_void*)(s_lds + stage * S::S_BYTES + 256 * wave), 4, off, 0, 0, 0);
         }
     };
     struct Bregs {
-        uint4 w;
-        std::uint32_t zp;
+        uint4 w[S::TPW];
+        std::uint32_t zp[S::TPW];
         std::uint32_t s[4];
     };
     auto issue_b = [&](int kt) {
         Bregs b;
-        b.w = ld16(wres, static_cast<std::uint32_t>(kt * kTileBytes + lane * 16));
-        b.zp = 8;
-        if constexpr (ZP)
-            b.zp = __builtin_amdgcn_raw_buffer_load_b8(zres, my_live ? static_cast<std::uint32_t>((my_nt * a.groups_p + kt) * 8 + (nn >> 1)) : kOob, 0, 0);
+#pragma unroll
+        for (int u = 0; u < S::TPW; ++u) {
+            b.w[u] = ld16(wres[u], static_cast<std::uint32_t>(kt * kTileBytes + lane * 16));
+            b.zp[u] = 8;
+            if constexpr (ZP)
+                b.zp[u] = __builtin_amdgcn_raw_buffer_load_b8(
+                    zres, st_nt[u] < a.n_tiles ? static_cast<std::uint32_t>((st_nt[u] * a.groups_p + kt) * 8 + (nn >> 1)) : kOob, 0, 0);
+        }
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) {
             const bool live = col_nt[ni] < a.n_tiles;
             const std::uint32_t mi = static_cast<std::uint32_t>((col_nt[ni] * a.groups_p + kt) * kTileRows + nn);
-            b.s[ni] = a.scale_half ? __builtin_amdgcn_raw_buffer_load_b16(scres, live ? 2 * mi : kOob, 0, 0)
-                                   : __builtin_amdgcn_raw_buffer_load_b32(scres, live ? 4 * mi : kOob, 0, 0);
+            if constexpr (SH) b.s[ni] = __builtin_amdgcn_raw_buffer_load_b16(scres, live ? 2 * mi : kOob, 0, 0);
+            else b.s[ni] = __builtin_amdgcn_raw_buffer_load_b32(scres, live ? 4 * mi : kOob, 0, 0);
         }
         return b;
     };
     auto stage_b = [&](const Bregs& b, int stage) {
-        // unpack to int8 with the zero point folded in: byte = (u + 128 - zp) ^ 0x80 = u - zp (two's complement)
-        const std::uint32_t z = ZP ? ((b.zp >> (4 * (nn & 1))) & 15u) : 8u;
-        const std::uint32_t zz = z * 0x01010101u;
-        const std::uint32_t d[4] = {b.w.x, b.w.y, b.w.z, b.w.w};
-        std::uint8_t* bb = lds + 2 * kABytes + stage * kBBytes;
+        // unpack to int8 with the zero point folded in: byte = ((u | 0x80) - zp) ^ 0x80 = u - zp (two's complement)
+        std::uint8_t* bb = b_lds + stage * kBBytes;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const std::uint32_t lo0 = d[2 * j] & 0x0F0F0F0Fu, hi0 = (d[2 * j] >> 4) & 0x0F0F0F0Fu;
-            const std::uint32_t lo1 = d[2 * j + 1] & 0x0F0F0F0Fu, hi1 = (d[2 * j + 1] >> 4) & 0x0F0F0F0Fu;
-            uint4 o;
-            o.x = ((lo0 | 0x80808080u) - zz) ^ 0x80808080u;
-            o.y = ((hi0 | 0x80808080u) - zz) ^ 0x80808080u;
-            o.z = ((lo1 | 0x80808080u) - zz) ^ 0x80808080u;
-            o.w = ((hi1 | 0x80808080u) - zz) ^ 0x80808080u;
-            *reinterpret_cast<uint4*>(bb + (st * 2 + j) * 1024 + lane * 16) = o;
+        for (int u = 0; u < S::TPW; ++u) {
+            const std::uint32_t z = ZP ? ((b.zp[u] >> (4 * (nn & 1))) & 15u) : 8u;
+            const std::uint32_t zz = z * 0x01010101u;
+            const std::uint32_t d[4] = {b.w[u].x, b.w[u].y, b.w[u].z, b.w[u].w};
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const std::uint32_t lo0 = d[2 * j] & 0x0F0F0F0Fu, hi0 = (d[2 * j] >> 4) & 0x0F0F0F0Fu;
+                const std::uint32_t lo1 = d[2 * j + 1] & 0x0F0F0F0Fu, hi1 = (d[2 * j + 1] >> 4) & 0x0F0F0F0Fu;
+                uint4 o;
+                o.x = ((lo0 | 0x80808080u) - zz) ^ 0x80808080u;
+                o.y = ((hi0 | 0x80808080u) - zz) ^ 0x80808080u;
+                o.z = ((lo1 | 0x80808080u) - zz) ^ 0x80808080u;
+                o.w = ((hi1 | 0x80808080u) - zz) ^ 0x80808080u;
+                *reinterpret_cast<uint4*>(bb + ((wave * S::TPW + u) * 2 + j) * 1024 + lane * 16) = o;
+            }
         }
     };
+    auto scale_of = [](std::uint32_t raw) {
+        if constexpr (SH) return __half2float(__ushort_as_half(static_cast<unsigned short>(raw)));
+        else return __uint_as_float(raw);
+    };
 
-    v4i C[4][4];
     float acc[4][4][4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
-            C[mi][ni] = v4i{0, 0, 0, 0};
+        for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[mi][ni][r] = 0.F;
-        }
 
     // prologue: stage 0
     issue_a(0, 0);
-    Bregs cur = issue_b(0);
-    stage_b(cur, 0);
     float sv[4];
+    {
+        const Bregs cur = issue_b(0);
+        stage_b(cur, 0);
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni)
-        sv[ni] = a.scale_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(cur.s[ni]))) : __uint_as_float(cur.s[ni]);
+        for (int ni = 0; ni < 4; ++ni) sv[ni] = scale_of(cur.s[ni]);
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     const int arow = wm * 64 + nn;  // A row of subtile 0 read by this lane
+    const int srow = wm * 64 + 4 * L + (lane & 3);  // row whose activation scale this lane feeds the outer product
+    const v4i zero = {0, 0, 0, 0};
+    const v4f zerof = {0.F, 0.F, 0.F, 0.F};
     for (int kt = 0; kt < a.k_tiles; ++kt) {
         const int stage = kt & 1;
-        const bool more = kt + 1 < a.k_tiles;
-        Bregs nxt;
-        if (more) {
-            issue_a(kt + 1, stage ^ 1);
-            nxt = issue_b(kt + 1);
-        }
-        const std::uint8_t* ab = lds + stage * kABytes;
-        const std::uint8_t* bb = lds + 2 * kABytes + stage * kBBytes;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            v4i A[4], B[4];
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
-                const int r = arow + mi * 16;
-                const int c = (4 * j + L) ^ (r & 7);
-                A[mi] = *reinterpret_cast<const v4i*>(ab + r * kBK + c * 16);
-            }
-#pragma unroll
-            for (int ni = 0; ni < 4; ++ni) B[ni] = *reinterpret_cast<const v4i*>(bb + (wave_slot<GELU>(wn, ni) * 2 + j) * 1024 + lane * 16);
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni) C[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], B[ni], C[mi][ni], 0, 0, 0);
-        }
-        // epilogue of group kt
-        const float* sb = reinterpret_cast<const float*>(lds + 2 * kABytes + 2 * kBBytes + stage * kSBytes);
+        // next stage (the last step reloads its own group into the idle stage, keeping the loop branch-free)
+        const int kn = kt + 1 < a.k_tiles ? kt + 1 : kt;
+        issue_a(kn, stage ^ 1);
+        const Bregs nxt = issue_b(kn);
+
+        const std::uint8_t* ab = a_lds + stage * S::A_BYTES;
+        const std::uint8_t* bb = b_lds + stage * kBBytes;
+        const float* sb = reinterpret_cast<const float*>(s_lds + stage * S::S_BYTES);
+        v4i A[4][2], B[4][2];
+        float asel[4];
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
-            const float4 as4 = *reinterpret_cast<const float4*>(sb + wm * 64 + mi * 16 + 4 * L);
-            const float as[4] = {as4.x, as4.y, as4.z, as4.w};
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) {
+            for (int j = 0; j < 2; ++j) {
+                const int r = arow + mi * 16;
+                A[mi][j] = *reinterpret_cast<const v4i*>(ab + r * kBK + (((4 * j + L) ^ (r & 7)) * 16));
+            }
+            asel[mi] = sb[srow + mi * 16];
+        }
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int P = C[mi][ni][r];
-                    if (DBG && a.dump) {
-                        const int row = m0 + wm * 64 + mi * 16 + 4 * L + r, col = col_nt[ni] * kTileRows + nn;
-                        if (row < a.M && col_nt[ni] < a.n_tiles && col < a.N)
-                            a.dump[(static_cast<std::int64_t>(row) * a.N + col) * a.groups + kt] = P;
-                    }
-                    if constexpr (QM == QUANT_STATIC) acc[mi][ni][r] = acc[mi][ni][r] + sv[ni] * static_cast<float>(P);
-                    else acc[mi][ni][r] = acc[mi][ni][r] + (as[r] * sv[ni]) * static_cast<float>(P);
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                B[ni][j] = *reinterpret_cast<const v4i*>(bb + (wave_slot<GELU>(wn, ni) * 2 + j) * 1024 + lane * 16);
+
+        // 16 blocks of 16 x 16. Block b: two int8 MFMAs give the exact partials P' of group kt; a 4x4x1 f32 MFMA
+        // (16 outer products of 4 rows x 4 columns) gives k = a_s * s in the same lane layout (lane = column
+        // nn + 16 L, register r = row 4 L + r). The epilogue of block b (acc += k * P', two VALU per element) is
+        // issued after the MFMAs of block b + 1.
+        auto mfmas = [&](int blk, v4i& c, v4f& k) {
+            const int mi = blk >> 2, ni = blk & 3;
+            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi][0], B[ni][0], zero, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi][1], B[ni][1], c, 0, 0, 0);
+            if constexpr (QM != QUANT_STATIC) k = __builtin_amdgcn_mfma_f32_4x4x1f32(asel[mi], sv[ni], zerof, 0, 0, 0);
+        };
+        auto epilogue = [&](const v4i& c, const v4f& k, int blk) {
+            const int mi = blk >> 2, ni = blk & 3;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int P = c[r];
+                if (DBG && a.dump) {
+                    const int row = m0 + wm * 64 + mi * 16 + 4 * L + r, col = col_nt[ni] * kTileRows + nn;
+                    if (row < a.M && col_nt[ni] < a.n_tiles && col < a.N)
+                        a.dump[(static_cast<std::int64_t>(row) * a.N + col) * a.groups + kt] = P;
                 }
-                C[mi][ni] = v4i{0, 0, 0, 0};
+                const float kk = QM == QUANT_STATIC ? sv[ni] : k[r];
+                acc[mi][ni][r] = __builtin_fmaf(kk, static_cast<float>(P), acc[mi][ni][r]);
+            }
+        };
+        v4i cp, cn;
+        v4f kp = zerof, kn4 = zerof;
+        mfmas(0, cp, kp);
+#pragma unroll
+        for (int blk = 1; blk <= 16; ++blk) {
+            if (blk < 16) mfmas(blk, cn, kn4);
+            epilogue(cp, kp, blk - 1);
+            cp = cn;
+            kp = kn4;
+        }
+        if constexpr (!DBG) {
+            // one block: 3 MFMAs (2 with static activations), then the 8 VALU of the previous block's epilogue
+            __builtin_amdgcn_sched_group_barrier(0x100, 20, 0);
+#pragma unroll
+            for (int blk = 0; blk < 16; ++blk) {
+                __builtin_amdgcn_sched_group_barrier(0x008, QM == QUANT_STATIC ? 2 : 3, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
             }
         }
-        if (more) {
-            stage_b(nxt, stage ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_b(nxt, stage ^ 1);
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni)
-                sv[ni] = a.scale_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(nxt.s[ni]))) : __uint_as_float(nxt.s[ni]);
-        }
+        for (int ni = 0; ni < 4; ++ni) sv[ni] = scale_of(nxt.s[ni]);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
@@ -394,14 +443,14 @@ bool gemm_i4_fits(const LinearCall& c) {
     if (w.zero_mode == ZERO_FLOAT) return false;
     if (w.geo.cols % 512 || w.geo.cols_p != w.geo.cols) return false;
     if (c.gelu_gate && ((w.geo.rows / 2) % kTileRows || w.geo.n_tiles % 2)) return false;
-    const std::int64_t M_p = round_up(c.M, kBM);
+    const std::int64_t M_p = round_up(c.M, kQuantRows);
     if (M_p * w.geo.cols >= (std::int64_t{1} << 31) || w.geo.k_tiles * kTileBytes >= (std::int64_t{1} << 31) ||
         w.geo.meta_count() * 4 >= (std::int64_t{1} << 31) || M_p * w.geo.groups_p * 4 >= (std::int64_t{1} << 31))
         return false;
     return true;
 }
 
-std::int64_t gemm_i4_rows(std::int64_t M) { return round_up(M, kBM); }
+std::int64_t gemm_i4_rows(std::int64_t M) { return round_up(M, kQuantRows); }
 
 hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_t stream) {
     const Weight& w = *c.w;
@@ -444,25 +493,43 @@ hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_
     a.scale_half = w.scale_type == META_F16;
     a.input_scale = c.input_scale;
     a.output_scale = c.output_scale;
-    a.m_blocks = M_p / kBM;
-    a.n_blocks = c.gelu_gate ? static_cast<int>((w.geo.n_tiles / 2 + 3) / 4) : static_cast<int>((w.geo.n_tiles + 7) / 8);
-    const dim3 grid(static_cast<unsigned>(a.m_blocks * a.n_blocks)), block(64 * kWaves);
+    const int n_blocks = c.gelu_gate ? static_cast<int>((w.geo.n_tiles / 2 + 3) / 4) : static_cast<int>((w.geo.n_tiles + 7) / 8);
+    // 256-row tiles when they give the chip at least two workgroups per CU, else 128-row tiles
+    static const int forced_wm = [] {
+        const char* e = std::getenv("KQ_GEMM_WM");  // tuning override: 2 or 4
+        return e ? std::atoi(e) : 0;
+    }();
+    int wm = static_cast<std::int64_t>((M + 255) / 256) * n_blocks >= 512 ? 4 : 2;
+    if (forced_wm == 2 || forced_wm == 4) wm = forced_wm;
+    a.m_blocks = (M + 64 * wm - 1) / (64 * wm);
+    a.n_blocks = n_blocks;
     const bool zp = w.zero_mode == ZERO_POINT;
     const bool dbg = c.dump != nullptr;
-#define KQ_G(GE, QM, Z, D) hipLaunchKernelGGL((gemm_i4_kernel<GE, QM, Z, D>), grid, block, kLds, stream, a)
+    const bool sh = w.scale_type == META_F16;
+    const dim3 grid(static_cast<unsigned>(a.m_blocks * a.n_blocks));
+#define KQ_G(WM, GE, QM, Z, H, D) \
+    hipLaunchKernelGGL((gemm_i4_kernel<WM, GE, QM, Z, H, D>), grid, dim3(GemmShape<WM>::THREADS), GemmShape<WM>::LDS, stream, a)
+#define KQ_GH(WM, GE, QM, Z, D) \
+    if (sh) KQ_G(WM, GE, QM, Z, true, D); \
+    else KQ_G(WM, GE, QM, Z, false, D)
+#define KQ_GW(GE, QM, Z, D) \
+    if (wm == 4) { KQ_GH(4, GE, QM, Z, D); } \
+    else { KQ_GH(2, GE, QM, Z, D); }
     if (stat) {
-        if (c.gelu_gate) KQ_G(true, dev::QUANT_STATIC, false, false);
-        else if (dbg) KQ_G(false, dev::QUANT_STATIC, false, true);
-        else KQ_G(false, dev::QUANT_STATIC, false, false);
+        if (c.gelu_gate) { KQ_GW(true, dev::QUANT_STATIC, false, false) }
+        else if (dbg) { KQ_GW(false, dev::QUANT_STATIC, false, true) }
+        else { KQ_GW(false, dev::QUANT_STATIC, false, false) }
     } else if (zp) {
-        if (c.gelu_gate) KQ_G(true, dev::QUANT_DYN_SYM, true, false);
-        else if (dbg) KQ_G(false, dev::QUANT_DYN_SYM, true, true);
-        else KQ_G(false, dev::QUANT_DYN_SYM, true, false);
+        if (c.gelu_gate) { KQ_GW(true, dev::QUANT_DYN_SYM, true, false) }
+        else if (dbg) { KQ_GW(false, dev::QUANT_DYN_SYM, true, true) }
+        else { KQ_GW(false, dev::QUANT_DYN_SYM, true, false) }
     } else {
-        if (c.gelu_gate) KQ_G(true, dev::QUANT_DYN_SYM, false, false);
-        else if (dbg) KQ_G(false, dev::QUANT_DYN_SYM, false, true);
-        else KQ_G(false, dev::QUANT_DYN_SYM, false, false);
+        if (c.gelu_gate) { KQ_GW(true, dev::QUANT_DYN_SYM, false, false) }
+        else if (dbg) { KQ_GW(false, dev::QUANT_DYN_SYM, false, true) }
+        else { KQ_GW(false, dev::QUANT_DYN_SYM, false, false) }
     }
+#undef KQ_GW
+#undef KQ_GH
 #undef KQ_G
     return hipGetLastError();
 }

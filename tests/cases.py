@@ -41,3 +41,17 @@ def activations(rng: np.random.Generator, M: int, K: int, outliers: float = 0.0)
     b = x.view(np.uint32)
     b = ((b + (((b >> 16) & 1) + 0x7FFF)) >> 16) << 16
     return b.astype(np.uint32).view(np.float32)
+
+
+def expected_partials(ref, q, codes, zpa, bits, group, zero_points=None, dynamic=True):
+    """P' as the kernels define it: sum q*c, plus (8 - zp) * Q for uint4 zero points, minus zp_a * C for 8-bit."""
+    P, C = ref.partials(q, codes, group)
+    P = P.astype(np.int64)
+    M, K = q.shape
+    B = K // group
+    Q = q.astype(np.int64).reshape(M, B, group).sum(axis=2)
+    if zero_points is not None:
+        P = P + (8 - zero_points.astype(np.int64))[None, :, :] * Q[:, None, :]
+    if bits == 8 and dynamic:
+        P = P - zpa.astype(np.int64)[:, None, :] * C.astype(np.int64)[None, :, :]
+    return P

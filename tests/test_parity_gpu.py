@@ -6,7 +6,7 @@ max|dy| <= 2e-3 * max|y_ref|; exact equality where the reference pins exact valu
 import numpy as np
 import pytest
 
-from tests.cases import activations, pack_codes, weights
+from tests.cases import activations, expected_partials, pack_codes, weights
 
 pytestmark = pytest.mark.gpu
 
@@ -34,20 +34,6 @@ def device_weight(values, scales, bits, group, dev, zeros=None, zero_points=None
     conv = (lambda a: to_dev(a, dev)) if on_device else (lambda a: torch.from_numpy(np.ascontiguousarray(a)))
     z = zeros if zeros is not None else zero_points
     return DeviceWeight(conv(values), conv(scales), bits, group, conv(z) if z is not None else None)
-
-
-def expected_partials(ref, q, codes, zpa, bits, group, zero_points=None, dynamic=True):
-    """P' as the kernels define it: sum q*c, plus (8 - zp) * Q for uint4 zero points, minus zp_a * C for 8-bit."""
-    P, C = ref.partials(q, codes, group)
-    P = P.astype(np.int64)
-    M, K = q.shape
-    B = K // group
-    Q = q.astype(np.int64).reshape(M, B, group).sum(axis=2)
-    if zero_points is not None:
-        P = P + (8 - zero_points.astype(np.int64))[None, :, :] * Q[:, None, :]
-    if bits == 8 and dynamic:
-        P = P - zpa.astype(np.int64)[:, None, :] * C.astype(np.int64)[None, :, :]
-    return P
 
 
 def check_close(y, y_ref, tol=TOL):
