@@ -50,6 +50,9 @@ def parse():
     p.add_argument("--prefill-steps", type=int, default=50)
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget (0 = skip)")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--pmc-workload", action="store_true",
+                   help="run the HBM-traffic workload for rocprofv3 --pmc passes (a plain 256 MiB copy for calibration, "
+                        "then every rotated decode projection twice, one launch each, no graphs) and exit")
     return p.parse_args()
 
 
@@ -185,6 +188,14 @@ def main():
     gen.manual_seed(args.seed)
     stream_ptr = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
 
+    if args.pmc_workload:
+        src = torch.rand((64 << 20,), device=dev, generator=gen)  # 256 MiB float32
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)  # calibration kernel: reads 256 MiB, writes 256 MiB
+        torch.cuda.synchronize()
+        del src, dst
+
     # ---------------- decode GEMV (value) ----------------
     x = make_x(torch, dev, gen, M_DEC, K_DEC)
     projs = []
@@ -198,6 +209,13 @@ def main():
             del values, scales, zp
     torch.cuda.synchronize()
     R = len(projs)
+    if args.pmc_workload:
+        for _ in range(2):
+            for p in projs:
+                p(stream_ptr())
+        torch.cuda.synchronize()
+        print("pmc workload done", flush=True)
+        return
     graph_full = capture(torch, projs, stream_ptr)
     rem_graphs = {}
 
@@ -228,13 +246,17 @@ def main():
     ms_per_step = dev_ms / args.steps
     bytes_step = gemv_bytes(M_DEC, K_DEC, N_DEC, G_DEC)
     value = bytes_step / (ms_per_step * 1e-3) / 1e9
-    # The decode step is one kernel launch (kq_packed_linear -> skinny_kernel: activation quantization fused), so the
-    # per-launch device time over the timed region is the kernel's average launch duration including the launch
-    # gap between back-to-back kernels on the stream.
+    # The decode step is one kernel launch (kq_packed_linear -> decode_kernel: activation quantization fused), so
+    # the per-launch device time over the timed region is the kernel's average launch duration including the gap
+    # between back-to-back kernels on the stream.
+    traffic = load_traffic()
     roofline = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "skinny_kernel (fused quantize + int8 MFMA GEMV)", "bytes_per_launch": bytes_step,
-                "us_per_launch": round(ms_per_step * 1e3, 3)}
+                "frac": round(value / HBM_PEAK_GBS, 4),
+                "traffic": traffic["traffic_bytes_per_launch"] if traffic else None,
+                "kernel": "decode_kernel<4,128> (fused activation quantization + int8 MFMA GEMV)",
+                "bytes_per_launch": bytes_step, "us_per_launch": round(ms_per_step * 1e3, 3)}
+    if traffic:
+        roofline["traffic_source"] = traffic["source"]
 
     # MALL-resident figure (one weight, repeated): reported separately, never as HBM %
     g1 = capture(torch, [projs[0]] * 64, stream_ptr)
@@ -316,6 +338,19 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+def load_traffic():
+    """HBM bytes per decode_kernel launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes over
+    `bench.py --pmc-workload`, each scaled by what the counter reads for a plain copy of known size."""
+    path = os.path.join(ROOT, "profiles", "decode_kernel_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return {"traffic_bytes_per_launch": t["traffic_bytes_per_launch"],
+            "source": f"profiles/decode_kernel_traffic.json (FETCH_SIZE x {t['fetch_factor']}, "
+                      f"WRITE_SIZE x {t['write_factor']})"}
 
 
 def projs_bytes(N, K, g):

@@ -37,15 +37,84 @@ constexpr int kBN = 128, kBK = 128;  // output columns (8 row tiles), columns pe
 constexpr int kBBytes = 8 * 2 * 1024;   // unpacked weights per stage: [tile slot][64-column half][lane][16 B]
 constexpr int kQuantRows = 256;         // activation rows are padded to this for every tile shape
 
-// Workgroup tile: WM x 2 waves of 64 x 64 outputs; BM = 64 WM rows x 128 columns.
+// Workgroup tile: WM x 2 waves of 64 x 64 outputs; BM = 64 WM rows x 128 columns (one group) per k step. Every
+// global operand reaches LDS through direct copies (buffer_load ... lds), so no loaded register lives across steps:
+//   - activation codes, weight scales, activation scales: copied two steps ahead into a 3-slot ring;
+//   - packed int4 weight tiles and zero points: copied three steps ahead into a 3-slot ring, unpacked to int8
+//     (zero point folded in) LDS to LDS at the end of the previous step into a 2-slot ring of B operands.
+// One barrier per step; before it, s_waitcnt vmcnt(copies of this step) leaves only this step's copies in flight.
 template <int WM>
 struct GemmShape {
     static constexpr int BM = 64 * WM, WAVES = 2 * WM, THREADS = 64 * WAVES;
-    static constexpr int A_BYTES = BM * kBK;  // activation codes per stage
-    static constexpr int S_BYTES = BM * 4;    // activation scales per stage
-    static constexpr int LDS = 2 * (A_BYTES + kBBytes + S_BYTES);
-    static constexpr int TPW = 8 / WAVES;     // weight tiles each wave stages per step
+    static constexpr int TPW = 8 / WAVES;                 // weight tiles each wave copies and unpacks per step
+    static constexpr int A_BYTES = BM * kBK;              // activation codes per slot
+    static constexpr int RAW_BYTES = 8 * kTileBytes;      // packed weight tiles per slot
+    static constexpr int WS_OFF = 0, ZP_OFF = 512, AS_OFF = 768;  // inside a metadata slot
+    static constexpr int META_BYTES = AS_OFF + BM * 4;
+    static constexpr int A_RING = 0;
+    static constexpr int RAW_RING = A_RING + 3 * A_BYTES;
+    static constexpr int BQ_RING = RAW_RING + 3 * RAW_BYTES;
+    static constexpr int META_RING = BQ_RING + 2 * kBBytes;
+    static constexpr int SCRATCH = META_RING + 3 * META_BYTES;  // 256 bytes that idle copies write into
+    static constexpr int LDS = SCRATCH + 256;
+    static_assert(LDS <= 160 * 1024, "LDS budget");
 };
+
+// LDS reads and writes of the k loop are inline assembly with explicit lgkmcnt/vmcnt waits: the compiler cannot
+// tell a read of one ring slot from the copies in flight into the others, and would wait for those copies before
+// every read. Each wait ties the registers it guards, so no use can move above it.
+__device__ __forceinline__ std::uint32_t lds_addr(void* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return static_cast<std::uint32_t>(reinterpret_cast<std::uintptr_t>((lds_void*)p));
+#else
+    return static_cast<std::uint32_t>(reinterpret_cast<std::uintptr_t>(p));
+#endif
+}
+// (the host pass sees these bodies too; the asm is device-only)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define KQ_ASM(...) asm volatile(__VA_ARGS__)
+#else
+#define KQ_ASM(...) (void)0
+#endif
+template <int OFF>
+__device__ __forceinline__ v4i ds_read16(std::uint32_t addr) {
+    v4i v = {0, 0, 0, 0};
+    KQ_ASM("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ std::uint32_t ds_read4(std::uint32_t addr) {
+    std::uint32_t v = 0;
+    KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ std::uint32_t ds_read2(std::uint32_t addr) {
+    std::uint32_t v = 0;
+    KQ_ASM("ds_read_u16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ std::uint32_t ds_read1(std::uint32_t addr) {
+    std::uint32_t v = 0;
+    KQ_ASM("ds_read_u8 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ void ds_write16(std::uint32_t addr, v4u v) {
+    KQ_ASM("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "v"(v), "n"(OFF));
+}
+template <typename T>
+__device__ __forceinline__ void tie(T& x) {
+    KQ_ASM("" : "+v"(x));
+}
+template <int N, typename... T>
+__device__ __forceinline__ void lgkm_wait(T&... x) {
+    KQ_ASM("s_waitcnt lgkmcnt(%0)" : : "n"(N));
+    // the empty statements below make every guarded register an output of code after the wait
+    (tie(x), ...);
+}
+
 constexpr int kRsrcWord3 = 0x00020000;
 constexpr std::uint32_t kOob = 0x80000000u;
 
@@ -73,6 +142,10 @@ __device__ __forceinline__ int row16_sum(int v) {
     v += dpp<0x141>(v);
     return v + dpp<0x140>(v);
 }
+
+// Position of row m's block scale inside a [groups][M_p] row of the transposed scales: within each 64-row block,
+// row 16 q + t is stored at 4 t + q, so the 4 rows 16 apart that one GEMM lane scales are adjacent.
+__device__ __forceinline__ int scale_slot(int m) { return (m & ~63) | ((m & 15) << 2) | ((m >> 4) & 3); }
 
 struct QRowArgs {
     const void* x;
@@ -130,7 +203,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(QRowArgs a) {
     *reinterpret_cast<uint2*>(a.q + static_cast<std::int64_t>(m) * a.K + c * 512 + act_position(8 * lane)) = make_uint2(lo, hi);
     total = row16_sum(total);
     if ((lane & 15) == 0) {
-        const std::int64_t o = static_cast<std::int64_t>(c * 4 + (lane >> 4)) * a.M_p + m;
+        const std::int64_t o = static_cast<std::int64_t>(c * 4 + (lane >> 4)) * a.M_p + scale_slot(m);
         a.scale_t[o] = qb.s;
         if (a.sum_t) a.sum_t[o] = total;
     }
@@ -176,6 +249,7 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave % WM, wn = wave / WM;
     const int nn = lane & 15, L = lane >> 4;
+    const std::uint32_t lds0 = lds_addr(lds);
 
     // workgroup -> (row block, column block): consecutive workgroups go to different XCDs, so give each XCD a
     // contiguous range (its column blocks x all row blocks share its L2)
@@ -185,15 +259,9 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
     const int mb = bid % a.m_blocks, nb = bid / a.m_blocks;
     const int m0 = mb * S::BM;
 
-    std::uint8_t* const a_lds = lds;
-    std::uint8_t* const b_lds = lds + 2 * S::A_BYTES;
-    std::uint8_t* const s_lds = lds + 2 * S::A_BYTES + 2 * kBBytes;
-
     // activation panel of this workgroup: rows [m0, m0 + BM) x K (rows are padded to a multiple of 256)
     const __amdgpu_buffer_rsrc_t ares = rsrc(a.q + static_cast<std::int64_t>(m0) * a.K, static_cast<std::uint32_t>(S::BM) * a.K);
-    const __amdgpu_buffer_rsrc_t sres = rsrc(a.scale_t, static_cast<std::uint32_t>(a.groups_p) * a.M_p * 4);
-
-    // weight staging: wave -> TPW tile slots (uniform), lane -> 16-byte slot of each tile
+    // packed weight tiles of the wave's slots (uniform per wave)
     int st_nt[S::TPW];
     __amdgpu_buffer_rsrc_t wres[S::TPW];
 #pragma unroll
@@ -203,80 +271,146 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
         wres[u] = rsrc(a.tiles + static_cast<std::int64_t>(live ? st_nt[u] : 0) * a.k_tiles * kTileBytes,
                        live ? static_cast<std::uint32_t>(a.k_tiles * kTileBytes) : 0u);
     }
-    const std::uint32_t meta_n = static_cast<std::uint32_t>(a.n_tiles * a.groups_p * kTileRows);
-    const __amdgpu_buffer_rsrc_t zres = rsrc(a.zero_points, ZP ? meta_n / 2 : 0u);
-    const __amdgpu_buffer_rsrc_t scres = rsrc(a.scales, meta_n * (SH ? 2 : 4));
-
     // the wave's 4 output column tiles (uniform)
     int col_nt[4];
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) col_nt[ni] = slot_tile<GELU>(a, nb, wave_slot<GELU>(wn, ni));
+    // Metadata copies (4-byte lanes), META_N per wave, by role r = META_N wave + i: r = 0 the weight scales of the 8
+    // tile slots (F16: all 8, lane l -> slot l / 8; F32: slots 0-3, lane l -> slot l / 16), r = 1 their zero points
+    // (lane l < 16 -> slot l / 2), r = 2 .. WM + 1 the activation scales of rows [64 (r - 2), +64), r = WM + 2 (F32
+    // only) the weight scales of slots 4-7; other roles copy zeros into the scratch area. Lane source byte:
+    // base + step * k; out-of-range lanes read zeros.
+    constexpr int META_N = (2 + WM + (SH ? 0 : 1) <= S::WAVES) ? 1 : 2;
+    const std::uint32_t meta_n = static_cast<std::uint32_t>(a.n_tiles * a.groups_p * kTileRows);
+    __amdgpu_buffer_rsrc_t mres[META_N];
+    std::uint32_t meta_base[META_N], meta_step[META_N];
+    int meta_dst[META_N];  // byte offset inside a metadata slot; -1: the scratch area
+    bool meta_lead3[META_N];  // zero points travel with the packed tiles, three steps ahead
+#pragma unroll
+    for (int i = 0; i < META_N; ++i) {
+        const int role = wave * META_N + i;
+        meta_base[i] = kOob;
+        meta_step[i] = 0;
+        meta_dst[i] = -1;
+        meta_lead3[i] = role == 1;
+        mres[i] = rsrc(a.q, 0u);
+        if (role == 0 || (!SH && role == WM + 2)) {
+            constexpr int es = SH ? 2 : 4, lanes_per_slot = 16 * es / 4;
+            const int t = (role == 0 ? 0 : 4) + lane / lanes_per_slot;
+            const int nt = slot_tile<GELU>(a, nb, t);
+            mres[i] = rsrc(a.scales, meta_n * es);
+            if (nt < a.n_tiles) {
+                meta_base[i] = static_cast<std::uint32_t>(nt * a.groups_p) * kTileRows * es + (lane % lanes_per_slot) * 4;
+                meta_step[i] = kTileRows * es;
+            }
+            meta_dst[i] = S::WS_OFF + (role == 0 ? 0 : 256);
+        } else if (role == 1) {
+            const int nt = lane < 16 ? slot_tile<GELU>(a, nb, lane / 2) : a.n_tiles;
+            mres[i] = rsrc(a.zero_points, ZP ? meta_n / 2 : 0u);
+            if (ZP && nt < a.n_tiles) {
+                meta_base[i] = static_cast<std::uint32_t>(nt * a.groups_p) * 8 + (lane % 2) * 4;
+                meta_step[i] = 8;
+            }
+            meta_dst[i] = S::ZP_OFF;
+        } else if (role < 2 + WM) {  // rows in the permuted order of scale_t
+            mres[i] = rsrc(a.scale_t, static_cast<std::uint32_t>(a.groups_p) * a.M_p * 4);
+            if (QM != QUANT_STATIC) {
+                meta_base[i] = static_cast<std::uint32_t>(m0 + 64 * (role - 2) + lane) * 4;
+                meta_step[i] = static_cast<std::uint32_t>(a.M_p) * 4;
+            }
+            meta_dst[i] = S::AS_OFF + 256 * (role - 2);
+        }
+    }
 
-    auto issue_a = [&](int kt, int stage) {
-        // BM / 8 copies of 1 KiB per step, 4 per wave. LDS byte 1024 i + 16 l of the stage is row r = 8 i + l / 8,
-        // 16-byte chunk c' = l % 8, which holds global chunk c = c' ^ (r & 7).
-        std::uint8_t* base = a_lds + stage * S::A_BYTES;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int i = wave * 4 + s;
-            const int r = i * 8 + (lane >> 3);
-            const int c = (lane & 7) ^ (r & 7);
-            const std::uint32_t off = static_cast<std::uint32_t>(r) * a.K + kt * kBK + c * 16;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(base + i * 1024), 16, off, 0, 0, 0);
-        }
-        if (wave < WM) {  // activation scales of rows [m0 + 64 wave, +64) for group kt
-            const std::uint32_t off = (static_cast<std::uint32_t>(kt) * a.M_p + m0 + 64 * wave + lane) * 4;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(sres, (lds_void*)(s_lds + stage * S::S_BYTES + 256 * wave), 4, off, 0, 0, 0);
-        }
+    // Copies of one step: activation codes of step ka into A slot ka % 3, packed tiles of step kb into raw slot
+    // kb % 3, and this wave's metadata (step kb for zero points, else ka). The slot indices use the unclamped
+    // step numbers; clamped steps copy the last group again into slots nobody reads.
+    auto issue_a = [&](int ka, int sa, int part) {
+        // LDS byte 1024 i + 16 l of the slot is row r = 8 i + l / 8, 16-byte chunk c' = l % 8, which holds
+        // global chunk c = c' ^ (r & 7)
+        const int i = wave * 4 + part;
+        const int r = i * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ (r & 7);
+        const std::uint32_t off = static_cast<std::uint32_t>(r) * a.K + ka * kBK + c * 16;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(lds + S::A_RING + sa * S::A_BYTES + i * 1024), 16, off, 0, 0, 0);
     };
-    struct Bregs {
-        uint4 w[S::TPW];
-        std::uint32_t zp[S::TPW];
-        std::uint32_t s[4];
-    };
-    auto issue_b = [&](int kt) {
-        Bregs b;
+    // (resources are copied out of their arrays: an array element passed to the builtin directly makes the host
+    // pass drop the kernel's launch stub)
+    auto issue_raw = [&](int kb, int sb) {
 #pragma unroll
         for (int u = 0; u < S::TPW; ++u) {
-            b.w[u] = ld16(wres[u], static_cast<std::uint32_t>(kt * kTileBytes + lane * 16));
-            b.zp[u] = 8;
-            if constexpr (ZP)
-                b.zp[u] = __builtin_amdgcn_raw_buffer_load_b8(
-                    zres, st_nt[u] < a.n_tiles ? static_cast<std::uint32_t>((st_nt[u] * a.groups_p + kt) * 8 + (nn >> 1)) : kOob, 0, 0);
+            const __amdgpu_buffer_rsrc_t wr = wres[u];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(lds + S::RAW_RING + sb * S::RAW_BYTES + (wave * S::TPW + u) * kTileBytes),
+                                                     16, static_cast<std::uint32_t>(kb * kTileBytes + lane * 16), 0, 0, 0);
         }
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
-            const bool live = col_nt[ni] < a.n_tiles;
-            const std::uint32_t mi = static_cast<std::uint32_t>((col_nt[ni] * a.groups_p + kt) * kTileRows + nn);
-            if constexpr (SH) b.s[ni] = __builtin_amdgcn_raw_buffer_load_b16(scres, live ? 2 * mi : kOob, 0, 0);
-            else b.s[ni] = __builtin_amdgcn_raw_buffer_load_b32(scres, live ? 4 * mi : kOob, 0, 0);
-        }
-        return b;
     };
-    auto stage_b = [&](const Bregs& b, int stage) {
-        // unpack to int8 with the zero point folded in: byte = ((u | 0x80) - zp) ^ 0x80 = u - zp (two's complement)
-        std::uint8_t* bb = b_lds + stage * kBBytes;
+    auto issue_meta = [&](int ka, int sa, int kb, int sb) {
+#pragma unroll
+        for (int i = 0; i < META_N; ++i) {
+            const int km = meta_lead3[i] ? kb : ka, sm = meta_lead3[i] ? sb : sa;
+            const std::uint32_t moff = meta_base[i] == kOob ? kOob : meta_base[i] + meta_step[i] * km;
+            std::uint8_t* mdst = meta_dst[i] < 0 ? lds + S::SCRATCH : lds + S::META_RING + sm * S::META_BYTES + meta_dst[i];
+            const __amdgpu_buffer_rsrc_t mr = mres[i];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(mr, (lds_void*)mdst, 4, moff, 0, 0, 0);
+        }
+    };
+    // all copies of one step: activation codes of step ka into A slot sa, packed tiles of step kb into raw slot sb,
+    // this wave's metadata (step kb for zero points, else ka)
+    auto issue = [&](int ka, int sa, int kb, int sb) {
+#pragma unroll
+        for (int part = 0; part < 4; ++part) issue_a(ka, sa, part);
+        issue_raw(kb, sb);
+        issue_meta(ka, sa, kb, sb);
+    };
+    constexpr int kStepLoads = 4 + S::TPW + META_N;
+    constexpr int kStepWait = (kStepLoads & 15) | (7 << 4) | ((kStepLoads >> 4) << 14);  // vmcnt(n) lgkmcnt(0)
+
+    // Unpack the packed tiles of a step (raw slot sr, zero points in meta slot sm) into B slot sq: int8 with the
+    // zero point folded in, byte = ((u | 0x80) - zp) ^ 0x80 = u - zp, in B-operand order [slot][half][lane][16 B].
+    const std::uint32_t raw_lane = lds0 + S::RAW_RING + wave * S::TPW * kTileBytes + lane * 16;
+    const std::uint32_t zp_lane = lds0 + S::META_RING + S::ZP_OFF + wave * S::TPW * 8 + (nn >> 1);
+    const std::uint32_t bq_lane = lds0 + S::BQ_RING + wave * S::TPW * 2048 + lane * 16;
+    struct Raw {
+        v4i w[2];
+        std::uint32_t zp[2];
+    };
+    auto unpack_read = [&](int sr, int sm) {
+        Raw r;
+        r.zp[0] = r.zp[1] = 8;
+        r.w[0] = ds_read16<0>(raw_lane + sr * S::RAW_BYTES);
+        if constexpr (S::TPW == 2) r.w[1] = ds_read16<kTileBytes>(raw_lane + sr * S::RAW_BYTES);
+        if constexpr (ZP) {
+            r.zp[0] = ds_read1<0>(zp_lane + sm * S::META_BYTES);
+            if constexpr (S::TPW == 2) r.zp[1] = ds_read1<8>(zp_lane + sm * S::META_BYTES);
+        }
+        return r;
+    };
+    auto unpack_write = [&](Raw& r, int sq) {
+        if constexpr (S::TPW == 1) lgkm_wait<0>(r.w[0], r.zp[0]);
+        else lgkm_wait<0>(r.w[0], r.w[1], r.zp[0], r.zp[1]);
 #pragma unroll
         for (int u = 0; u < S::TPW; ++u) {
-            const std::uint32_t z = ZP ? ((b.zp[u] >> (4 * (nn & 1))) & 15u) : 8u;
+            const std::uint32_t z = ZP ? ((r.zp[u] >> (4 * (nn & 1))) & 15u) : 8u;
             const std::uint32_t zz = z * 0x01010101u;
-            const std::uint32_t d[4] = {b.w[u].x, b.w[u].y, b.w[u].z, b.w[u].w};
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const std::uint32_t lo0 = d[2 * j] & 0x0F0F0F0Fu, hi0 = (d[2 * j] >> 4) & 0x0F0F0F0Fu;
-                const std::uint32_t lo1 = d[2 * j + 1] & 0x0F0F0F0Fu, hi1 = (d[2 * j + 1] >> 4) & 0x0F0F0F0Fu;
-                uint4 o;
-                o.x = ((lo0 | 0x80808080u) - zz) ^ 0x80808080u;
-                o.y = ((hi0 | 0x80808080u) - zz) ^ 0x80808080u;
-                o.z = ((lo1 | 0x80808080u) - zz) ^ 0x80808080u;
-                o.w = ((hi1 | 0x80808080u) - zz) ^ 0x80808080u;
-                *reinterpret_cast<uint4*>(bb + ((wave * S::TPW + u) * 2 + j) * 1024 + lane * 16) = o;
+                const std::uint32_t d0 = static_cast<std::uint32_t>(r.w[u][2 * j]), d1 = static_cast<std::uint32_t>(r.w[u][2 * j + 1]);
+                v4u o;
+                o.x = (((d0 & 0x0F0F0F0Fu) | 0x80808080u) - zz) ^ 0x80808080u;
+                o.y = ((((d0 >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - zz) ^ 0x80808080u;
+                o.z = (((d1 & 0x0F0F0F0Fu) | 0x80808080u) - zz) ^ 0x80808080u;
+                o.w = ((((d1 >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - zz) ^ 0x80808080u;
+                const std::uint32_t dst = bq_lane + sq * kBBytes;
+                if (u == 0 && j == 0) ds_write16<0>(dst, o);
+                if (u == 0 && j == 1) ds_write16<1024>(dst, o);
+                if (u == 1 && j == 0) ds_write16<2048>(dst, o);
+                if (u == 1 && j == 1) ds_write16<3072>(dst, o);
             }
         }
     };
-    auto scale_of = [](std::uint32_t raw) {
-        if constexpr (SH) return __half2float(__ushort_as_half(static_cast<unsigned short>(raw)));
-        else return __uint_as_float(raw);
+    auto unpack = [&](int sr, int sm, int sq) {
+        Raw r = unpack_read(sr, sm);
+        unpack_write(r, sq);
     };
 
     float acc[4][4][4];
@@ -287,48 +421,68 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[mi][ni][r] = 0.F;
 
-    // prologue: stage 0
-    issue_a(0, 0);
-    float sv[4];
+    // prologue: steps 0 and 1 (activations, metadata) and 0..2 (packed tiles, zero points) copied, step 0 unpacked
     {
-        const Bregs cur = issue_b(0);
-        stage_b(cur, 0);
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni) sv[ni] = scale_of(cur.s[ni]);
+        const int k1 = a.k_tiles > 1 ? 1 : 0, k2 = a.k_tiles > 2 ? 2 : a.k_tiles - 1;
+        issue(0, 0, 0, 0);
+        issue(k1, 1, k1, 1);
+        issue(k1, 1, k2, 2);  // activations and scales of step 1 again (same bytes, same slot), tiles of step 2
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        unpack(0, 0, 0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
 
+    // per-lane operand addresses (add the slot base per step)
     const int arow = wm * 64 + nn;  // A row of subtile 0 read by this lane
-    const int srow = wm * 64 + 4 * L + (lane & 3);  // row whose activation scale this lane feeds the outer product
+    const std::uint32_t a_lane0 = lds0 + S::A_RING + arow * kBK + ((L ^ (arow & 7)) * 16);
+    const std::uint32_t a_lane1 = lds0 + S::A_RING + arow * kBK + (((4 + L) ^ (arow & 7)) * 16);
+    // B operands of the wave's subtiles start at slot wave_slot(wn, 0) (plain 4 wn; GELU 2 wn: gate 2 wn, 2 wn + 1
+    // and up 4 + 2 wn, 5 + 2 wn)
+    const std::uint32_t b_lane = lds0 + S::BQ_RING + wave_slot<GELU>(wn, 0) * 2048 + lane * 16;
+    constexpr int kWsStride = SH ? 32 : 64;  // bytes of one slot's 16 weight scales
+    const std::uint32_t ws_lane = lds0 + S::META_RING + S::WS_OFF + wave_slot<GELU>(wn, 0) * kWsStride + nn * (SH ? 2 : 4);
+    // activation scales of rows srow + 16 mi, mi = 0..3, srow = wm * 64 + t, t = 4 L + (lane & 3): adjacent in the
+    // permuted order (row 16 q + t of a 64-row block at 4 t + q)
+    const std::uint32_t as_lane = lds0 + S::META_RING + S::AS_OFF + (wm * 64 + 4 * (4 * L + (lane & 3))) * 4;
     const v4i zero = {0, 0, 0, 0};
     const v4f zerof = {0.F, 0.F, 0.F, 0.F};
-    for (int kt = 0; kt < a.k_tiles; ++kt) {
-        const int stage = kt & 1;
-        // next stage (the last step reloads its own group into the idle stage, keeping the loop branch-free)
-        const int kn = kt + 1 < a.k_tiles ? kt + 1 : kt;
-        issue_a(kn, stage ^ 1);
-        const Bregs nxt = issue_b(kn);
+#define KQ_BSLOT(ni) (GELU ? ((ni) < 2 ? (ni) : 2 + (ni)) : (ni))
 
-        const std::uint8_t* ab = a_lds + stage * S::A_BYTES;
-        const std::uint8_t* bb = b_lds + stage * kBBytes;
-        const float* sb = reinterpret_cast<const float*>(s_lds + stage * S::S_BYTES);
-        v4i A[4][2], B[4][2];
-        float asel[4];
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int r = arow + mi * 16;
-                A[mi][j] = *reinterpret_cast<const v4i*>(ab + r * kBK + (((4 * j + L) ^ (r & 7)) * 16));
-            }
-            asel[mi] = sb[srow + mi * 16];
+    int s0 = 0, s2 = 2;  // ring slots (mod 3) of steps kt and kt + 2; kt + 3 uses s0
+    for (int kt = 0; kt < a.k_tiles; ++kt) {
+        const int s1 = s0 == 2 ? 0 : s0 + 1;
+        // copies for steps kt + 2 (activations, scales) and kt + 3 (packed tiles, zero points), spread over the
+        // MFMA blocks below so the waves do not queue on the memory pipe together (clamped at the end: the last
+        // group again, into slots nobody reads)
+        const int ka = kt + 2 < a.k_tiles ? kt + 2 : a.k_tiles - 1, kb = kt + 3 < a.k_tiles ? kt + 3 : a.k_tiles - 1;
+
+        // operand reads, in the order the blocks consume them
+        const std::uint32_t mslot = s0 * S::META_BYTES;
+        std::uint32_t svr[4];
+        if constexpr (SH) {
+            svr[0] = ds_read2<KQ_BSLOT(0) * kWsStride>(ws_lane + mslot);
+            svr[1] = ds_read2<KQ_BSLOT(1) * kWsStride>(ws_lane + mslot);
+            svr[2] = ds_read2<KQ_BSLOT(2) * kWsStride>(ws_lane + mslot);
+            svr[3] = ds_read2<KQ_BSLOT(3) * kWsStride>(ws_lane + mslot);
+        } else {
+            svr[0] = ds_read4<KQ_BSLOT(0) * kWsStride>(ws_lane + mslot);
+            svr[1] = ds_read4<KQ_BSLOT(1) * kWsStride>(ws_lane + mslot);
+            svr[2] = ds_read4<KQ_BSLOT(2) * kWsStride>(ws_lane + mslot);
+            svr[3] = ds_read4<KQ_BSLOT(3) * kWsStride>(ws_lane + mslot);
         }
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                B[ni][j] = *reinterpret_cast<const v4i*>(bb + (wave_slot<GELU>(wn, ni) * 2 + j) * 1024 + lane * 16);
+        v4i asr = zero;
+        if constexpr (QM != QUANT_STATIC) asr = ds_read16<0>(as_lane + mslot);
+        const std::uint32_t aslot = s0 * S::A_BYTES, bslot = (kt & 1) * kBBytes;
+        v4i A[4][2], B[4][2];
+        A[0][0] = ds_read16<0>(a_lane0 + aslot);
+        A[0][1] = ds_read16<0>(a_lane1 + aslot);
+        B[0][0] = ds_read16<(KQ_BSLOT(0) * 2 + 0) * 1024>(b_lane + bslot);
+        B[0][1] = ds_read16<(KQ_BSLOT(0) * 2 + 1) * 1024>(b_lane + bslot);
+        B[1][0] = ds_read16<(KQ_BSLOT(1) * 2 + 0) * 1024>(b_lane + bslot);
+        B[1][1] = ds_read16<(KQ_BSLOT(1) * 2 + 1) * 1024>(b_lane + bslot);
+        float sv[4], asel[4];
 
         // 16 blocks of 16 x 16. Block b: two int8 MFMAs give the exact partials P' of group kt; a 4x4x1 f32 MFMA
         // (16 outer products of 4 rows x 4 columns) gives k = a_s * s in the same lane layout (lane = column
@@ -336,6 +490,40 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
         // issued after the MFMAs of block b + 1.
         auto mfmas = [&](int blk, v4i& c, v4f& k) {
             const int mi = blk >> 2, ni = blk & 3;
+            // wait for this block's operands (reads return in order): 11 (10) reads issued at the start of the
+            // step; each later operand pair is issued two blocks before its first use
+            if (blk == 0) {
+                lgkm_wait<2>(svr[0], svr[1], svr[2], svr[3], asr, A[0][0], A[0][1], B[0][0], B[0][1]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    sv[i] = SH ? __half2float(__ushort_as_half(static_cast<unsigned short>(svr[i]))) : __uint_as_float(svr[i]);
+                    asel[i] = __int_as_float(asr[i]);
+                }
+                B[2][0] = ds_read16<(KQ_BSLOT(2) * 2 + 0) * 1024>(b_lane + bslot);
+                B[2][1] = ds_read16<(KQ_BSLOT(2) * 2 + 1) * 1024>(b_lane + bslot);
+            }
+            if (blk == 1) {
+                lgkm_wait<2>(B[1][0], B[1][1]);
+                B[3][0] = ds_read16<(KQ_BSLOT(3) * 2 + 0) * 1024>(b_lane + bslot);
+                B[3][1] = ds_read16<(KQ_BSLOT(3) * 2 + 1) * 1024>(b_lane + bslot);
+            }
+            if (blk == 2) {
+                lgkm_wait<2>(B[2][0], B[2][1]);
+                A[1][0] = ds_read16<16 * kBK>(a_lane0 + aslot);
+                A[1][1] = ds_read16<16 * kBK>(a_lane1 + aslot);
+            }
+            if (blk == 3) lgkm_wait<2>(B[3][0], B[3][1]);
+            if (blk == 4) {
+                lgkm_wait<0>(A[1][0], A[1][1]);
+                A[2][0] = ds_read16<32 * kBK>(a_lane0 + aslot);
+                A[2][1] = ds_read16<32 * kBK>(a_lane1 + aslot);
+            }
+            if (blk == 8) {
+                lgkm_wait<0>(A[2][0], A[2][1]);
+                A[3][0] = ds_read16<48 * kBK>(a_lane0 + aslot);
+                A[3][1] = ds_read16<48 * kBK>(a_lane1 + aslot);
+            }
+            if (blk == 12) lgkm_wait<0>(A[3][0], A[3][1]);
             c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi][0], B[ni][0], zero, 0, 0, 0);
             c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi][1], B[ni][1], c, 0, 0, 0);
             if constexpr (QM != QUANT_STATIC) k = __builtin_amdgcn_mfma_f32_4x4x1f32(asel[mi], sv[ni], zerof, 0, 0, 0);
@@ -356,17 +544,25 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
         };
         v4i cp, cn;
         v4f kp = zerof, kn4 = zerof;
+        Raw raw;
         mfmas(0, cp, kp);
 #pragma unroll
         for (int blk = 1; blk <= 16; ++blk) {
             if (blk < 16) mfmas(blk, cn, kn4);
+            if (blk == 1 || blk == 3 || blk == 5 || blk == 7) issue_a(ka, s2, blk >> 1);
+            if (blk == 9) issue_raw(kb, s0);
+            if (blk == 11) issue_meta(ka, s2, kb, s0);
+            // step kt + 1's packed tiles (copied during step kt - 2) into B slot (kt + 1) % 2, read once every
+            // operand read of this step has returned (block 12) (after the last step: stale tiles into a slot
+            // nobody reads)
+            if (blk == 13) raw = unpack_read(s1, s1);
+            if (blk == 15) unpack_write(raw, (kt + 1) & 1);
             epilogue(cp, kp, blk - 1);
             cp = cn;
             kp = kn4;
         }
         if constexpr (!DBG) {
             // one block: 3 MFMAs (2 with static activations), then the 8 VALU of the previous block's epilogue
-            __builtin_amdgcn_sched_group_barrier(0x100, 20, 0);
 #pragma unroll
             for (int blk = 0; blk < 16; ++blk) {
                 __builtin_amdgcn_sched_group_barrier(0x008, QM == QUANT_STATIC ? 2 : 3, 0);
@@ -374,12 +570,13 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        stage_b(nxt, stage ^ 1);
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni) sv[ni] = scale_of(nxt.s[ni]);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        s2 = s0;
+        s0 = s1;
+        // all LDS traffic of the loop is explicit: the wait covers it, so a bare barrier (no fence) suffices
+        __builtin_amdgcn_s_waitcnt(kStepWait);
+        __builtin_amdgcn_s_barrier();
     }
+#undef KQ_BSLOT
 
     // store
 #pragma unroll
@@ -429,8 +626,8 @@ __global__ __launch_bounds__(256) void transpose_stats_kernel(const float* s_t, 
     const int id = blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= M * groups) return;
     const int m = id / groups, b = id % groups;
-    if (s) s[id] = s_t[b * M_p + m];
-    if (q) q[id] = q_t[b * M_p + m];
+    if (s) s[id] = s_t[b * M_p + scale_slot(m)];
+    if (q) q[id] = q_t[b * M_p + scale_slot(m)];
     if (z) z[id] = 0;
 }
 

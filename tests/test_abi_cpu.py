@@ -32,6 +32,17 @@ def test_exports_every_declared_symbol(native):
     assert lib.kq_version() >= 1
 
 
+def test_library_resolves_every_symbol_at_load(native):
+    """The library binds with RTLD_NOW (a kernel whose launch stub the host pass dropped shows up here as an
+    undefined symbol, not as a lazy-binding failure on the GPU box)."""
+    import subprocess
+    import sys
+
+    code = f"import ctypes, os; ctypes.CDLL({native.LIB_PATH!r}, mode=os.RTLD_NOW)"
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+
+
 def test_select_path_matches_oracle(native, ref):
     lib = native.load()
     for bits in (2, 4, 8):
