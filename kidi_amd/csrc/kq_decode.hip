@@ -1,17 +1,19 @@
-// Decode projection of the MI355X quantized linear layer for M <= 4 rows and K a multiple of 512: one launch per
+// Decode projection of the MI355X quantized linear layer for M <= 8 rows and K a multiple of 512: one launch per
 // call, activation quantization fused in, every shape parameter that the inner loop touches fixed at compile time.
 //
-// Grid: one workgroup per pair of row tiles (16 output rows each; with GELU gating a gate tile and its up tile,
-// Kidi's gate_up_proj row order, model/gemma4.cpp:308-316). Block: W = K/512 waves; wave w owns columns
+// Grid: one workgroup per run of consecutive pairs of row tiles (16 output rows each; with GELU gating a gate tile
+// and its up tile, Kidi's gate_up_proj row order, model/gemma4.cpp:308-316): one pair for projections up to ~1024
+// pairs, more for large ones (the N = 262,144 output head), so a workgroup's activation quantization serves more
+// weight tiles. Block: W = K/512 waves; wave w owns columns
 // [512 w, 512 w + 512) of both row tiles, i.e. NT = 512/KT weight tiles per row tile. A wave
 //   1. loads its activation pieces (8 columns per lane and row), the group metadata its epilogue lanes need, and
 //      its 2 x NT weight tiles (one 16-byte load per tile per lane), all up front into registers;
 //   2. quantizes its columns of the M rows into its LDS region (codes in the tiles' permuted order, per-group
 //      scale, code sum, zero point), with the arithmetic of kq_device.hpp;
-//   3. runs one v_mfma_i32_16x16x64_i8 per 64-column block and row tile. A row nn of the MFMA is activation row
-//      m = nn & 3 restricted to the groups whose index is nn >> 2 (mod 4), so the accumulator of lane (n, L)
-//      collects, in register i, the exact int32 partial of group slot L and row i; one epilogue per four groups
-//      folds them into fp32;
+//   3. runs one v_mfma_i32_16x16x64_i8 per 64-column block, row tile and group of 4 rows. A row nn of the MFMA is
+//      activation row 4 h + (nn & 3) restricted to the groups whose index is nn >> 2 (mod 4), so the accumulator of
+//      lane (n, L) collects, in register i, the exact int32 partial of group slot L and row 4 h + i; one epilogue
+//      per four groups folds them into fp32;
 //   4. sums its four group slots across lanes and hands 16 x M sums per row tile to the cross-wave reduction.
 //
 // Numerics: BlockwiseLinear / SymmetricPackedLinear closed forms (runtime/ynn/operators.cpp:1118-1169,
@@ -22,6 +24,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 
 #include "kq_device.hpp"
 #include "kq_internal.hpp"
@@ -33,7 +36,7 @@ using namespace dev;
 
 constexpr std::uint32_t kOob = 0x80000000u;  // buffer offset past every resource: the load returns zeros
 constexpr int kRsrcWord3 = 0x00020000;       // raw (unformatted) buffer resource, gfx9-family word 3
-constexpr int kMaxRows = 4;
+constexpr int kMaxRows = 8;  // rows of the widest variant (MR = 8: two MFMA row halves)
 
 struct DecodeArgs {
     const void* x;  // activations [M][K]
@@ -47,6 +50,7 @@ struct DecodeArgs {
     std::int32_t* dq_sums;
     std::int32_t* dq_zeros;
     int M, K, N, k_tiles, n_tiles, groups_p, groups;
+    int pairs, total_pairs;  // row-tile pairs per workgroup (consecutive), pairs in the projection
     int x_f32, scale_half, aux_half;
     float input_scale, output_scale;
 };
@@ -82,15 +86,18 @@ __device__ __forceinline__ v4i block_codes(const uint4 w) {
     return v4i{o[0], o[1], o[2], o[3]};
 }
 
-template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG>
-__global__ __launch_bounds__(1024) void decode_kernel(DecodeArgs a) {
+// MR: rows of the variant (4 or 8); WMAX: most waves per workgroup (4 for K <= 2048, 16 up to K = 8192), which
+// sets the register budget (512 / (WMAX / 4) VGPRs per lane)
+template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, int MR, int WMAX>
+__global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
+    constexpr int H = MR / 4;            // MFMA row halves: rows 4 h .. 4 h + 3
     constexpr int KT = 512 / BITS;       // columns per weight tile
     constexpr int J = KT / 64;           // 64-column blocks per tile
     constexpr int NT = 512 / KT;         // tiles per wave and row tile
     constexpr int NG = 512 / G;          // groups per wave
     constexpr int NQ = NG / 4;           // quads of groups per wave
     constexpr int LGC = G == 32 ? 2 : (G == 64 ? 3 : 4);  // log2 of 8-column pieces per group
-    constexpr int WAVE_BYTES = kMaxRows * 512 + 3 * 4 * kMaxRows * NG + 16;
+    constexpr int WAVE_BYTES = MR * 512 + 3 * 4 * MR * NG + 16;
     static_assert(G == 32 || G == 64 || G == 128, "group size");
     extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
 
@@ -98,33 +105,39 @@ __global__ __launch_bounds__(1024) void decode_kernel(DecodeArgs a) {
     const int W = blockDim.x >> 6;
     const int nn = lane & 15, L = lane >> 4;
     const int M = a.M;
-    const int am = nn & 3, aslot = nn >> 2;  // A-operand row of this lane: activation row, group slot
+    const int aslot = nn >> 2;  // A-operand row of this lane: activation row (nn & 3) + 4 h, group slot
 
-    int nts[2];
-    if constexpr (GELU) {
-        nts[0] = blockIdx.x;
-        nts[1] = blockIdx.x + (a.n_tiles >> 1);
-    } else {
-        nts[0] = 2 * blockIdx.x;
-        nts[1] = 2 * blockIdx.x + 1;
-    }
-    const bool live1 = nts[1] < a.n_tiles;
-    const int nt1 = live1 ? nts[1] : nts[0];
+    // row tiles of a pair: plain 2 p, 2 p + 1; GELU the gate tile p and its up tile p + n_tiles / 2
+    int nts[2] = {0, 0};
+    bool live1 = false;
+    auto set_pair = [&](int pair) {
+        if constexpr (GELU) {
+            nts[0] = pair;
+            nts[1] = pair + (a.n_tiles >> 1);
+        } else {
+            nts[0] = 2 * pair;
+            nts[1] = 2 * pair + 1;
+        }
+        live1 = nts[1] < a.n_tiles;
+    };
+    const int pair0 = blockIdx.x * a.pairs;
+    const int pend = min(pair0 + a.pairs, a.total_pairs);
+    set_pair(pair0);
 
     std::uint8_t* wl = lds + wave * WAVE_BYTES;
     std::int8_t* codes = reinterpret_cast<std::int8_t*>(wl);                     // [M][512]
-    float* st_s = reinterpret_cast<float*>(wl + kMaxRows * 512);                  // [M][NG]
-    int* st_q = reinterpret_cast<int*>(st_s + kMaxRows * NG);
-    int* st_z = st_q + kMaxRows * NG;
+    float* st_s = reinterpret_cast<float*>(wl + MR * 512);                        // [M][NG]
+    int* st_q = reinterpret_cast<int*>(st_s + MR * NG);
+    int* st_z = st_q + MR * NG;
     const int zero_slot = WAVE_BYTES - 16;
     if (lane == 0) *reinterpret_cast<uint4*>(wl + zero_slot) = make_uint4(0, 0, 0, 0);
 
     // ---- 1. loads: activations, metadata, weights (in this order) ----
     const __amdgpu_buffer_rsrc_t xres = rsrc(a.x, static_cast<std::uint32_t>(M * a.K * (a.x_f32 ? 4 : 2)));
     const int kb = wave * 512;  // first column of this wave
-    uint4 xr[kMaxRows][2];
+    uint4 xr[MR][2];
 #pragma unroll
-    for (int m = 0; m < kMaxRows; ++m) {
+    for (int m = 0; m < MR; ++m) {
         if (m < M) {
             const std::uint32_t e = static_cast<std::uint32_t>(m * a.K + kb + 8 * lane);
             const std::uint32_t off = a.x_f32 ? 4 * e : 2 * e;
@@ -132,44 +145,47 @@ __global__ __launch_bounds__(1024) void decode_kernel(DecodeArgs a) {
             xr[m][1] = ld16(xres, a.x_f32 ? off + 16 : off);
         }
     }
-    // metadata entry of quad q for this lane: group 4q + L of the wave, row nn
+    // metadata entry of quad q for this lane: group 4q + L of the wave, row nn; one 16-byte slot per weight tile
     const std::uint32_t meta_n = static_cast<std::uint32_t>(a.n_tiles * a.groups_p * kTileRows);
     const __amdgpu_buffer_rsrc_t sres = rsrc(a.scales, meta_n * (a.scale_half ? 2 : 4));
     std::uint32_t s_raw[2][NQ], x_raw[2][NQ];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int nt = r == 0 ? nts[0] : nt1;
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-            const std::uint32_t mi = static_cast<std::uint32_t>((nt * a.groups_p + wave * NG + 4 * q + L) * kTileRows + nn);
-            s_raw[r][q] = a.scale_half ? __builtin_amdgcn_raw_buffer_load_b16(sres, 2 * mi, 0, 0)
-                                       : __builtin_amdgcn_raw_buffer_load_b32(sres, 4 * mi, 0, 0);
-            x_raw[r][q] = 0;
-            if constexpr (BITS == 8 && QM == QUANT_DYN_ASYM)
-                x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b32(rsrc(a.aux, meta_n * 4), 4 * mi, 0, 0);
-            if constexpr (BITS != 8 && ZM == ZERO_POINT)
-                x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b8(rsrc(a.aux, meta_n / 2), (mi - nn) / 2 + nn / 2, 0, 0);
-            if constexpr (BITS != 8 && ZM == ZERO_FLOAT)
-                x_raw[r][q] = a.aux_half ? __builtin_amdgcn_raw_buffer_load_b16(rsrc(a.aux, meta_n * 2), 2 * mi, 0, 0)
-                                         : __builtin_amdgcn_raw_buffer_load_b32(rsrc(a.aux, meta_n * 4), 4 * mi, 0, 0);
-        }
-    }
-    const __amdgpu_buffer_rsrc_t w0 = rsrc(a.tiles + static_cast<std::int64_t>(nts[0]) * a.k_tiles * kTileBytes,
-                                           static_cast<std::uint32_t>(a.k_tiles * kTileBytes));
-    const __amdgpu_buffer_rsrc_t w1 = rsrc(a.tiles + static_cast<std::int64_t>(nt1) * a.k_tiles * kTileBytes,
-                                           static_cast<std::uint32_t>(a.k_tiles * kTileBytes));
     uint4 wv[2][NT];
+    auto load_pair = [&]() {
 #pragma unroll
-    for (int u = 0; u < NT; ++u) {
-        const std::uint32_t off = static_cast<std::uint32_t>((wave * NT + u) * kTileBytes + 16 * lane);
-        wv[0][u] = ld16(w0, off);
-        wv[1][u] = ld16(w1, off);
-    }
+        for (int r = 0; r < 2; ++r) {
+            const int nt = (r == 0 || !live1) ? nts[0] : nts[1];
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const std::uint32_t mi = static_cast<std::uint32_t>((nt * a.groups_p + wave * NG + 4 * q + L) * kTileRows + nn);
+                s_raw[r][q] = a.scale_half ? __builtin_amdgcn_raw_buffer_load_b16(sres, 2 * mi, 0, 0)
+                                           : __builtin_amdgcn_raw_buffer_load_b32(sres, 4 * mi, 0, 0);
+                x_raw[r][q] = 0;
+                if constexpr (BITS == 8 && QM == QUANT_DYN_ASYM)
+                    x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b32(rsrc(a.aux, meta_n * 4), 4 * mi, 0, 0);
+                if constexpr (BITS != 8 && ZM == ZERO_POINT)
+                    x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b8(rsrc(a.aux, meta_n / 2), (mi - nn) / 2 + nn / 2, 0, 0);
+                if constexpr (BITS != 8 && ZM == ZERO_FLOAT)
+                    x_raw[r][q] = a.aux_half ? __builtin_amdgcn_raw_buffer_load_b16(rsrc(a.aux, meta_n * 2), 2 * mi, 0, 0)
+                                             : __builtin_amdgcn_raw_buffer_load_b32(rsrc(a.aux, meta_n * 4), 4 * mi, 0, 0);
+            }
+        }
+        const __amdgpu_buffer_rsrc_t w0 = rsrc(a.tiles + static_cast<std::int64_t>(nts[0]) * a.k_tiles * kTileBytes,
+                                               static_cast<std::uint32_t>(a.k_tiles * kTileBytes));
+        const __amdgpu_buffer_rsrc_t w1 = rsrc(a.tiles + static_cast<std::int64_t>(live1 ? nts[1] : nts[0]) * a.k_tiles * kTileBytes,
+                                               static_cast<std::uint32_t>(a.k_tiles * kTileBytes));
+#pragma unroll
+        for (int u = 0; u < NT; ++u) {
+            const std::uint32_t off = static_cast<std::uint32_t>((wave * NT + u) * kTileBytes + 16 * lane);
+            wv[0][u] = ld16(w0, off);
+            wv[1][u] = ld16(w1, off);
+        }
+    };
+    load_pair();
 
     // ---- 2. quantize this wave's 512 columns of each row: lane = 8-column piece, 2^LGC lanes = one group ----
     const bool dump_block = DBG && blockIdx.x == 0;
 #pragma unroll
-    for (int m = 0; m < kMaxRows; ++m) {
+    for (int m = 0; m < MR; ++m) {
         if (m < M) {
             float v[8];
             if (a.x_f32) {
@@ -224,17 +240,22 @@ __global__ __launch_bounds__(1024) void decode_kernel(DecodeArgs a) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- 3. MFMA over the wave's blocks, one epilogue per quad of groups ----
-    float acc[2][4];
-    v4i C[2];
+    // ---- 3-4 per pair of row tiles: MFMA with one epilogue per quad of groups, then the reductions ----
+    float* red = reinterpret_cast<float*>(lds + W * WAVE_BYTES);  // [W][2][MR][16]
+    for (int pair = pair0; pair < pend; ++pair) {
+    if (pair != pair0) {  // the first pair's loads went out before the quantization
+        set_pair(pair);
+        load_pair();
+    }
+    float acc[2][MR];
+    v4i C[2][H];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-        C[r] = v4i{0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[r][i] = 0.F;
+        for (int h = 0; h < H; ++h) C[r][h] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < MR; ++i) acc[r][i] = 0.F;
     }
-    const int abase = am * 512 + 16 * L;
-    const bool arow = am < M;
 
     auto flush = [&](int q) {
         const int gi = 4 * q + L;  // this lane's group (of the wave) and the stats slot of row i
@@ -248,15 +269,16 @@ __global__ __launch_bounds__(1024) void decode_kernel(DecodeArgs a) {
                 x2 = __float_as_int(a.aux_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(x_raw[r][q]))) : __uint_as_float(x_raw[r][q]));
             const int n = (r == 0 ? nts[0] : nts[1]) * kTileRows + nn;
 #pragma unroll
-            for (int i = 0; i < kMaxRows; ++i) {
+            for (int i = 0; i < MR; ++i) {
                 if (i < M) {
                     const int sl = i * NG + gi;
+                    const int Ci = C[r][i >> 2][i & 3];
                     int Pp;
                     if constexpr (BITS == 8) {
-                        Pp = QM == QUANT_STATIC ? C[r][i] : C[r][i] - st_z[sl] * x2;
+                        Pp = QM == QUANT_STATIC ? Ci : Ci - st_z[sl] * x2;
                     } else {
                         const int zw = ZM == ZERO_POINT ? x2 : sign_offset(BITS);
-                        Pp = C[r][i] - zw * st_q[sl];
+                        Pp = Ci - zw * st_q[sl];
                     }
                     if (DBG && a.dump && n < a.N && (r == 0 || live1))
                         a.dump[(static_cast<std::int64_t>(i) * a.N + n) * a.groups + wave * NG + gi] = Pp;
@@ -265,7 +287,8 @@ __global__ __launch_bounds__(1024) void decode_kernel(DecodeArgs a) {
                     acc[r][i] = QM == QUANT_STATIC ? acc[r][i] + t : acc[r][i] + st_s[sl] * t;
                 }
             }
-            C[r] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int h = 0; h < H; ++h) C[r][h] = v4i{0, 0, 0, 0};
         }
     };
 
@@ -276,43 +299,50 @@ __global__ __launch_bounds__(1024) void decode_kernel(DecodeArgs a) {
             constexpr int dummy = 0;
             (void)dummy;
             const int c = u * KT + 64 * j;  // wave-local first column of the block
-            v4i A;
-            if constexpr (G == 32) {
-                // two groups per block: bytes 0-7 of a lane's 16 belong to group c/32, bytes 8-15 to c/32 + 1
-                const int s0 = (c >> 5) & 3, s1 = ((c >> 5) + 1) & 3;
-                const int o0 = (arow && aslot == s0) ? abase + act_position(c) : zero_slot;
-                const int o1 = (arow && aslot == s1) ? abase + act_position(c) + 8 : zero_slot;
-                const uint2 lo = *reinterpret_cast<const uint2*>(wl + o0);
-                const uint2 hi = *reinterpret_cast<const uint2*>(wl + o1);
-                A = v4i{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(hi.x), static_cast<int>(hi.y)};
-            } else {
-                const int sg = (c / G) & 3;
-                A = *reinterpret_cast<const v4i*>(wl + ((arow && aslot == sg) ? abase + act_position(c) : zero_slot));
-            }
+            v4i B[2];
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
-                v4i B;
-                if (j == 0) B = block_codes<BITS, 0>(wv[r][u]);
-                else if (j == 1) B = block_codes<BITS, (J > 1 ? 1 : 0)>(wv[r][u]);
-                else if (j == 2) B = block_codes<BITS, (J > 2 ? 2 : 0)>(wv[r][u]);
-                else B = block_codes<BITS, (J > 3 ? 3 : 0)>(wv[r][u]);
-                C[r] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, C[r], 0, 0, 0);
+                if (j == 0) B[r] = block_codes<BITS, 0>(wv[r][u]);
+                else if (j == 1) B[r] = block_codes<BITS, (J > 1 ? 1 : 0)>(wv[r][u]);
+                else if (j == 2) B[r] = block_codes<BITS, (J > 2 ? 2 : 0)>(wv[r][u]);
+                else B[r] = block_codes<BITS, (J > 3 ? 3 : 0)>(wv[r][u]);
+            }
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+                const int am = (nn & 3) + 4 * h;
+                const int abase = am * 512 + 16 * L;
+                const bool arow = am < M;
+                v4i A;
+                if constexpr (G == 32) {
+                    // two groups per block: bytes 0-7 of a lane's 16 belong to group c/32, bytes 8-15 to c/32 + 1
+                    const int s0 = (c >> 5) & 3, s1 = ((c >> 5) + 1) & 3;
+                    const int o0 = (arow && aslot == s0) ? abase + act_position(c) : zero_slot;
+                    const int o1 = (arow && aslot == s1) ? abase + act_position(c) + 8 : zero_slot;
+                    const uint2 lo = *reinterpret_cast<const uint2*>(wl + o0);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(wl + o1);
+                    A = v4i{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(hi.x), static_cast<int>(hi.y)};
+                } else {
+                    const int sg = (c / G) & 3;
+                    A = *reinterpret_cast<const v4i*>(wl + ((arow && aslot == sg) ? abase + act_position(c) : zero_slot));
+                }
+#pragma unroll
+                for (int r = 0; r < 2; ++r) C[r][h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[r], C[r][h], 0, 0, 0);
             }
             if (((c + 64) % (4 * G)) == 0) flush((c + 64) / (4 * G) - 1);
         }
     }
 
-    // ---- 4. sum the four group slots (lanes nn + 16 L) and the waves ----
-    float* red = reinterpret_cast<float*>(lds + W * WAVE_BYTES);  // [W][2][M][16]
+    const int cur_nt0 = nts[0], cur_nt1 = nts[1];
+    // sum the four group slots (lanes nn + 16 L) and the waves
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
 #pragma unroll
-        for (int i = 0; i < kMaxRows; ++i) {
+        for (int i = 0; i < MR; ++i) {
             if (i < M) {
                 float v = acc[r][i];
                 v = v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));  // xor 16
                 v = v + __shfl_xor(v, 32);
-                if (L == 0) red[((wave * 2 + r) * kMaxRows + i) * 16 + nn] = v;
+                if (L == 0) red[((wave * 2 + r) * MR + i) * 16 + nn] = v;
             }
         }
     }
@@ -323,25 +353,34 @@ __global__ __launch_bounds__(1024) void decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int h = 0; h < (GELU ? 2 : 1); ++h) {
             const int rr = GELU ? h : r;
-            for (int w = 0; w < W; ++w) v[h] = v[h] + red[((w * 2 + rr) * kMaxRows + i) * 16 + c];
+            for (int w = 0; w < W; ++w) v[h] = v[h] + red[((w * 2 + rr) * MR + i) * 16 + c];
             if (QM == QUANT_STATIC) v[h] = v[h] * a.input_scale;
             v[h] = calibrate_output(v[h], a.output_scale);
         }
         if constexpr (GELU) {
             const int half_n = a.N >> 1;
-            const int n = nts[0] * kTileRows + c;
+            const int n = cur_nt0 * kTileRows + c;
             if (n < half_n) a.y[static_cast<std::int64_t>(i) * half_n + n] = gelu_tanh(v[0]) * v[1];
         } else {
-            const int nt = nts[r];
+            const int nt = r == 0 ? cur_nt0 : cur_nt1;
             const int n = nt * kTileRows + c;
             if (nt < a.n_tiles && n < a.N) a.y[static_cast<std::int64_t>(i) * a.N + n] = v[0];
         }
+    }
+    __syncthreads();  // the reduction buffer is reused by the next pair
     }
 }
 
 template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG>
 hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds, hipStream_t stream) {
-    hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG>), grid, block, lds, stream, a);
+    const bool wide = block.x > 256 || DBG;  // debug variants: one register budget for every K
+    if (a.M <= 4) {
+        if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, 16>), grid, block, lds, stream, a);
+        else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, (DBG ? 16 : 4)>), grid, block, lds, stream, a);
+    } else {
+        if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 8, 16>), grid, block, lds, stream, a);
+        else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 8, (DBG ? 16 : 4)>), grid, block, lds, stream, a);
+    }
     return hipGetLastError();
 }
 
@@ -359,7 +398,7 @@ hipError_t launch_modes(const DecodeArgs& a, int g, bool gelu, bool dbg, dim3 gr
 #undef KQ_DEC
 }
 
-int wave_bytes(int g) { return kMaxRows * 512 + 3 * 4 * kMaxRows * (512 / g) + 16; }
+int wave_bytes(int g, int mr) { return mr * 512 + 3 * 4 * mr * (512 / g) + 16; }
 
 }  // namespace
 
@@ -404,9 +443,18 @@ hipError_t launch_decode(const LinearCall& c, hipStream_t stream) {
     a.input_scale = c.input_scale;
     a.output_scale = c.output_scale;
     const int W = static_cast<int>(w.geo.cols / 512);
-    const int blocks = static_cast<int>(c.gelu_gate ? w.geo.n_tiles / 2 : (w.geo.n_tiles + 1) / 2);
+    a.total_pairs = static_cast<int>(c.gelu_gate ? w.geo.n_tiles / 2 : (w.geo.n_tiles + 1) / 2);
+    // several pairs per workgroup once the grid passes ~2 workgroups per CU: the activation quantization and the
+    // launch of a workgroup are then shared by more weight tiles
+    static const int forced_pairs = [] {
+        const char* e = std::getenv("KQ_DECODE_PAIRS");  // tuning override
+        return e ? std::atoi(e) : 0;
+    }();
+    a.pairs = forced_pairs > 0 ? forced_pairs : std::max(1, a.total_pairs / 512);
+    const int blocks = (a.total_pairs + a.pairs - 1) / a.pairs;
     const dim3 grid(static_cast<unsigned>(blocks)), block(64 * W);
-    const std::size_t lds = static_cast<std::size_t>(W * wave_bytes(w.geo.group) + W * 2 * kMaxRows * 16 * 4);
+    const int mr = c.M <= 4 ? 4 : 8;
+    const std::size_t lds = static_cast<std::size_t>(W * wave_bytes(w.geo.group, mr) + W * 2 * mr * 16 * 4);
     const bool dbg = c.dump || c.dq_codes || c.dq_scales || c.dq_sums || c.dq_zeros;
     const bool stat = c.path == PATH_SYMMETRIC;
     const int g = w.geo.group;

@@ -76,6 +76,12 @@ CASES = [
     (2, 128, 6, 512, 128, None, 0.05, True, 0.0),
     (4, 32, 2, 256, 256, None, 0.05, False, 0.0),
     (8, 64, 1, 256, 128, None, 0.03, False, 0.0),
+    # decode kernel, 5..8 rows (two MFMA row halves)
+    (8, 32, 8, 2048, 256, None, 0.0, False, 0.001),
+    (4, 128, 6, 1024, 272, "zp", 0.0, True, 0.001),
+    (4, 32, 5, 512, 256, None, 0.0, False, 0.0),
+    (2, 32, 7, 512, 128, None, 0.05, False, 0.0),
+    (8, 64, 8, 512, 64, None, 0.03, False, 0.0),
     # prefill GEMM shapes (M > 8, ragged M and N)
     (4, 128, 130, 512, 272, "zp", 0.0, True, 0.001),
     (4, 32, 129, 256, 256, None, 0.0, False, 0.0),
@@ -263,7 +269,7 @@ def test_zero_block_and_empty(dev, ref):
     assert tuple(empty.shape) == (0, 256)
 
 
-@pytest.mark.parametrize("M,I", [(1, 256), (4, 256), (16, 256), (200, 256), (300, 272)])
+@pytest.mark.parametrize("M,I", [(1, 256), (4, 256), (8, 256), (16, 256), (200, 256), (300, 272)])
 def test_gelu_gate_fused(dev, ref, M, I):
     """gate/up projection + GELU-tanh in one pass equals the oracle's projection followed by gelu_gate."""
     rng = np.random.default_rng(M)
