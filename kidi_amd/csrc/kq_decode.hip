@@ -91,6 +91,7 @@ __device__ __forceinline__ v4i block_codes(const uint4 w) {
 template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, int MR, int WMAX>
 __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     constexpr int H = MR / 4;            // MFMA row halves: rows 4 h .. 4 h + 3
+    constexpr int RT = (WMAX > 4 && !GELU) ? 1 : 2;  // row tiles per unit: one when K > 2048 (more workgroups)
     constexpr int KT = 512 / BITS;       // columns per weight tile
     constexpr int J = KT / 64;           // 64-column blocks per tile
     constexpr int NT = 512 / KT;         // tiles per wave and row tile
@@ -107,13 +108,17 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     const int M = a.M;
     const int aslot = nn >> 2;  // A-operand row of this lane: activation row (nn & 3) + 4 h, group slot
 
-    // row tiles of a pair: plain 2 p, 2 p + 1; GELU the gate tile p and its up tile p + n_tiles / 2
+    // row tiles of a unit: plain 2 p, 2 p + 1 (or the single tile p when RT = 1); GELU the gate tile p and its up
+    // tile p + n_tiles / 2
     int nts[2] = {0, 0};
     bool live1 = false;
     auto set_pair = [&](int pair) {
         if constexpr (GELU) {
             nts[0] = pair;
             nts[1] = pair + (a.n_tiles >> 1);
+        } else if constexpr (RT == 1) {
+            nts[0] = pair;
+            nts[1] = a.n_tiles;
         } else {
             nts[0] = 2 * pair;
             nts[1] = 2 * pair + 1;
@@ -148,11 +153,11 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     // metadata entry of quad q for this lane: group 4q + L of the wave, row nn; one 16-byte slot per weight tile
     const std::uint32_t meta_n = static_cast<std::uint32_t>(a.n_tiles * a.groups_p * kTileRows);
     const __amdgpu_buffer_rsrc_t sres = rsrc(a.scales, meta_n * (a.scale_half ? 2 : 4));
-    std::uint32_t s_raw[2][NQ], x_raw[2][NQ];
-    uint4 wv[2][NT];
+    std::uint32_t s_raw[RT][NQ], x_raw[RT][NQ];
+    uint4 wv[RT][NT];
     auto load_pair = [&]() {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < RT; ++r) {
             const int nt = (r == 0 || !live1) ? nts[0] : nts[1];
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
@@ -177,7 +182,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
         for (int u = 0; u < NT; ++u) {
             const std::uint32_t off = static_cast<std::uint32_t>((wave * NT + u) * kTileBytes + 16 * lane);
             wv[0][u] = ld16(w0, off);
-            wv[1][u] = ld16(w1, off);
+            if constexpr (RT == 2) wv[RT - 1][u] = ld16(w1, off);
         }
     };
     load_pair();
@@ -241,16 +246,16 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // ---- 3-4 per pair of row tiles: MFMA with one epilogue per quad of groups, then the reductions ----
-    float* red = reinterpret_cast<float*>(lds + W * WAVE_BYTES);  // [W][2][MR][16]
+    float* red = reinterpret_cast<float*>(lds + W * WAVE_BYTES);  // [W][RT][MR][16]
     for (int pair = pair0; pair < pend; ++pair) {
     if (pair != pair0) {  // the first pair's loads went out before the quantization
         set_pair(pair);
         load_pair();
     }
-    float acc[2][MR];
-    v4i C[2][H];
+    float acc[RT][MR];
+    v4i C[RT][H];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < RT; ++r) {
 #pragma unroll
         for (int h = 0; h < H; ++h) C[r][h] = v4i{0, 0, 0, 0};
 #pragma unroll
@@ -260,7 +265,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     auto flush = [&](int q) {
         const int gi = 4 * q + L;  // this lane's group (of the wave) and the stats slot of row i
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < RT; ++r) {
             const float s = a.scale_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(s_raw[r][q]))) : __uint_as_float(s_raw[r][q]);
             int x2 = 0;
             if constexpr (BITS == 8 && QM == QUANT_DYN_ASYM) x2 = static_cast<int>(x_raw[r][q]);
@@ -299,9 +304,9 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
             constexpr int dummy = 0;
             (void)dummy;
             const int c = u * KT + 64 * j;  // wave-local first column of the block
-            v4i B[2];
+            v4i B[RT];
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
+            for (int r = 0; r < RT; ++r) {
                 if (j == 0) B[r] = block_codes<BITS, 0>(wv[r][u]);
                 else if (j == 1) B[r] = block_codes<BITS, (J > 1 ? 1 : 0)>(wv[r][u]);
                 else if (j == 2) B[r] = block_codes<BITS, (J > 2 ? 2 : 0)>(wv[r][u]);
@@ -326,7 +331,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
                     A = *reinterpret_cast<const v4i*>(wl + ((arow && aslot == sg) ? abase + act_position(c) : zero_slot));
                 }
 #pragma unroll
-                for (int r = 0; r < 2; ++r) C[r][h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[r], C[r][h], 0, 0, 0);
+                for (int r = 0; r < RT; ++r) C[r][h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[r], C[r][h], 0, 0, 0);
             }
             if (((c + 64) % (4 * G)) == 0) flush((c + 64) / (4 * G) - 1);
         }
@@ -335,25 +340,25 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     const int cur_nt0 = nts[0], cur_nt1 = nts[1];
     // sum the four group slots (lanes nn + 16 L) and the waves
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < RT; ++r) {
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
             if (i < M) {
                 float v = acc[r][i];
                 v = v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));  // xor 16
                 v = v + __shfl_xor(v, 32);
-                if (L == 0) red[((wave * 2 + r) * MR + i) * 16 + nn] = v;
+                if (L == 0) red[((wave * RT + r) * MR + i) * 16 + nn] = v;
             }
         }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < (GELU ? 1 : 2) * M * 16; idx += blockDim.x) {
+    for (int idx = threadIdx.x; idx < (GELU ? 1 : RT) * M * 16; idx += blockDim.x) {
         const int r = idx / (M * 16), i = (idx / 16) % M, c = idx % 16;
         float v[2] = {0.F, 0.F};
 #pragma unroll
         for (int h = 0; h < (GELU ? 2 : 1); ++h) {
             const int rr = GELU ? h : r;
-            for (int w = 0; w < W; ++w) v[h] = v[h] + red[((w * 2 + rr) * MR + i) * 16 + c];
+            for (int w = 0; w < W; ++w) v[h] = v[h] + red[((w * RT + rr) * MR + i) * 16 + c];
             if (QM == QUANT_STATIC) v[h] = v[h] * a.input_scale;
             v[h] = calibrate_output(v[h], a.output_scale);
         }
@@ -443,8 +448,12 @@ hipError_t launch_decode(const LinearCall& c, hipStream_t stream) {
     a.input_scale = c.input_scale;
     a.output_scale = c.output_scale;
     const int W = static_cast<int>(w.geo.cols / 512);
-    a.total_pairs = static_cast<int>(c.gelu_gate ? w.geo.n_tiles / 2 : (w.geo.n_tiles + 1) / 2);
-    // several pairs per workgroup once the grid passes ~2 workgroups per CU: the activation quantization and the
+    // units of one workgroup iteration: pairs of row tiles, or single row tiles for the variants with the wide
+    // register budget (K > 2048, i.e. more than 4 waves, and every debug variant) without gating
+    const bool dbg_any = c.dump || c.dq_codes || c.dq_scales || c.dq_sums || c.dq_zeros;
+    const bool single = (W > 4 || dbg_any) && !c.gelu_gate;
+    a.total_pairs = static_cast<int>(c.gelu_gate ? w.geo.n_tiles / 2 : (single ? w.geo.n_tiles : (w.geo.n_tiles + 1) / 2));
+    // several units per workgroup once the grid passes ~2 workgroups per CU: the activation quantization and the
     // launch of a workgroup are then shared by more weight tiles
     static const int forced_pairs = [] {
         const char* e = std::getenv("KQ_DECODE_PAIRS");  // tuning override
