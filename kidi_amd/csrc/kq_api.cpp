@@ -4,6 +4,7 @@
 // selection (runtime/ynn/operators.cpp:2739-2900) and its errors (core/error.h:8-14). No function throws.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -424,11 +425,30 @@ kq_status run_call(kq::LinearCall& c, const kq_linear_args* args, std::size_t ws
 
 namespace kq {
 
+namespace {
+// Partial tiles of a K-split prefill GEMM (kq_gemm.hip): the larger of the plans with and without GELU gating, 0
+// where that GEMM does not run or does not split.
+std::size_t split_bytes(const Weight& w, std::int64_t M) {
+    std::size_t partial = 0;
+    if (!w.tiled || w.geo.bits != 4 || w.geo.group != 128 || M <= 16 || w.geo.cols % 512 || w.geo.cols_p != w.geo.cols)
+        return 0;
+    for (int gelu = 0; gelu < 2; ++gelu) {
+        if (gelu && ((w.geo.rows / 2) % kTileRows || w.geo.n_tiles % 2)) continue;
+        const GemmPlan p = gemm_i4_plan(w, M, gelu != 0);
+        if (p.ksplit == 1) continue;
+        const std::size_t tiles = static_cast<std::size_t>(p.m_blocks) * p.n_blocks;
+        partial = std::max(partial, align_up(static_cast<std::size_t>(p.ksplit) * tiles * (128 * p.wm) * 64 * 4));
+    }
+    return partial;
+}
+}  // namespace
+
 std::size_t workspace_bytes(const Weight& w, std::int64_t M) {
     const std::int64_t rows = act_rows(w, M);
     const std::int64_t cols = w.tiled ? w.geo.cols_p : w.geo.cols;
     const std::int64_t groups = w.tiled ? w.geo.groups_p : w.geo.cols / w.geo.group;
-    return align_up(static_cast<std::size_t>(rows * cols)) + 3 * align_up(static_cast<std::size_t>(rows * groups) * 4);
+    return align_up(static_cast<std::size_t>(rows * cols)) + 3 * align_up(static_cast<std::size_t>(rows * groups) * 4) +
+           split_bytes(w, M);
 }
 
 ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base) {
@@ -444,6 +464,8 @@ ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base) {
     a.sum = reinterpret_cast<std::int32_t*>(p);
     p += align_up(static_cast<std::size_t>(a.rows_p * groups) * 4);
     a.zero = reinterpret_cast<std::int32_t*>(p);
+    p += align_up(static_cast<std::size_t>(a.rows_p * groups) * 4);
+    if (split_bytes(w, M)) a.partial = reinterpret_cast<float*>(p);
     return a;
 }
 

@@ -221,6 +221,8 @@ struct GemmArgs {
     int scale_half;
     float input_scale, output_scale;
     int m_blocks, n_blocks;
+    int ksplit;          // K ranges per output tile (1, 2, 4 or 8)
+    float* partial;      // ksplit > 1: fp32 partial tiles [ksplit][tiles][THREADS][64]
 };
 
 // Global row tile of LDS tile slot t (0..7) of column block nb, or n_tiles when out of range. GELU: slots 0-3 are
@@ -241,6 +243,46 @@ __device__ __forceinline__ constexpr int wave_slot(int wn, int ni) {
     return GELU ? (ni < 2 ? 2 * wn + ni : 4 + 2 * wn + ni - 2) : 4 * wn + ni;
 }
 
+// Epilogue of one output tile: acc[mi][ni][r] is row m0 + 64 wm + 16 mi + 4 L + r, column 16 col_nt[ni] + nn;
+// calibrated inputs scale by input_scale, calibrated outputs round to output_scale steps, GELU pairs gate and up.
+template <int WM, bool GELU, int QM>
+__device__ __forceinline__ void store_tile(const GemmArgs& a, const float (&acc)[4][4][4], int m0, const int (&col_nt)[4],
+                                           int wm, int nn, int L) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = m0 + wm * 64 + mi * 16 + 4 * L + r;
+            if (row >= a.M) continue;
+            if constexpr (GELU) {
+                const int half_n = a.N >> 1;
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni) {
+                    const int i = col_nt[ni] * kTileRows + nn;
+                    if (col_nt[ni] >= a.n_tiles || i >= half_n) continue;
+                    float g = acc[mi][ni][r], up = acc[mi][ni + 2][r];
+                    if (QM == QUANT_STATIC) {
+                        g = g * a.input_scale;
+                        up = up * a.input_scale;
+                    }
+                    g = calibrate_output(g, a.output_scale);
+                    up = calibrate_output(up, a.output_scale);
+                    a.y[static_cast<std::int64_t>(row) * half_n + i] = gelu_tanh(g) * up;
+                }
+            } else {
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) {
+                    const int col = col_nt[ni] * kTileRows + nn;
+                    if (col_nt[ni] >= a.n_tiles || col >= a.N) continue;
+                    float v = acc[mi][ni][r];
+                    if (QM == QUANT_STATIC) v = v * a.input_scale;
+                    a.y[static_cast<std::int64_t>(row) * a.N + col] = calibrate_output(v, a.output_scale);
+                }
+            }
+        }
+    }
+}
+
 template <int WM, bool GELU, int QM, bool ZP, bool SH, bool DBG>
 __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArgs a) {
     using S = GemmShape<WM>;
@@ -253,11 +295,14 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
 
     // workgroup -> (row block, column block): consecutive workgroups go to different XCDs, so give each XCD a
     // contiguous range (its column blocks x all row blocks share its L2)
-    const int total = a.m_blocks * a.n_blocks;
+    const int tiles = a.m_blocks * a.n_blocks;
+    const int total = tiles * a.ksplit;
     int bid = blockIdx.x;
     if (total % 8 == 0) bid = (bid % 8) * (total / 8) + bid / 8;
-    const int mb = bid % a.m_blocks, nb = bid / a.m_blocks;
+    const int ks = bid / tiles, tile = bid % tiles;  // K range ks of output tile `tile`
+    const int mb = tile % a.m_blocks, nb = tile / a.m_blocks;
     const int m0 = mb * S::BM;
+    const int nk = a.k_tiles / a.ksplit, kofs = ks * nk, kend = kofs + nk;  // groups [kofs, kend)
 
     // activation panel of this workgroup: rows [m0, m0 + BM) x K (rows are padded to a multiple of 256)
     const __amdgpu_buffer_rsrc_t ares = rsrc(a.q + static_cast<std::int64_t>(m0) * a.K, static_cast<std::uint32_t>(S::BM) * a.K);
@@ -423,8 +468,8 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
 
     // prologue: steps 0 and 1 (activations, metadata) and 0..2 (packed tiles, zero points) copied, step 0 unpacked
     {
-        const int k1 = a.k_tiles > 1 ? 1 : 0, k2 = a.k_tiles > 2 ? 2 : a.k_tiles - 1;
-        issue(0, 0, 0, 0);
+        const int k1 = nk > 1 ? kofs + 1 : kofs, k2 = nk > 2 ? kofs + 2 : kend - 1;
+        issue(kofs, 0, kofs, 0);
         issue(k1, 1, k1, 1);
         issue(k1, 1, k2, 2);  // activations and scales of step 1 again (same bytes, same slot), tiles of step 2
         __builtin_amdgcn_s_waitcnt(0);
@@ -451,12 +496,12 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
 #define KQ_BSLOT(ni) (GELU ? ((ni) < 2 ? (ni) : 2 + (ni)) : (ni))
 
     int s0 = 0, s2 = 2;  // ring slots (mod 3) of steps kt and kt + 2; kt + 3 uses s0
-    for (int kt = 0; kt < a.k_tiles; ++kt) {
+    for (int kt = kofs; kt < kend; ++kt) {
         const int s1 = s0 == 2 ? 0 : s0 + 1;
         // copies for steps kt + 2 (activations, scales) and kt + 3 (packed tiles, zero points), spread over the
         // MFMA blocks below so the waves do not queue on the memory pipe together (clamped at the end: the last
         // group again, into slots nobody reads)
-        const int ka = kt + 2 < a.k_tiles ? kt + 2 : a.k_tiles - 1, kb = kt + 3 < a.k_tiles ? kt + 3 : a.k_tiles - 1;
+        const int ka = kt + 2 < kend ? kt + 2 : kend - 1, kb = kt + 3 < kend ? kt + 3 : kend - 1;
 
         // operand reads, in the order the blocks consume them
         const std::uint32_t mslot = s0 * S::META_BYTES;
@@ -474,7 +519,7 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
         }
         v4i asr = zero;
         if constexpr (QM != QUANT_STATIC) asr = ds_read16<0>(as_lane + mslot);
-        const std::uint32_t aslot = s0 * S::A_BYTES, bslot = (kt & 1) * kBBytes;
+        const std::uint32_t aslot = s0 * S::A_BYTES, bslot = ((kt - kofs) & 1) * kBBytes;
         v4i A[4][2], B[4][2];
         A[0][0] = ds_read16<0>(a_lane0 + aslot);
         A[0][1] = ds_read16<0>(a_lane1 + aslot);
@@ -556,7 +601,7 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
             // operand read of this step has returned (block 12) (after the last step: stale tiles into a slot
             // nobody reads)
             if (blk == 13) raw = unpack_read(s1, s1);
-            if (blk == 15) unpack_write(raw, (kt + 1) & 1);
+            if (blk == 15) unpack_write(raw, (kt - kofs + 1) & 1);
             epilogue(cp, kp, blk - 1);
             cp = cn;
             kp = kn4;
@@ -578,40 +623,55 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
     }
 #undef KQ_BSLOT
 
-    // store
+    if (a.ksplit > 1) {
+        // K-split: every range stores its fp32 partial tile; gemm_i4_reduce_kernel adds them in range order
+        float* const dst = a.partial + ((static_cast<std::int64_t>(ks) * tiles + tile) * S::THREADS + tid) * 64;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
+        for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = m0 + wm * 64 + mi * 16 + 4 * L + r;
-            if (row >= a.M) continue;
-            if constexpr (GELU) {
-                const int half_n = a.N >> 1;
-#pragma unroll
-                for (int ni = 0; ni < 2; ++ni) {
-                    const int i = col_nt[ni] * kTileRows + nn;
-                    if (col_nt[ni] >= a.n_tiles || i >= half_n) continue;
-                    float g = acc[mi][ni][r], up = acc[mi][ni + 2][r];
-                    if (QM == QUANT_STATIC) {
-                        g = g * a.input_scale;
-                        up = up * a.input_scale;
-                    }
-                    g = calibrate_output(g, a.output_scale);
-                    up = calibrate_output(up, a.output_scale);
-                    a.y[static_cast<std::int64_t>(row) * half_n + i] = gelu_tanh(g) * up;
-                }
-            } else {
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni) {
-                    const int col = col_nt[ni] * kTileRows + nn;
-                    if (col_nt[ni] >= a.n_tiles || col >= a.N) continue;
-                    float v = acc[mi][ni][r];
-                    if (QM == QUANT_STATIC) v = v * a.input_scale;
-                    a.y[static_cast<std::int64_t>(row) * a.N + col] = calibrate_output(v, a.output_scale);
-                }
-            }
-        }
+            for (int ni = 0; ni < 4; ++ni)
+                *reinterpret_cast<float4*>(dst + (mi * 4 + ni) * 4) =
+                    make_float4(acc[mi][ni][0], acc[mi][ni][1], acc[mi][ni][2], acc[mi][ni][3]);
+        return;
     }
+    store_tile<WM, GELU, QM>(a, acc, m0, col_nt, wm, nn, L);
+}
+
+// Sum of the K ranges of one output tile (range order, so the result does not depend on which range finished
+// first), then the same epilogue as the unsplit GEMM. One workgroup per output tile, threads as in the GEMM.
+template <int WM, bool GELU, int QM>
+__global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_reduce_kernel(GemmArgs a) {
+    using S = GemmShape<WM>;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WM, wn = wave / WM;
+    const int nn = lane & 15, L = lane >> 4;
+    const int tiles = a.m_blocks * a.n_blocks, tile = blockIdx.x;
+    const int mb = tile % a.m_blocks, nb = tile / a.m_blocks;
+    int col_nt[4];
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) col_nt[ni] = slot_tile<GELU>(a, nb, wave_slot<GELU>(wn, ni));
+    float acc[4][4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[mi][ni][r] = 0.F;
+    for (int q = 0; q < a.ksplit; ++q) {
+        const float* src = a.partial + ((static_cast<std::int64_t>(q) * tiles + tile) * S::THREADS + tid) * 64;
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const float4 v = *reinterpret_cast<const float4*>(src + (mi * 4 + ni) * 4);
+                acc[mi][ni][0] = acc[mi][ni][0] + v.x;
+                acc[mi][ni][1] = acc[mi][ni][1] + v.y;
+                acc[mi][ni][2] = acc[mi][ni][2] + v.z;
+                acc[mi][ni][3] = acc[mi][ni][3] + v.w;
+            }
+    }
+    store_tile<WM, GELU, QM>(a, acc, mb * S::BM, col_nt, wm, nn, L);
 }
 
 __global__ __launch_bounds__(256) void unpermute_rows_kernel(const std::int8_t* q, int M, int K, std::int8_t* codes) {
@@ -632,6 +692,50 @@ __global__ __launch_bounds__(256) void transpose_stats_kernel(const float* s_t, 
 }
 
 }  // namespace
+
+namespace {
+int env_int(const char* name) {
+    const char* e = std::getenv(name);  // tuning overrides
+    return e ? std::atoi(e) : 0;
+}
+}  // namespace
+
+// Launch plan: 256-row tiles (WM = 4), the K range split in 2, 4 or 8 when that fills the chip (at least 256
+// workgroups) and every range keeps >= 16 groups; otherwise 128-row tiles (WM = 2), split the same way. A split adds
+// one small reduction launch and the partial tiles' traffic, so short K ranges do not pay for it.
+GemmPlan gemm_i4_plan(const Weight& w, std::int64_t M, bool gelu) {
+    static const int forced_wm = env_int("KQ_GEMM_WM"), forced_split = env_int("KQ_GEMM_KSPLIT");
+    const int kt = static_cast<int>(w.geo.k_tiles);
+    GemmPlan p;
+    p.n_blocks = gelu ? static_cast<int>((w.geo.n_tiles / 2 + 3) / 4) : static_cast<int>((w.geo.n_tiles + 7) / 8);
+    auto blocks_m = [&](int wm) { return static_cast<int>((M + 64 * wm - 1) / (64 * wm)); };
+    auto best_split = [&](int tiles, bool need_full) {
+        int best = 0;
+        for (int sp = 1; sp <= 8; sp *= 2) {
+            if (kt % sp || (sp > 1 && kt / sp < 16)) break;
+            best = sp;
+            if (tiles * sp >= 256) return sp;
+        }
+        return need_full ? 0 : best;
+    };
+    if (forced_wm == 2 || forced_wm == 4) {
+        p.wm = forced_wm;
+        p.m_blocks = blocks_m(p.wm);
+        p.ksplit = best_split(p.m_blocks * p.n_blocks, false);
+    } else {
+        p.wm = 4;
+        p.m_blocks = blocks_m(4);
+        p.ksplit = best_split(p.m_blocks * p.n_blocks, true);
+        if (p.ksplit == 0) {
+            p.wm = 2;
+            p.m_blocks = blocks_m(2);
+            p.ksplit = best_split(p.m_blocks * p.n_blocks, false);
+        }
+    }
+    if (p.ksplit < 1) p.ksplit = 1;
+    if (forced_split > 0 && kt % forced_split == 0 && kt / forced_split >= 4) p.ksplit = forced_split;
+    return p;
+}
 
 bool gemm_i4_fits(const LinearCall& c) {
     const Weight& w = *c.w;
@@ -664,6 +768,7 @@ hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_
     q.q = act.q;
     q.scale_t = act.scale;
     q.sum_t = nullptr;
+    const GemmPlan plan = gemm_i4_plan(w, c.M, c.gelu_gate);
     const int waves = M_p * (K / 512);
     const dim3 qgrid(static_cast<unsigned>((waves + 3) / 4)), qblock(256);
     if (stat) hipLaunchKernelGGL(quantize_rows_kernel<dev::QUANT_STATIC>, qgrid, qblock, 0, stream, q);
@@ -690,20 +795,16 @@ hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_
     a.scale_half = w.scale_type == META_F16;
     a.input_scale = c.input_scale;
     a.output_scale = c.output_scale;
-    const int n_blocks = c.gelu_gate ? static_cast<int>((w.geo.n_tiles / 2 + 3) / 4) : static_cast<int>((w.geo.n_tiles + 7) / 8);
-    // 256-row tiles when they give the chip at least two workgroups per CU, else 128-row tiles
-    static const int forced_wm = [] {
-        const char* e = std::getenv("KQ_GEMM_WM");  // tuning override: 2 or 4
-        return e ? std::atoi(e) : 0;
-    }();
-    int wm = static_cast<std::int64_t>((M + 255) / 256) * n_blocks >= 512 ? 4 : 2;
-    if (forced_wm == 2 || forced_wm == 4) wm = forced_wm;
-    a.m_blocks = (M + 64 * wm - 1) / (64 * wm);
-    a.n_blocks = n_blocks;
+    const int wm = plan.wm;
+    a.m_blocks = plan.m_blocks;
+    a.n_blocks = plan.n_blocks;
+    a.ksplit = plan.ksplit;
+    a.partial = act.partial;
+    if (plan.ksplit > 1 && !act.partial) return hipErrorInvalidValue;
     const bool zp = w.zero_mode == ZERO_POINT;
     const bool dbg = c.dump != nullptr;
     const bool sh = w.scale_type == META_F16;
-    const dim3 grid(static_cast<unsigned>(a.m_blocks * a.n_blocks));
+    const dim3 grid(static_cast<unsigned>(a.m_blocks * a.n_blocks * a.ksplit));
 #define KQ_G(WM, GE, QM, Z, H, D) \
     hipLaunchKernelGGL((gemm_i4_kernel<WM, GE, QM, Z, H, D>), grid, dim3(GemmShape<WM>::THREADS), GemmShape<WM>::LDS, stream, a)
 #define KQ_GH(WM, GE, QM, Z, D) \
@@ -728,6 +829,22 @@ hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_
 #undef KQ_GW
 #undef KQ_GH
 #undef KQ_G
+    e = hipGetLastError();
+    if (e != hipSuccess || plan.ksplit == 1) return e;
+    const dim3 rgrid(static_cast<unsigned>(a.m_blocks * a.n_blocks));
+#define KQ_R(WM, GE, QM) hipLaunchKernelGGL((gemm_i4_reduce_kernel<WM, GE, QM>), rgrid, dim3(GemmShape<WM>::THREADS), 0, stream, a)
+#define KQ_RW(GE, QM) \
+    if (wm == 4) KQ_R(4, GE, QM); \
+    else KQ_R(2, GE, QM)
+    if (stat) {
+        if (c.gelu_gate) { KQ_RW(true, dev::QUANT_STATIC); }
+        else { KQ_RW(false, dev::QUANT_STATIC); }
+    } else {
+        if (c.gelu_gate) { KQ_RW(true, dev::QUANT_DYN_SYM); }
+        else { KQ_RW(false, dev::QUANT_DYN_SYM); }
+    }
+#undef KQ_RW
+#undef KQ_R
     return hipGetLastError();
 }
 

@@ -39,6 +39,7 @@ struct ActBuffers {
     float* scale = nullptr;         // [rows_p][groups_p]
     std::int32_t* sum = nullptr;    // [rows_p][groups_p]
     std::int32_t* zero = nullptr;   // [rows_p][groups_p]
+    float* partial = nullptr;       // prefill GEMM with split K: fp32 partial tiles of every K range
     std::int64_t rows_p = 0;
 };
 
@@ -79,6 +80,10 @@ hipError_t launch_skinny(const LinearCall& c, const SkinnyPlan& p, hipStream_t s
 // Prefill projection (M > 16) for 4-bit weights with g = 128 and K a multiple of 512 (kq_gemm.hip): a row
 // quantizer writing codes [rows_p][K] and transposed block scales [K/128][rows_p] into the workspace, then the int8
 // MFMA GEMM. rows_p = round_up(M, 256).
+struct GemmPlan {
+    int wm = 4, m_blocks = 0, n_blocks = 0, ksplit = 1;
+};
+GemmPlan gemm_i4_plan(const Weight& w, std::int64_t M, bool gelu);
 bool gemm_i4_fits(const LinearCall& c);
 hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_t stream);
 hipError_t launch_gemm_i4_quantize_dump(const LinearCall& c, const ActBuffers& act, std::int8_t* codes, float* scales,

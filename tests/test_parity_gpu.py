@@ -99,6 +99,10 @@ CASES = [
     (4, 128, 17, 2048, 128, None, 0.05, False, 0.0),
     (4, 128, 64, 512, 1040, "zp", 0.0, True, 0.0),
     (4, 128, 260, 1536, 144, "zp", 0.0, False, 0.001),
+    # split K (2 or 4 ranges per output tile, summed in range order by a reduction kernel)
+    (4, 128, 64, 4096, 256, "zp", 0.0, True, 0.0),
+    (4, 128, 300, 8192, 256, None, 0.0, False, 0.001),
+    (4, 128, 40, 8192, 144, None, 0.05, False, 0.0),
     # group sizes the tiles cannot carry (row-major integer path)
     (4, 96, 3, 384, 256, "zp", 0.0, False, 0.0),
     (8, 48, 2, 288, 96, None, 0.0, False, 0.0),
@@ -269,11 +273,11 @@ def test_zero_block_and_empty(dev, ref):
     assert tuple(empty.shape) == (0, 256)
 
 
-@pytest.mark.parametrize("M,I", [(1, 256), (4, 256), (8, 256), (16, 256), (200, 256), (300, 272)])
-def test_gelu_gate_fused(dev, ref, M, I):
+@pytest.mark.parametrize("M,I,K", [(1, 256, 512), (4, 256, 512), (8, 256, 512), (16, 256, 512), (200, 256, 512),
+                                   (300, 272, 512), (40, 256, 2048), (40, 256, 4096)])
+def test_gelu_gate_fused(dev, ref, M, I, K):
     """gate/up projection + GELU-tanh in one pass equals the oracle's projection followed by gelu_gate."""
     rng = np.random.default_rng(M)
-    K = 512
     values, scales, zp, _ = weights(rng, 2 * I, K, 4, 128, zero_points=True)
     x = activations(rng, M, K)
     y_full, _ = ref.packed_linear(x, values, scales, 4, 128, zero_points=zp)
