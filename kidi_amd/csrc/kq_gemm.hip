@@ -247,9 +247,10 @@ __device__ __forceinline__ constexpr int wave_slot(int wn, int ni) {
 // calibrated inputs scale by input_scale, calibrated outputs round to output_scale steps, GELU pairs gate and up.
 template <int WM, bool GELU, int QM>
 __device__ __forceinline__ void store_tile(const GemmArgs& a, const float (&acc)[4][4][4], int m0, const int (&col_nt)[4],
-                                           int wm, int nn, int L) {
+                                           int wm, int nn, int L, int only_mi = -1) {
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
+        if (only_mi >= 0 && mi != only_mi) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = m0 + wm * 64 + mi * 16 + 4 * L + r;
@@ -624,21 +625,23 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
 #undef KQ_BSLOT
 
     if (a.ksplit > 1) {
-        // K-split: every range stores its fp32 partial tile; gemm_i4_reduce_kernel adds them in range order
-        float* const dst = a.partial + ((static_cast<std::int64_t>(ks) * tiles + tile) * S::THREADS + tid) * 64;
+        // K-split: every range stores its fp32 partial tile, as [16 groups (mi, ni)][thread] of float4 so each store
+        // of a wave is 1 KiB contiguous; gemm_i4_reduce_kernel adds the ranges in range order
+        float* const dst = a.partial + (static_cast<std::int64_t>(ks) * tiles + tile) * S::THREADS * 64 + tid * 4;
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni)
-                *reinterpret_cast<float4*>(dst + (mi * 4 + ni) * 4) =
-                    make_float4(acc[mi][ni][0], acc[mi][ni][1], acc[mi][ni][2], acc[mi][ni][3]);
+                __builtin_nontemporal_store(v4f{acc[mi][ni][0], acc[mi][ni][1], acc[mi][ni][2], acc[mi][ni][3]},
+                                            reinterpret_cast<v4f*>(dst + (mi * 4 + ni) * S::THREADS * 4));
         return;
     }
     store_tile<WM, GELU, QM>(a, acc, m0, col_nt, wm, nn, L);
 }
 
 // Sum of the K ranges of one output tile (range order, so the result does not depend on which range finished
-// first), then the same epilogue as the unsplit GEMM. One workgroup per output tile, threads as in the GEMM.
+// first), then the same epilogue as the unsplit GEMM. Four workgroups per output tile, one per 16-row strip mi of
+// every wave's 64 x 64 block; threads as in the GEMM.
 template <int WM, bool GELU, int QM>
 __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_reduce_kernel(GemmArgs a) {
     using S = GemmShape<WM>;
@@ -646,7 +649,7 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_reduce_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave % WM, wn = wave / WM;
     const int nn = lane & 15, L = lane >> 4;
-    const int tiles = a.m_blocks * a.n_blocks, tile = blockIdx.x;
+    const int tiles = a.m_blocks * a.n_blocks, tile = blockIdx.x >> 2, strip = blockIdx.x & 3;
     const int mb = tile % a.m_blocks, nb = tile / a.m_blocks;
     int col_nt[4];
 #pragma unroll
@@ -659,19 +662,21 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_reduce_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[mi][ni][r] = 0.F;
     for (int q = 0; q < a.ksplit; ++q) {
-        const float* src = a.partial + ((static_cast<std::int64_t>(q) * tiles + tile) * S::THREADS + tid) * 64;
+        const float* src = a.partial + (static_cast<std::int64_t>(q) * tiles + tile) * S::THREADS * 64 + tid * 4;
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
+        for (int ni = 0; ni < 4; ++ni) {
+            const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(src + (strip * 4 + ni) * S::THREADS * 4));
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) {
-                const float4 v = *reinterpret_cast<const float4*>(src + (mi * 4 + ni) * 4);
-                acc[mi][ni][0] = acc[mi][ni][0] + v.x;
-                acc[mi][ni][1] = acc[mi][ni][1] + v.y;
-                acc[mi][ni][2] = acc[mi][ni][2] + v.z;
-                acc[mi][ni][3] = acc[mi][ni][3] + v.w;
+            for (int mi = 0; mi < 4; ++mi) {
+                if (mi != strip) continue;
+                acc[mi][ni][0] = acc[mi][ni][0] + v[0];
+                acc[mi][ni][1] = acc[mi][ni][1] + v[1];
+                acc[mi][ni][2] = acc[mi][ni][2] + v[2];
+                acc[mi][ni][3] = acc[mi][ni][3] + v[3];
             }
+        }
     }
-    store_tile<WM, GELU, QM>(a, acc, mb * S::BM, col_nt, wm, nn, L);
+    store_tile<WM, GELU, QM>(a, acc, mb * S::BM, col_nt, wm, nn, L, strip);
 }
 
 __global__ __launch_bounds__(256) void unpermute_rows_kernel(const std::int8_t* q, int M, int K, std::int8_t* codes) {
@@ -831,7 +836,7 @@ hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_
 #undef KQ_G
     e = hipGetLastError();
     if (e != hipSuccess || plan.ksplit == 1) return e;
-    const dim3 rgrid(static_cast<unsigned>(a.m_blocks * a.n_blocks));
+    const dim3 rgrid(static_cast<unsigned>(a.m_blocks * a.n_blocks * 4));
 #define KQ_R(WM, GE, QM) hipLaunchKernelGGL((gemm_i4_reduce_kernel<WM, GE, QM>), rgrid, dim3(GemmShape<WM>::THREADS), 0, stream, a)
 #define KQ_RW(GE, QM) \
     if (wm == 4) KQ_R(4, GE, QM); \
