@@ -5,11 +5,11 @@
 //   max |x| and the code sum with DPP; codes go to [M_p][K] in the tiles' permuted order, block scales to
 //   [groups][M_p] (transposed so a GEMM stage copies one contiguous 1 KiB row of them).
 // gemm_i4_kernel: workgroup tile 256 (rows) x 128 (output columns = 8 weight row tiles), 8 waves of 64 x 64, one
-//   128-column k-step (= one 4-bit tile = one group) per iteration, double-buffered:
+//   128-column k-step (= one 4-bit tile = one group) per iteration, operands in LDS rings:
 //     - activation codes: 32 direct-to-LDS copies of 1 KiB per step (buffer_load ... lds), lane addresses XOR-
 //       swizzled by row so A-operand reads spread over the LDS banks;
-//     - weights: each thread loads one 16-byte packed slot (one per tile lane) a step ahead, unpacks it to int8
-//       with the zero point folded in (u - zp per byte, SWAR), and stores both 64-column halves in B-operand order;
+//     - weights: packed tiles copied to LDS the same way; each wave unpacks one (two) of them to int8 with the zero
+//       point folded in (u - zp per byte, SWAR) and stores both 64-column halves in B-operand order;
 //     - MFMA: per 64-column half 4 A and 4 B reads, 16 v_mfma_i32_16x16x64_i8; the int32 accumulators hold the
 //       exact per-group partials P' = sum q (u - zp);
 //     - epilogue per group: acc += a_s[row] * s[col] * P' (calibrated: s * P', input_scale applied at the end).
@@ -38,11 +38,12 @@ constexpr int kBBytes = 8 * 2 * 1024;   // unpacked weights per stage: [tile slo
 constexpr int kQuantRows = 256;         // activation rows are padded to this for every tile shape
 
 // Workgroup tile: WM x 2 waves of 64 x 64 outputs; BM = 64 WM rows x 128 columns (one group) per k step. Every
-// global operand reaches LDS through direct copies (buffer_load ... lds), so no loaded register lives across steps:
-//   - activation codes, weight scales, activation scales: copied two steps ahead into a 3-slot ring;
-//   - packed int4 weight tiles and zero points: copied three steps ahead into a 3-slot ring, unpacked to int8
-//     (zero point folded in) LDS to LDS at the end of the previous step into a 2-slot ring of B operands.
-// One barrier per step; before it, s_waitcnt vmcnt(copies of this step) leaves only this step's copies in flight.
+// global operand reaches LDS through direct copies (buffer_load ... lds), so no loaded register waits on memory:
+//   - activation codes, weight scales, activation scales: copied three steps ahead into a 3-slot ring;
+//   - packed int4 weight tiles and zero points: copied four steps ahead into a 3-slot ring, unpacked to int8
+//     (zero point folded in) LDS to LDS during the previous step into a 2-slot ring of B operands.
+// One barrier per step, in the middle of it; before it, s_waitcnt vmcnt(copies of the previous step) leaves only
+// those in flight.
 template <int WM>
 struct GemmShape {
     static constexpr int BM = 64 * WM, WAVES = 2 * WM, THREADS = 64 * WAVES;
@@ -331,39 +332,33 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
     __amdgpu_buffer_rsrc_t mres[META_N];
     std::uint32_t meta_base[META_N], meta_step[META_N];
     int meta_dst[META_N];  // byte offset inside a metadata slot; -1: the scratch area
-    bool meta_lead3[META_N];  // zero points travel with the packed tiles, three steps ahead
+    bool meta_lead[META_N];  // zero points travel with the packed tiles (four steps ahead, the rest three)
 #pragma unroll
     for (int i = 0; i < META_N; ++i) {
         const int role = wave * META_N + i;
         meta_base[i] = kOob;
         meta_step[i] = 0;
         meta_dst[i] = -1;
-        meta_lead3[i] = role == 1;
+        meta_lead[i] = role == 1;
         mres[i] = rsrc(a.q, 0u);
         if (role == 0 || (!SH && role == WM + 2)) {
             constexpr int es = SH ? 2 : 4, lanes_per_slot = 16 * es / 4;
             const int t = (role == 0 ? 0 : 4) + lane / lanes_per_slot;
             const int nt = slot_tile<GELU>(a, nb, t);
             mres[i] = rsrc(a.scales, meta_n * es);
-            if (nt < a.n_tiles) {
-                meta_base[i] = static_cast<std::uint32_t>(nt * a.groups_p) * kTileRows * es + (lane % lanes_per_slot) * 4;
-                meta_step[i] = kTileRows * es;
-            }
+            meta_step[i] = kTileRows * es;
+            if (nt < a.n_tiles) meta_base[i] = static_cast<std::uint32_t>(nt * a.groups_p) * kTileRows * es + (lane % lanes_per_slot) * 4;
             meta_dst[i] = S::WS_OFF + (role == 0 ? 0 : 256);
         } else if (role == 1) {
             const int nt = lane < 16 ? slot_tile<GELU>(a, nb, lane / 2) : a.n_tiles;
             mres[i] = rsrc(a.zero_points, ZP ? meta_n / 2 : 0u);
-            if (ZP && nt < a.n_tiles) {
-                meta_base[i] = static_cast<std::uint32_t>(nt * a.groups_p) * 8 + (lane % 2) * 4;
-                meta_step[i] = 8;
-            }
+            meta_step[i] = 8;
+            if (ZP && nt < a.n_tiles) meta_base[i] = static_cast<std::uint32_t>(nt * a.groups_p) * 8 + (lane % 2) * 4;
             meta_dst[i] = S::ZP_OFF;
         } else if (role < 2 + WM) {  // rows in the permuted order of scale_t
             mres[i] = rsrc(a.scale_t, static_cast<std::uint32_t>(a.groups_p) * a.M_p * 4);
-            if (QM != QUANT_STATIC) {
-                meta_base[i] = static_cast<std::uint32_t>(m0 + 64 * (role - 2) + lane) * 4;
-                meta_step[i] = static_cast<std::uint32_t>(a.M_p) * 4;
-            }
+            meta_step[i] = static_cast<std::uint32_t>(a.M_p) * 4;
+            if (QM != QUANT_STATIC) meta_base[i] = static_cast<std::uint32_t>(m0 + 64 * (role - 2) + lane) * 4;
             meta_dst[i] = S::AS_OFF + 256 * (role - 2);
         }
     }
@@ -371,14 +366,20 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
     // Copies of one step: activation codes of step ka into A slot ka % 3, packed tiles of step kb into raw slot
     // kb % 3, and this wave's metadata (step kb for zero points, else ka). The slot indices use the unclamped
     // step numbers; clamped steps copy the last group again into slots nobody reads.
+    // Copy offsets: the lane part goes in the VGPR offset (computed once), the step part in the SGPR offset, so a
+    // copy costs no vector instruction. Out-of-range lanes carry kOob in the VGPR part (their sum stays >= 2^31,
+    // beyond every buffer); every other lane's sum is in range.
+    // LDS byte 1024 i + 16 l of an A slot is row r = 8 i + l / 8, 16-byte chunk c' = l % 8, which holds global chunk
+    // c = c' ^ (r & 7); i = 4 wave + part
+    std::uint32_t a_voff[4];
+#pragma unroll
+    for (int part = 0; part < 4; ++part) {
+        const int r = (wave * 4 + part) * 8 + (lane >> 3);
+        a_voff[part] = static_cast<std::uint32_t>(r) * a.K + ((lane & 7) ^ (r & 7)) * 16;
+    }
     auto issue_a = [&](int ka, int sa, int part) {
-        // LDS byte 1024 i + 16 l of the slot is row r = 8 i + l / 8, 16-byte chunk c' = l % 8, which holds
-        // global chunk c = c' ^ (r & 7)
-        const int i = wave * 4 + part;
-        const int r = i * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ (r & 7);
-        const std::uint32_t off = static_cast<std::uint32_t>(r) * a.K + ka * kBK + c * 16;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(lds + S::A_RING + sa * S::A_BYTES + i * 1024), 16, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(lds + S::A_RING + sa * S::A_BYTES + (wave * 4 + part) * 1024), 16,
+                                                 a_voff[part], ka * kBK, 0, 0);
     };
     // (resources are copied out of their arrays: an array element passed to the builtin directly makes the host
     // pass drop the kernel's launch stub)
@@ -387,17 +388,19 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
         for (int u = 0; u < S::TPW; ++u) {
             const __amdgpu_buffer_rsrc_t wr = wres[u];
             __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(lds + S::RAW_RING + sb * S::RAW_BYTES + (wave * S::TPW + u) * kTileBytes),
-                                                     16, static_cast<std::uint32_t>(kb * kTileBytes + lane * 16), 0, 0, 0);
+                                                     16, static_cast<std::uint32_t>(lane * 16), kb * kTileBytes, 0, 0);
         }
     };
+    // (ka < 0: only the zero points are copied, the other roles copy zeros into the scratch area)
     auto issue_meta = [&](int ka, int sa, int kb, int sb) {
 #pragma unroll
         for (int i = 0; i < META_N; ++i) {
-            const int km = meta_lead3[i] ? kb : ka, sm = meta_lead3[i] ? sb : sa;
-            const std::uint32_t moff = meta_base[i] == kOob ? kOob : meta_base[i] + meta_step[i] * km;
-            std::uint8_t* mdst = meta_dst[i] < 0 ? lds + S::SCRATCH : lds + S::META_RING + sm * S::META_BYTES + meta_dst[i];
+            const int km = meta_lead[i] ? kb : ka, sm = meta_lead[i] ? sb : sa;
+            const bool idle = meta_dst[i] < 0 || km < 0;
+            std::uint8_t* mdst = idle ? lds + S::SCRATCH : lds + S::META_RING + sm * S::META_BYTES + meta_dst[i];
             const __amdgpu_buffer_rsrc_t mr = mres[i];
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(mr, (lds_void*)mdst, 4, moff, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(mr, (lds_void*)mdst, 4, km < 0 ? kOob : meta_base[i],
+                                                     km < 0 ? 0u : meta_step[i] * static_cast<std::uint32_t>(km), 0, 0);
         }
     };
     // all copies of one step: activation codes of step ka into A slot sa, packed tiles of step kb into raw slot sb,
@@ -437,7 +440,7 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
 #pragma unroll
         for (int u = 0; u < S::TPW; ++u) {
             const std::uint32_t z = ZP ? ((r.zp[u] >> (4 * (nn & 1))) & 15u) : 8u;
-            const std::uint32_t zz = z * 0x01010101u;
+            const std::uint32_t zz = __builtin_amdgcn_perm(0u, z, 0u);  // z in every byte (v_perm, not a multiply)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const std::uint32_t d0 = static_cast<std::uint32_t>(r.w[u][2 * j]), d1 = static_cast<std::uint32_t>(r.w[u][2 * j + 1]);
@@ -467,17 +470,30 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[mi][ni][r] = 0.F;
 
-    // prologue: steps 0 and 1 (activations, metadata) and 0..2 (packed tiles, zero points) copied, step 0 unpacked
+    // Step schedule: one barrier per step, between blocks 7 and 8 (blocks are 16 x 16 output blocks, mi-major).
+    //   - Step kt's operand registers are read during step kt - 1, each right after its last use there: metadata and
+    //     A rows 0-1 after the barrier, A row 2 after block 12, B columns 0-2 after blocks 13-15, B column 3 and A
+    //     row 3 last. By block 4 of step kt every operand of the step is in registers.
+    //   - Blocks 4-6 unpack step kt + 1's packed tiles into B slot (kt + 1) % 2 (free since the previous barrier).
+    //   - The barrier (after s_waitcnt vmcnt(copies of step kt - 1) lgkmcnt(0)) ends every read of step kt's A and
+    //     metadata slots and of step kt + 1's raw slot, and publishes B slot (kt + 1) % 2. Blocks 8-13 then copy
+    //     step kt + 3's activation codes and metadata into the slots of step kt, and step kt + 4's packed tiles and
+    //     zero points into the raw / zero-point slots unpacked at blocks 4-6.
+    // Ring slots are step - kofs modulo 3 (A, raw, metadata) and modulo 2 (B). Copies past the K range repeat the
+    // range's last group into slots nobody reads.
+    auto clamp_k = [&](int k) { return k < kend ? k : kend - 1; };
     {
-        const int k1 = nk > 1 ? kofs + 1 : kofs, k2 = nk > 2 ? kofs + 2 : kend - 1;
         issue(kofs, 0, kofs, 0);
-        issue(k1, 1, k1, 1);
-        issue(k1, 1, k2, 2);  // activations and scales of step 1 again (same bytes, same slot), tiles of step 2
+        issue(clamp_k(kofs + 1), 1, clamp_k(kofs + 1), 1);
+        issue(clamp_k(kofs + 2), 2, clamp_k(kofs + 2), 2);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         unpack(0, 0, 0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        // packed tiles and zero points of step kofs + 3 into the slots step kofs used
+        issue_raw(clamp_k(kofs + 3), 0);
+        issue_meta(-1, 0, clamp_k(kofs + 3), 0);
     }
 
     // per-lane operand addresses (add the slot base per step)
@@ -496,17 +512,11 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
     const v4f zerof = {0.F, 0.F, 0.F, 0.F};
 #define KQ_BSLOT(ni) (GELU ? ((ni) < 2 ? (ni) : 2 + (ni)) : (ni))
 
-    int s0 = 0, s2 = 2;  // ring slots (mod 3) of steps kt and kt + 2; kt + 3 uses s0
-    for (int kt = kofs; kt < kend; ++kt) {
-        const int s1 = s0 == 2 ? 0 : s0 + 1;
-        // copies for steps kt + 2 (activations, scales) and kt + 3 (packed tiles, zero points), spread over the
-        // MFMA blocks below so the waves do not queue on the memory pipe together (clamped at the end: the last
-        // group again, into slots nobody reads)
-        const int ka = kt + 2 < kend ? kt + 2 : kend - 1, kb = kt + 3 < kend ? kt + 3 : kend - 1;
-
-        // operand reads, in the order the blocks consume them
-        const std::uint32_t mslot = s0 * S::META_BYTES;
-        std::uint32_t svr[4];
+    // operand registers of one step, read in this order: svr[0..3], asr, A0, A1 | A2 | B0 | B1 | B2 | B3, A3
+    std::uint32_t svr[4];
+    v4i asr = zero;
+    v4i A[4][2], B[4][2];
+    auto read_meta = [&](std::uint32_t mslot) {
         if constexpr (SH) {
             svr[0] = ds_read2<KQ_BSLOT(0) * kWsStride>(ws_lane + mslot);
             svr[1] = ds_read2<KQ_BSLOT(1) * kWsStride>(ws_lane + mslot);
@@ -518,111 +528,191 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
             svr[2] = ds_read4<KQ_BSLOT(2) * kWsStride>(ws_lane + mslot);
             svr[3] = ds_read4<KQ_BSLOT(3) * kWsStride>(ws_lane + mslot);
         }
-        v4i asr = zero;
         if constexpr (QM != QUANT_STATIC) asr = ds_read16<0>(as_lane + mslot);
-        const std::uint32_t aslot = s0 * S::A_BYTES, bslot = ((kt - kofs) & 1) * kBBytes;
-        v4i A[4][2], B[4][2];
-        A[0][0] = ds_read16<0>(a_lane0 + aslot);
-        A[0][1] = ds_read16<0>(a_lane1 + aslot);
-        B[0][0] = ds_read16<(KQ_BSLOT(0) * 2 + 0) * 1024>(b_lane + bslot);
-        B[0][1] = ds_read16<(KQ_BSLOT(0) * 2 + 1) * 1024>(b_lane + bslot);
-        B[1][0] = ds_read16<(KQ_BSLOT(1) * 2 + 0) * 1024>(b_lane + bslot);
-        B[1][1] = ds_read16<(KQ_BSLOT(1) * 2 + 1) * 1024>(b_lane + bslot);
-        float sv[4], asel[4];
+        if constexpr (DBG) lgkm_wait<0>(svr[0], svr[1], svr[2], svr[3], asr);
+    };
+    // A register read from LDS is written when the data returns: until the covering lgkmcnt wait nothing may copy,
+    // spill or reuse it. Every read here has a consumer behind a wait; the debug variant, which spills, waits at
+    // once.
+#define KQ_READ_A(mi, aslot)                                                       \
+    do {                                                                           \
+        A[mi][0] = ds_read16<(mi) * 16 * kBK>(a_lane0 + (aslot));                  \
+        A[mi][1] = ds_read16<(mi) * 16 * kBK>(a_lane1 + (aslot));                  \
+        if constexpr (DBG) lgkm_wait<0>(A[mi][0], A[mi][1]);                       \
+    } while (0)
+#define KQ_READ_B(ni, bslot)                                                       \
+    do {                                                                           \
+        B[ni][0] = ds_read16<(KQ_BSLOT(ni) * 2 + 0) * 1024>(b_lane + (bslot));     \
+        B[ni][1] = ds_read16<(KQ_BSLOT(ni) * 2 + 1) * 1024>(b_lane + (bslot));     \
+        if constexpr (DBG) lgkm_wait<0>(B[ni][0], B[ni][1]);                       \
+    } while (0)
+    // step kofs's operands
+    read_meta(0);
+    KQ_READ_A(0, 0);
+    KQ_READ_A(1, 0);
+    KQ_READ_A(2, 0);
+    KQ_READ_B(0, 0);
+    KQ_READ_B(1, 0);
+    KQ_READ_B(2, 0);
+    KQ_READ_B(3, 0);
+    KQ_READ_A(3, 0);
 
-        // 16 blocks of 16 x 16. Block b: two int8 MFMAs give the exact partials P' of group kt; a 4x4x1 f32 MFMA
-        // (16 outer products of 4 rows x 4 columns) gives k = a_s * s in the same lane layout (lane = column
-        // nn + 16 L, register r = row 4 L + r). The epilogue of block b (acc += k * P', two VALU per element) is
-        // issued after the MFMAs of block b + 1.
-        auto mfmas = [&](int blk, v4i& c, v4f& k) {
-            const int mi = blk >> 2, ni = blk & 3;
-            // wait for this block's operands (reads return in order): 11 (10) reads issued at the start of the
-            // step; each later operand pair is issued two blocks before its first use
-            if (blk == 0) {
-                lgkm_wait<2>(svr[0], svr[1], svr[2], svr[3], asr, A[0][0], A[0][1], B[0][0], B[0][1]);
+    float sv[4], asel[4];  // weight and activation scales of the current step
+    // Block b: two int8 MFMAs give the exact partials P' of the step's group; a 4x4x1 f32 MFMA (16 outer products
+    // of 4 rows x 4 columns) gives k = a_s * s in the same lane layout (lane = column nn + 16 L, register r = row
+    // 4 L + r). The epilogue of block b (acc += k * P', two VALU per element) is issued after the MFMAs of block
+    // b + 1.
+    auto mfmas = [&](int blk, v4i& c, v4f& k) {
+        const int mi = blk >> 2, ni = blk & 3;
+        // reads return in order: after B0 come B1, B2, B3 and A3 (8 reads)
+        if (blk == 0) {
+            lgkm_wait<8>(svr[0], svr[1], svr[2], svr[3], asr, A[0][0], A[0][1], A[1][0], A[1][1], A[2][0], A[2][1], B[0][0], B[0][1]);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    sv[i] = SH ? __half2float(__ushort_as_half(static_cast<unsigned short>(svr[i]))) : __uint_as_float(svr[i]);
-                    asel[i] = __int_as_float(asr[i]);
-                }
-                B[2][0] = ds_read16<(KQ_BSLOT(2) * 2 + 0) * 1024>(b_lane + bslot);
-                B[2][1] = ds_read16<(KQ_BSLOT(2) * 2 + 1) * 1024>(b_lane + bslot);
+            for (int i = 0; i < 4; ++i) {
+                sv[i] = SH ? __half2float(__ushort_as_half(static_cast<unsigned short>(svr[i]))) : __uint_as_float(svr[i]);
+                asel[i] = __int_as_float(asr[i]);
             }
-            if (blk == 1) {
-                lgkm_wait<2>(B[1][0], B[1][1]);
-                B[3][0] = ds_read16<(KQ_BSLOT(3) * 2 + 0) * 1024>(b_lane + bslot);
-                B[3][1] = ds_read16<(KQ_BSLOT(3) * 2 + 1) * 1024>(b_lane + bslot);
-            }
-            if (blk == 2) {
-                lgkm_wait<2>(B[2][0], B[2][1]);
-                A[1][0] = ds_read16<16 * kBK>(a_lane0 + aslot);
-                A[1][1] = ds_read16<16 * kBK>(a_lane1 + aslot);
-            }
-            if (blk == 3) lgkm_wait<2>(B[3][0], B[3][1]);
-            if (blk == 4) {
-                lgkm_wait<0>(A[1][0], A[1][1]);
-                A[2][0] = ds_read16<32 * kBK>(a_lane0 + aslot);
-                A[2][1] = ds_read16<32 * kBK>(a_lane1 + aslot);
-            }
-            if (blk == 8) {
-                lgkm_wait<0>(A[2][0], A[2][1]);
-                A[3][0] = ds_read16<48 * kBK>(a_lane0 + aslot);
-                A[3][1] = ds_read16<48 * kBK>(a_lane1 + aslot);
-            }
-            if (blk == 12) lgkm_wait<0>(A[3][0], A[3][1]);
-            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi][0], B[ni][0], zero, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi][1], B[ni][1], c, 0, 0, 0);
-            if constexpr (QM != QUANT_STATIC) k = __builtin_amdgcn_mfma_f32_4x4x1f32(asel[mi], sv[ni], zerof, 0, 0, 0);
-        };
-        auto epilogue = [&](const v4i& c, const v4f& k, int blk) {
-            const int mi = blk >> 2, ni = blk & 3;
+        }
+        if (blk == 1) lgkm_wait<6>(B[1][0], B[1][1]);
+        if (blk == 2) lgkm_wait<4>(B[2][0], B[2][1]);
+        if (blk == 3) lgkm_wait<2>(B[3][0], B[3][1]);
+        if (blk == 4) lgkm_wait<0>(A[3][0], A[3][1]);
+#if defined(__HIP_DEVICE_COMPILE__)
+        if constexpr (!DBG) {
+            // issue order pinned (see the epilogue)
+            KQ_ASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=&v"(c) : "v"(A[mi][0]), "v"(B[ni][0]));
+            KQ_ASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(c) : "v"(A[mi][1]), "v"(B[ni][1]));
+            if constexpr (QM != QUANT_STATIC) KQ_ASM("v_mfma_f32_4x4x1_16b_f32 %0, %1, %2, 0" : "=&v"(k) : "v"(asel[mi]), "v"(sv[ni]));
+            return;
+        }
+#endif
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi][0], B[ni][0], zero, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi][1], B[ni][1], c, 0, 0, 0);
+        if constexpr (QM != QUANT_STATIC) k = __builtin_amdgcn_mfma_f32_4x4x1f32(asel[mi], sv[ni], zerof, 0, 0, 0);
+    };
+    auto epilogue = [&](const v4i& c, const v4f& k, int blk, int kt) {
+        const int mi = blk >> 2, ni = blk & 3;
+#if defined(__HIP_DEVICE_COMPILE__)
+        if constexpr (!DBG) {
+            // Inline assembly keeps this block's conversions and FMAs after the MFMAs of the next block (the
+            // compiler would pull them up behind their own MFMAs and stall on the results); by then at least ten
+            // instructions separate every MFMA result from its first VALU read, beyond the dependency window.
+            float t[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) KQ_ASM("v_cvt_f32_i32 %0, %1" : "=v"(t[r]) : "v"(c[r]));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int P = c[r];
-                if (DBG && a.dump) {
-                    const int row = m0 + wm * 64 + mi * 16 + 4 * L + r, col = col_nt[ni] * kTileRows + nn;
-                    if (row < a.M && col_nt[ni] < a.n_tiles && col < a.N)
-                        a.dump[(static_cast<std::int64_t>(row) * a.N + col) * a.groups + kt] = P;
-                }
                 const float kk = QM == QUANT_STATIC ? sv[ni] : k[r];
-                acc[mi][ni][r] = __builtin_fmaf(kk, static_cast<float>(P), acc[mi][ni][r]);
+                KQ_ASM("v_fmac_f32 %0, %1, %2" : "+v"(acc[mi][ni][r]) : "v"(kk), "v"(t[r]));
             }
-        };
-        v4i cp, cn;
-        v4f kp = zerof, kn4 = zerof;
-        Raw raw;
-        mfmas(0, cp, kp);
-#pragma unroll
-        for (int blk = 1; blk <= 16; ++blk) {
-            if (blk < 16) mfmas(blk, cn, kn4);
-            if (blk == 1 || blk == 3 || blk == 5 || blk == 7) issue_a(ka, s2, blk >> 1);
-            if (blk == 9) issue_raw(kb, s0);
-            if (blk == 11) issue_meta(ka, s2, kb, s0);
-            // step kt + 1's packed tiles (copied during step kt - 2) into B slot (kt + 1) % 2, read once every
-            // operand read of this step has returned (block 12) (after the last step: stale tiles into a slot
-            // nobody reads)
-            if (blk == 13) raw = unpack_read(s1, s1);
-            if (blk == 15) unpack_write(raw, (kt - kofs + 1) & 1);
-            epilogue(cp, kp, blk - 1);
-            cp = cn;
-            kp = kn4;
+            return;
         }
+#endif
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int P = c[r];
+            if (DBG && a.dump) {
+                const int row = m0 + wm * 64 + mi * 16 + 4 * L + r, col = col_nt[ni] * kTileRows + nn;
+                if (row < a.M && col_nt[ni] < a.n_tiles && col < a.N)
+                    a.dump[(static_cast<std::int64_t>(row) * a.N + col) * a.groups + kt] = P;
+            }
+            const float kk = QM == QUANT_STATIC ? sv[ni] : k[r];
+            acc[mi][ni][r] = __builtin_fmaf(kk, static_cast<float>(P), acc[mi][ni][r]);
+        }
+    };
+    auto sched_blocks = [&]() {
         if constexpr (!DBG) {
             // one block: 3 MFMAs (2 with static activations), then the 8 VALU of the previous block's epilogue
 #pragma unroll
-            for (int blk = 0; blk < 16; ++blk) {
+            for (int b = 0; b < 8; ++b) {
                 __builtin_amdgcn_sched_group_barrier(0x008, QM == QUANT_STATIC ? 2 : 3, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        s2 = s0;
-        s0 = s1;
+    };
+    v4i cp;  // MFMA results of the block whose epilogue is pending
+    v4f kp = zerof;
+    // First half of step kt (slot s1 = step kt + 1): blocks 0-7, step kt + 1's tiles unpacked into B slot
+    // (kt + 1) % 2, then the step's barrier.
+    auto phase1 = [&](int kt, int s1) {
+        v4i cn;
+        v4f kn4 = zerof;
+        Raw raw;
+        mfmas(0, cp, kp);
+#pragma unroll
+        for (int blk = 1; blk < 8; ++blk) {
+            mfmas(blk, cn, kn4);
+            if (blk == 4) raw = unpack_read(s1, s1);
+            if (blk == 6) unpack_write(raw, (kt - kofs + 1) & 1);
+            epilogue(cp, kp, blk - 1, kt);
+            cp = cn;
+            kp = kn4;
+        }
+        sched_blocks();
         // all LDS traffic of the loop is explicit: the wait covers it, so a bare barrier (no fence) suffices
         __builtin_amdgcn_s_waitcnt(kStepWait);
         __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Second half of step kt (slots s0 = step kt, s1 = step kt + 1): blocks 8-15; copies of step kt + 3 (activation
+    // codes, metadata) and kt + 4 (packed tiles, zero points); step kt + 1's operand registers read after their
+    // last use here (not after the last step: a read nobody waits for would land in a register by then reused).
+    auto phase2 = [&](int kt, int s0, int s1, bool next) {
+        const int k3 = clamp_k(kt + 3), k4 = clamp_k(kt + 4);
+        const std::uint32_t aslot1 = s1 * S::A_BYTES, mslot1 = s1 * S::META_BYTES;
+        const std::uint32_t bslot1 = ((kt - kofs + 1) & 1) * kBBytes;
+        v4i cn;
+        v4f kn4 = zerof;
+        if (next) {
+            read_meta(mslot1);
+            KQ_READ_A(0, aslot1);
+            KQ_READ_A(1, aslot1);
+        }
+#pragma unroll
+        for (int blk = 8; blk <= 16; ++blk) {
+            if (blk < 16) mfmas(blk, cn, kn4);
+            if (blk <= 11) issue_a(k3, s0, blk - 8);
+            if (blk == 12) {
+                issue_raw(k4, s1);
+                if (next) KQ_READ_A(2, aslot1);
+            }
+            if (blk == 13) {
+                issue_meta(k3, s0, k4, s1);
+                if (next) KQ_READ_B(0, bslot1);
+            }
+            if (next && blk == 14) KQ_READ_B(1, bslot1);
+            if (next && blk == 15) KQ_READ_B(2, bslot1);
+            if (next && blk == 16) {
+                KQ_READ_B(3, bslot1);
+                KQ_READ_A(3, aslot1);
+            }
+            epilogue(cp, kp, blk - 1, kt);
+            if (blk < 16) {
+                cp = cn;
+                kp = kn4;
+            }
+        }
+        sched_blocks();
+    };
+
+    // one iteration: second half of step kt, first half of step kt + 1 (its barrier ends the iteration), so every
+    // register read from LDS is complete before the loop's back edge
+    phase1(kofs, 1);
+    int s0 = 0, s1 = 1;  // ring slots (mod 3) of steps kt and kt + 1
+    for (int kt = kofs; kt < kend - 1; ++kt) {
+        const int s2 = s1 == 2 ? 0 : s1 + 1;
+        phase2(kt, s0, s1, true);
+        phase1(kt + 1, s2);
+        s0 = s1;
+        s1 = s2;
     }
+    phase2(kend - 1, s0, s1, false);
 #undef KQ_BSLOT
+#undef KQ_READ_A
+#undef KQ_READ_B
+    // no copy or read may still be in flight when the workgroup's LDS is handed to the next workgroup
+    __builtin_amdgcn_s_waitcnt(0);
 
     if (a.ksplit > 1) {
         // K-split: every range stores its fp32 partial tile, as [16 groups (mi, ni)][thread] of float4 so each store

@@ -1,0 +1,90 @@
+"""Static check of the device code: a register loaded by an inline-assembly LDS read (ds_read_*) is written when the
+data returns, so no instruction may touch it before an s_waitcnt lgkmcnt that covers the read. The compiler waits for
+its own loads, but not for these; a copy, spill or reuse of such a register before the wait reads or is overwritten
+by stale data (a dead read whose register was reused for a store address has faulted the GPU).
+
+Each HIP source is compiled for gfx950 to device assembly (same flags as kidi_amd/build.py) and every kernel is
+scanned in order: LDS operations queue in issue order, lgkmcnt(N) retires all but the newest N."""
+
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+SOURCES = ["kq_gemm.hip", "kq_decode.hip", "kq_skinny.hip", "kq_kernels.hip"]
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S"]
+
+
+def vgprs(text):
+    out = set()
+    for m in re.finditer(r"\bv\[(\d+):(\d+)\]|\bv(\d+)\b", text):
+        if m.group(3) is not None:
+            out.add(int(m.group(3)))
+        else:
+            out.update(range(int(m.group(1)), int(m.group(2)) + 1))
+    return out
+
+
+def hazards(asm: str):
+    """(kernel, line, instruction, pending read) for every touch of a register with an outstanding asm LDS read."""
+    found = []
+    for func in re.split(r"\n(?=_Z\w+:)", asm):
+        name = func.split(":", 1)[0]
+        if not name.startswith("_Z"):
+            continue
+        pending = []  # (instruction, destination registers) of LDS operations in issue order
+        in_asm = False
+        for i, line in enumerate(func.split("s_endpgm")[0].split("\n")):
+            if ";;#ASMSTART" in line:
+                in_asm = True
+            if ";;#ASMEND" in line:
+                in_asm = False
+            ins = line.split(";")[0].strip()
+            if not ins or ins.endswith(":") or ins.startswith("."):
+                continue
+            op = ins.split()[0]
+            if op == "s_waitcnt":
+                m = re.search(r"lgkmcnt\((\d+)\)", ins)
+                if m:
+                    del pending[:max(0, len(pending) - int(m.group(1)))]
+                continue
+            args = ins[len(op):]
+            used = vgprs(args)
+            for read, dest in pending:
+                if dest & used:
+                    found.append((name, i, ins, read))
+            if op.startswith(("ds_", "s_load", "s_buffer_load")):
+                dest = vgprs(args.split(",")[0]) if in_asm and op.startswith("ds_read") else set()
+                pending.append((ins, dest))
+    return found
+
+
+def test_checker_flags_a_read_reused_before_its_wait():
+    asm = "\n".join([
+        "_Zk:", ";;#ASMSTART", "ds_read_b128 v[4:7], v1 offset:0", ";;#ASMEND",
+        "v_mov_b32_e32 v5, 0", "s_waitcnt lgkmcnt(0)", "v_mov_b32_e32 v6, 0", "s_endpgm"])
+    assert [h[2] for h in hazards(asm)] == ["v_mov_b32_e32 v5, 0"]
+    ordered = asm.replace("v_mov_b32_e32 v5, 0\n", "")
+    assert hazards(ordered) == []
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
+def test_no_register_of_a_pending_lds_read_is_touched():
+    with tempfile.TemporaryDirectory() as tmp:
+        procs = []
+        for src in SOURCES:
+            out = os.path.join(tmp, src + ".s")
+            cmd = [HIPCC, *FLAGS, "-I", os.path.join(ROOT, "include"), os.path.join(ROOT, "kidi_amd", "csrc", src), "-o", out]
+            procs.append((src, out, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+        bad = []
+        for src, out, p in procs:
+            log, _ = p.communicate()
+            assert p.returncode == 0, log.decode(errors="replace")[-2000:]
+            with open(out) as f:
+                bad += [(src,) + h for h in hazards(f.read())]
+    assert not bad, "\n".join(f"{s} {k[:70]} line {i}: {ins!r} before the wait for {r!r}" for s, k, i, ins, r in bad[:10])
