@@ -1,9 +1,9 @@
 // Prefill projection (M > 16) of the MI355X quantized linear layer for 4-bit weights with g = 128 (symmetric or
 // with zero points) and K a multiple of 512: an activation quantizer and an int8 MFMA GEMM.
 //
-// quantize_rows_kernel: one wave per (row, 512 columns); lane = 8-column piece, the g/8 lanes of a group reduce
-//   max |x| and the code sum with DPP; codes go to [M_p][K] in the tiles' permuted order, block scales to
-//   [groups][M_p] (transposed so a GEMM stage copies one contiguous 1 KiB row of them).
+// quantize_rows_kernel: one lane per 32 columns of a row, a lane quad per group (max |x| reduced with DPP); codes go
+//   to [M_p][K] in the tiles' permuted order, block scales to [groups][M_p] (transposed so a GEMM stage copies one
+//   contiguous 1 KiB row of them).
 // gemm_i4_kernel: workgroup tile 256 (rows) x 128 (output columns = 8 weight row tiles), 8 waves of 64 x 64, one
 //   128-column k-step (= one 4-bit tile = one group) per iteration, operands in LDS rings:
 //     - activation codes: 32 direct-to-LDS copies of 1 KiB per step (buffer_load ... lds), lane addresses XOR-
@@ -130,20 +130,6 @@ template <int CTRL>
 __device__ __forceinline__ int dpp(int v) {
     return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
 }
-__device__ __forceinline__ int row16_max(int v) {  // max over 16-lane rows (float bits)
-    auto mx = [](int p, int q) { return __float_as_int(fmaxf(__int_as_float(p), __int_as_float(q))); };
-    v = mx(v, dpp<0xB1>(v));
-    v = mx(v, dpp<0x4E>(v));
-    v = mx(v, dpp<0x141>(v));
-    return mx(v, dpp<0x140>(v));
-}
-__device__ __forceinline__ int row16_sum(int v) {
-    v += dpp<0xB1>(v);
-    v += dpp<0x4E>(v);
-    v += dpp<0x141>(v);
-    return v + dpp<0x140>(v);
-}
-
 // Position of row m's block scale inside a [groups][M_p] row of the transposed scales: within each 64-row block,
 // row 16 q + t is stored at 4 t + q, so the 4 rows 16 apart that one GEMM lane scales are adjacent.
 __device__ __forceinline__ int scale_slot(int m) { return (m & ~63) | ((m & 15) << 2) | ((m >> 4) & 3); }
@@ -158,55 +144,115 @@ struct QRowArgs {
     std::int32_t* sum_t; // [K/128][M_p] (optional)
 };
 
-// g = 128: a group is one 16-lane row of the wave.
-template <int QM>
+// g = 128. One lane per 32 columns of a row: the pieces [16 a, 16 a + 16) and [32 + 16 a, 32 + 16 a + 16) of 64-column
+// block b, lane unit j = 2 b + a. Their codes fill 32 contiguous bytes of the permuted row (column 32 h + 8 L + i of
+// a 64-column block at 16 L + 8 h + i), and a group is one lane quad (2 DPP steps reduce it). Codes are packed with
+// v_cvt_pk_u8_f32 on rint(x * inverse) + 128 (an integer in [1, 255]; calibrated codes clamped to [-128, 127]
+// first), then the bias is flipped off per byte.
+template <int QM, bool F32>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(QRowArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int wid = static_cast<int>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    const int chunks = a.K / 512;
-    const int m = wid / chunks, c = wid % chunks;
-    if (m >= a.M_p) return;
+    const int units = a.K / 32;  // lanes per row (a multiple of 16: rows never share a lane quad)
+    const int t = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    const int m = t / units, j = t - m * units;
+    if (m >= a.M_p) return;  // whole waves (M_p * units is a multiple of 64)
     const bool live = m < a.M;
-    const __amdgpu_buffer_rsrc_t xr = rsrc(a.x, static_cast<std::uint32_t>(a.M) * a.K * (a.x_f32 ? 4 : 2));
-    const std::uint32_t e = static_cast<std::uint32_t>(m) * a.K + c * 512 + 8 * lane;
-    const std::uint32_t off = live ? (a.x_f32 ? 4 * e : 2 * e) : kOob;
-    const uint4 r0 = ld16(xr, off);
-    const uint4 r1 = ld16(xr, a.x_f32 ? off + 16 : off);
-    float v[8];
-    if (a.x_f32) {
-        const std::uint32_t w8[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+    const int col0 = 64 * (j >> 1) + 16 * (j & 1);
+    constexpr std::uint32_t ES = F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t xr = rsrc(a.x, static_cast<std::uint32_t>(a.M) * a.K * ES);
+    const std::uint32_t e0 = (static_cast<std::uint32_t>(m) * a.K + col0) * ES;
+    float v[32];  // v[0..15]: columns col0 + [0, 16); v[16..31]: col0 + 32 + [0, 16)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w8[i]);
-    } else {
-        const std::uint32_t w4[4] = {r0.x, r0.y, r0.z, r0.w};
+    for (int p = 0; p < 2; ++p) {
+        const std::uint32_t off = live ? e0 + p * 32 * ES : kOob;
+        if constexpr (F32) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[2 * i] = __uint_as_float(w4[i] << 16);
-            v[2 * i + 1] = __uint_as_float(w4[i] & 0xFFFF0000u);
+            for (int i = 0; i < 4; ++i) {
+                const uint4 r = ld16(xr, off + 16 * i);
+                v[16 * p + 4 * i] = __uint_as_float(r.x);
+                v[16 * p + 4 * i + 1] = __uint_as_float(r.y);
+                v[16 * p + 4 * i + 2] = __uint_as_float(r.z);
+                v[16 * p + 4 * i + 3] = __uint_as_float(r.w);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint4 r = ld16(xr, off + 16 * i);
+                const std::uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    v[16 * p + 8 * i + 2 * d] = __uint_as_float(w4[d] << 16);
+                    v[16 * p + 8 * i + 2 * d + 1] = __uint_as_float(w4[d] & 0xFFFF0000u);
+                }
+            }
         }
     }
     float mx = 0.F, mn = 0.F;
     if constexpr (QM != QUANT_STATIC) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) quant_stat(QM, v[i], mx, mn);
-        mx = __int_as_float(row16_max(__float_as_int(mx)));
+        for (int i = 0; i < 32; ++i) quant_stat(QM, v[i], mx, mn);
+        mx = fmaxf(mx, __int_as_float(dpp<0xB1>(__float_as_int(mx))));
+        mx = fmaxf(mx, __int_as_float(dpp<0x4E>(__float_as_int(mx))));
     }
     const QuantBlock qb = quant_block(QM, mx, mn, a.input_scale, live);
-    std::uint32_t lo = 0, hi = 0;
-    int total = 0;
+    // output order: columns col0 + [0, 8), col0 + 32 + [0, 8), col0 + [8, 16), col0 + 32 + [8, 16)
+    constexpr int kSrc[4] = {0, 16, 8, 24};
+    std::uint32_t out[8];
+    if constexpr (QM == QUANT_STATIC) {
+        // calibrated: rint(x / input_scale) clamped to [-128, 127], + 128 packed as unsigned bytes, bias flipped off
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int code = quant_code(QM, v[i], qb, a.input_scale);
-        total += code;
-        if (i < 4) lo |= (static_cast<std::uint32_t>(code) & 0xFFu) << (8 * i);
-        else hi |= (static_cast<std::uint32_t>(code) & 0xFFu) << (8 * (i - 4));
+        for (int w = 0; w < 8; ++w) {
+            std::uint32_t d = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float c = fminf(fmaxf(__builtin_rintf(v[kSrc[w >> 1] + 4 * (w & 1) + i] / a.input_scale), -128.F), 127.F);
+                d = __builtin_amdgcn_cvt_pk_u8_f32(c + 128.F, i, d);
+            }
+            out[w] = d ^ 0x80808080u;
+        }
+    } else {
+        // dynamic: |x * inverse| <= 127 (1 + 2^-24) rounds to at most 127 (no clamp). Adding 1.5 * 2^23 rounds
+        // x * inverse to an integer (round to nearest even, as rint) held in the low mantissa bits, so the low byte
+        // is the code in two's complement; v_perm gathers four of them.
+        constexpr float kMagic = 12582912.F;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            std::uint32_t u[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) u[i] = __float_as_uint(v[kSrc[w >> 1] + 4 * (w & 1) + i] * qb.inverse + kMagic);
+            const std::uint32_t lo = __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(u[3], u[2], 0x0c0c0400u);
+            out[w] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        }
     }
-    *reinterpret_cast<uint2*>(a.q + static_cast<std::int64_t>(m) * a.K + c * 512 + act_position(8 * lane)) = make_uint2(lo, hi);
-    total = row16_sum(total);
-    if ((lane & 15) == 0) {
-        const std::int64_t o = static_cast<std::int64_t>(c * 4 + (lane >> 4)) * a.M_p + scale_slot(m);
+    std::int8_t* dst = a.q + static_cast<std::int64_t>(m) * a.K + 64 * (j >> 1) + 32 * (j & 1);
+    *reinterpret_cast<uint4*>(dst) = make_uint4(out[0], out[1], out[2], out[3]);
+    *reinterpret_cast<uint4*>(dst + 16) = make_uint4(out[4], out[5], out[6], out[7]);
+    // code sums (parity instrumentation only): from the packed bytes
+    const bool sums = a.sum_t != nullptr;
+    int q = 0;
+    if (sums) {
+#pragma unroll
+        for (int w = 0; w < 8; ++w)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q += static_cast<std::int8_t>((out[w] >> (8 * i)) & 0xFFu);
+        q += dpp<0xB1>(q);
+        q += dpp<0x4E>(q);
+    }
+    if ((j & 3) == 0) {
+        const std::int64_t o = static_cast<std::int64_t>(j >> 2) * a.M_p + scale_slot(m);
         a.scale_t[o] = qb.s;
-        if (a.sum_t) a.sum_t[o] = total;
+        if (sums) a.sum_t[o] = q;
+    }
+}
+
+// launch over M_p rows x K / 32 lanes
+inline void launch_quantize_rows(const QRowArgs& q, bool calibrated, bool x_f32, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(static_cast<std::int64_t>(q.M_p) * (q.K / 32) / 256)), block(256);
+    if (calibrated) {
+        if (x_f32) hipLaunchKernelGGL((quantize_rows_kernel<dev::QUANT_STATIC, true>), grid, block, 0, stream, q);
+        else hipLaunchKernelGGL((quantize_rows_kernel<dev::QUANT_STATIC, false>), grid, block, 0, stream, q);
+    } else {
+        if (x_f32) hipLaunchKernelGGL((quantize_rows_kernel<dev::QUANT_DYN_SYM, true>), grid, block, 0, stream, q);
+        else hipLaunchKernelGGL((quantize_rows_kernel<dev::QUANT_DYN_SYM, false>), grid, block, 0, stream, q);
     }
 }
 
@@ -864,10 +910,7 @@ hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_
     q.scale_t = act.scale;
     q.sum_t = nullptr;
     const GemmPlan plan = gemm_i4_plan(w, c.M, c.gelu_gate);
-    const int waves = M_p * (K / 512);
-    const dim3 qgrid(static_cast<unsigned>((waves + 3) / 4)), qblock(256);
-    if (stat) hipLaunchKernelGGL(quantize_rows_kernel<dev::QUANT_STATIC>, qgrid, qblock, 0, stream, q);
-    else hipLaunchKernelGGL(quantize_rows_kernel<dev::QUANT_DYN_SYM>, qgrid, qblock, 0, stream, q);
+    launch_quantize_rows(q, stat, q.x_f32 != 0, stream);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
 
@@ -959,10 +1002,7 @@ hipError_t launch_gemm_i4_quantize_dump(const LinearCall& c, const ActBuffers& a
     q.q = act.q;
     q.scale_t = act.scale;
     q.sum_t = act.sum;
-    const int waves = M_p * (K / 512);
-    const dim3 qgrid(static_cast<unsigned>((waves + 3) / 4)), qblock(256);
-    if (c.path == PATH_SYMMETRIC) hipLaunchKernelGGL(quantize_rows_kernel<dev::QUANT_STATIC>, qgrid, qblock, 0, stream, q);
-    else hipLaunchKernelGGL(quantize_rows_kernel<dev::QUANT_DYN_SYM>, qgrid, qblock, 0, stream, q);
+    launch_quantize_rows(q, c.path == PATH_SYMMETRIC, q.x_f32 != 0, stream);
     const std::int64_t total = static_cast<std::int64_t>(M) * K;
     if (codes) hipLaunchKernelGGL(unpermute_rows_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, act.q, M, K, codes);
     const int groups = K / 128;
