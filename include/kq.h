@@ -132,6 +132,32 @@ kq_status kq_weight_pack_concat(const kq_pack_desc* descs, int32_t count, void* 
  * (Context::gelu_gate, ops/context.cpp:957-963; formula eager_test.cpp:444-452). */
 kq_status kq_packed_linear_gelu_gate(const kq_weight* weight, const kq_linear_args* args, void* stream);
 
+/* Gated feed-forward of one decoder layer: Context::gated_feed_forward (src/kidi/ops/context.cpp:970-996) ->
+ * Operation::GATED_FEED_FORWARD, run by PackedFeedForward (runtime/ynn/operators.cpp:1321-1517) for calibrated
+ * inputs. `gate_up` holds [gate rows; up rows] (2*I rows, K columns), `down` holds K rows of I columns, equal bits.
+ *   h [M, I] = act(gate) * up, where [gate | up] is the gate/up projection of x with gate_up_input_scale and
+ *              gate_up_output_scale, act = GELU-tanh or (silu != 0, attributes[6]) SiLU;
+ *   y [M, K] = the down projection of h with down_input_scale (h's int8 codes clamp(rint(h / down_input_scale)),
+ *              PackedFeedForward's mid tiles) and down_output_scale.
+ * Zero input scales select dynamic activations, as the composed form Context::gated_feed_forward runs outside
+ * CHECKPOINT precision (:977-984). Asynchronous on `stream`. */
+typedef struct kq_ffn_args {
+    const void* x;              /* device [M, K] */
+    kq_dtype x_dtype;           /* KQ_F32 or KQ_BF16 */
+    int64_t m;
+    float gate_up_input_scale;  /* OperatorSpec::epsilon */
+    float gate_up_output_scale; /* bit_cast of attributes[3] */
+    float down_input_scale;     /* attributes[4] */
+    float down_output_scale;    /* attributes[5] */
+    int32_t silu;               /* attributes[6] */
+    float* y;                   /* device [M, K] F32 */
+    void* workspace;            /* device scratch of kq_ffn_workspace_size() bytes, or NULL (library buffer) */
+    size_t workspace_bytes;
+} kq_ffn_args;
+
+size_t kq_ffn_workspace_size(const kq_weight* gate_up, const kq_weight* down, int64_t m);
+kq_status kq_gated_feed_forward(const kq_weight* gate_up, const kq_weight* down, const kq_ffn_args* args, void* stream);
+
 /* ---- parity instrumentation (same kernels as kq_packed_linear, with an extra store) --------------------- */
 
 /* Activation quantization exactly as the projection performs it: codes int8 [M, K] (natural k order),

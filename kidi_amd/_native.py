@@ -24,7 +24,7 @@ EXPORTS = (
     "kq_last_error", "kq_version", "kq_arch", "kq_weight_pack", "kq_weight_free", "kq_weight_info",
     "kq_select_path", "kq_linear_workspace_size", "kq_packed_linear", "kq_weight_pack_concat",
     "kq_packed_linear_gelu_gate", "kq_debug_quantize", "kq_debug_partials", "kq_layout_bytes",
-    "kq_layout_encode_host", "kq_layout_decode_host",
+    "kq_layout_encode_host", "kq_layout_decode_host", "kq_ffn_workspace_size", "kq_gated_feed_forward",
 )
 
 
@@ -41,6 +41,22 @@ class PackDesc(ctypes.Structure):
         ("zeros", ctypes.c_void_p),
         ("zeros_dtype", ctypes.c_int),
         ("memory", ctypes.c_int),
+    ]
+
+
+class FfnArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("x_dtype", ctypes.c_int),
+        ("m", ctypes.c_int64),
+        ("gate_up_input_scale", ctypes.c_float),
+        ("gate_up_output_scale", ctypes.c_float),
+        ("down_input_scale", ctypes.c_float),
+        ("down_output_scale", ctypes.c_float),
+        ("silu", ctypes.c_int32),
+        ("y", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -97,6 +113,10 @@ def load() -> ctypes.CDLL:
     L.kq_packed_linear.restype = ctypes.c_int
     L.kq_packed_linear_gelu_gate.argtypes = [vp, ctypes.POINTER(LinearArgs), vp]
     L.kq_packed_linear_gelu_gate.restype = ctypes.c_int
+    L.kq_ffn_workspace_size.argtypes = [vp, vp, i64]
+    L.kq_ffn_workspace_size.restype = sz
+    L.kq_gated_feed_forward.argtypes = [vp, vp, ctypes.POINTER(FfnArgs), vp]
+    L.kq_gated_feed_forward.restype = ctypes.c_int
     L.kq_debug_quantize.argtypes = [vp, vp, ctypes.c_int, i64, f32, vp, vp, vp, vp, vp]
     L.kq_debug_quantize.restype = ctypes.c_int
     L.kq_debug_partials.argtypes = [vp, ctypes.POINTER(LinearArgs), vp, vp]

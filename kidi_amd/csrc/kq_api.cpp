@@ -94,6 +94,7 @@ struct Scratch {
 std::mutex g_scratch_mutex;
 std::map<int, Scratch> g_scratch;
 std::map<int, Scratch> g_gelu_scratch;
+std::map<int, Scratch> g_ffn_scratch;
 
 kq_status device_scratch(std::map<int, Scratch>& pool, std::size_t bytes, void** out) {
     int dev = 0;
@@ -421,6 +422,36 @@ kq_status run_call(kq::LinearCall& c, const kq_linear_args* args, std::size_t ws
     return KQ_OK;
 }
 
+// Gated feed-forward workspace: h [M, I], the full gate/up projection [M, 2I] (SiLU gating runs as its own pass),
+// then the larger of the two projections' workspaces (they run one after the other on the stream).
+struct FfnLayout {
+    std::size_t h = 0, full = 0, proj = 0;
+    std::size_t total() const { return h + full + proj; }
+};
+FfnLayout ffn_layout(const kq::Weight& gu, const kq::Weight& dn, std::int64_t M) {
+    FfnLayout l;
+    const std::int64_t I = gu.geo.rows / 2;
+    l.h = align_up(static_cast<std::size_t>(M * I) * 4);
+    l.full = align_up(static_cast<std::size_t>(M * gu.geo.rows) * 4);
+    l.proj = std::max(kq::workspace_bytes(gu, M), kq::workspace_bytes(dn, M));
+    return l;
+}
+
+kq_status ffn_validate(const kq_weight* gate_up, const kq_weight* down, const kq_ffn_args* a) {
+    if (!gate_up || !down || !a) return fail(KQ_INVALID_ARGUMENT, "null weight or arguments");
+    const kq::Weight& gu = *as_weight(gate_up);
+    const kq::Weight& dn = *as_weight(down);
+    if (gu.geo.rows % 2 || dn.geo.cols != gu.geo.rows / 2 || dn.geo.rows != gu.geo.cols || dn.geo.bits != gu.geo.bits)
+        return fail(KQ_INVALID_ARGUMENT, "gated feed-forward weights must be gate_up [2I, K] and down [K, I] of equal bits");
+    for (float v : {a->gate_up_input_scale, a->gate_up_output_scale, a->down_input_scale, a->down_output_scale})
+        if (!std::isfinite(v) || v < 0) return fail(KQ_INVALID_ARGUMENT, "invalid calibrated projection scales");
+    if (a->m < 0) return fail(KQ_INVALID_ARGUMENT, "negative row count");
+    if (a->x_dtype != KQ_F32 && a->x_dtype != KQ_BF16) return fail(KQ_INVALID_ARGUMENT, "feed-forward input must be F32 or BF16");
+    if (a->m > 0 && (!a->x || !a->y)) return fail(KQ_INVALID_ARGUMENT, "null input or output");
+    if (gu.device != dn.device) return fail(KQ_INVALID_ARGUMENT, "weights were packed on different devices");
+    return KQ_OK;
+}
+
 }  // namespace
 
 namespace kq {
@@ -527,6 +558,53 @@ kq_status kq_packed_linear_gelu_gate(const kq_weight* weight, const kq_linear_ar
     std::size_t ws = 0;
     if (kq_status s = prepare_call(weight, args, true, c, &ws); s != KQ_OK) return s;
     return run_call(c, args, ws, static_cast<hipStream_t>(stream));
+}
+
+size_t kq_ffn_workspace_size(const kq_weight* gate_up, const kq_weight* down, int64_t m) {
+    if (!gate_up || !down || m < 0) return 0;
+    return ffn_layout(*as_weight(gate_up), *as_weight(down), m).total();
+}
+
+kq_status kq_gated_feed_forward(const kq_weight* gate_up, const kq_weight* down, const kq_ffn_args* args, void* stream) {
+    if (kq_status s = ffn_validate(gate_up, down, args); s != KQ_OK) return s;
+    if (args->m == 0) return KQ_OK;
+    const kq::Weight& gu = *as_weight(gate_up);
+    const kq::Weight& dn = *as_weight(down);
+    const FfnLayout l = ffn_layout(gu, dn, args->m);
+    void* ws = args->workspace;
+    if (ws) {
+        if (args->workspace_bytes < l.total()) return fail(KQ_INVALID_ARGUMENT, "workspace too small");
+    } else if (kq_status s = device_scratch(g_ffn_scratch, l.total(), &ws); s != KQ_OK) {
+        return s;
+    }
+    auto* base = static_cast<std::uint8_t*>(ws);
+    float* h = reinterpret_cast<float*>(base);
+    float* full = reinterpret_cast<float*>(base + l.h);
+    void* proj = base + l.h + l.full;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    kq_linear_args a{};
+    a.x = args->x;
+    a.x_dtype = args->x_dtype;
+    a.m = args->m;
+    a.input_scale = args->gate_up_input_scale;
+    a.output_scale = args->gate_up_output_scale;
+    a.workspace = proj;
+    a.workspace_bytes = l.proj;
+    if (args->silu) {
+        a.y = full;
+        if (kq_status s = kq_packed_linear(gate_up, &a, stream); s != KQ_OK) return s;
+        if (hipError_t e = kq::launch_silu_gate(full, args->m, gu.geo.rows / 2, h, st); e != hipSuccess)
+            return hip_fail(e, "SiLU gate launch");
+    } else {
+        a.y = h;
+        if (kq_status s = kq_packed_linear_gelu_gate(gate_up, &a, stream); s != KQ_OK) return s;
+    }
+    a.x = h;
+    a.x_dtype = KQ_F32;
+    a.input_scale = args->down_input_scale;
+    a.output_scale = args->down_output_scale;
+    a.y = args->y;
+    return kq_packed_linear(down, &a, stream);
 }
 
 kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_dtype, int64_t m, float input_scale,

@@ -96,6 +96,7 @@ ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base);
 hipError_t launch_quantize(const LinearCall& c, hipStream_t stream);
 hipError_t launch_linear(const LinearCall& c, hipStream_t stream);
 hipError_t launch_gelu_gate(const float* in, std::int64_t M, std::int64_t I, float* out, hipStream_t stream);
+hipError_t launch_silu_gate(const float* in, std::int64_t M, std::int64_t I, float* out, hipStream_t stream);
 hipError_t launch_unpermute_codes(const Weight& w, const ActBuffers& act, std::int64_t M, std::int8_t* codes,
                                   hipStream_t stream);
 hipError_t launch_copy_block_stats(const Weight& w, const ActBuffers& act, std::int64_t M, float* scales,

@@ -762,6 +762,15 @@ __global__ __launch_bounds__(256) void gelu_gate_kernel(const float* in, std::in
     out[id] = gelu_tanh(in[m * 2 * I + i]) * in[m * 2 * I + I + i];
 }
 
+// SiLU gating h = g / (1 + exp(-g)) * up (Context::silu_multiply, ops/context.cpp:964-969; eager_test.cpp:176-179)
+__global__ __launch_bounds__(256) void silu_gate_kernel(const float* in, std::int64_t M, std::int64_t I, float* out) {
+    const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= M * I) return;
+    const std::int64_t m = id / I, i = id % I;
+    const float g = in[m * 2 * I + i];
+    out[id] = g / (1.F + expf(-g)) * in[m * 2 * I + I + i];
+}
+
 __global__ __launch_bounds__(256) void unpermute_kernel(const std::int8_t* q, std::int64_t M, std::int64_t K,
                                                         std::int64_t cols_p, std::int8_t* codes) {
     const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -906,6 +915,12 @@ hipError_t launch_linear(const LinearCall& c, hipStream_t stream) {
 hipError_t launch_gelu_gate(const float* in, std::int64_t M, std::int64_t I, float* out, hipStream_t stream) {
     const std::int64_t total = M * I;
     hipLaunchKernelGGL(gelu_gate_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, in, M, I, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_gate(const float* in, std::int64_t M, std::int64_t I, float* out, hipStream_t stream) {
+    const std::int64_t total = M * I;
+    hipLaunchKernelGGL(silu_gate_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, in, M, I, out);
     return hipGetLastError();
 }
 

@@ -170,6 +170,34 @@ class DeviceWeight:
         return codes, s, q, z
 
 
+def gated_feed_forward(gate_up: DeviceWeight, down: DeviceWeight, x: torch.Tensor, gate_up_input_scale: float,
+                       gate_up_output_scale: float, down_input_scale: float, down_output_scale: float,
+                       silu: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """y [..., K] = down(act(gate) * up) of packed weights gate_up [2I, K] and down [K, I] (kq_gated_feed_forward)."""
+    if x.dim() < 1 or x.shape[-1] != gate_up.cols:
+        raise Failure("INVALID_ARGUMENT", "gated feed-forward input shape mismatch")
+    x2 = x.reshape(-1, gate_up.cols).contiguous()
+    m = x2.shape[0]
+    y = out if out is not None else torch.empty((m, down.rows), dtype=torch.float32, device=x.device)
+    L = N.load()
+    ws_bytes = L.kq_ffn_workspace_size(gate_up.handle, down.handle, m)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    a = N.FfnArgs()
+    a.x = x2.data_ptr()
+    a.x_dtype = N.KQ_BF16 if x2.dtype == torch.bfloat16 else (N.KQ_F32 if x2.dtype == torch.float32 else 99)
+    a.m = m
+    a.gate_up_input_scale = gate_up_input_scale
+    a.gate_up_output_scale = gate_up_output_scale
+    a.down_input_scale = down_input_scale
+    a.down_output_scale = down_output_scale
+    a.silu = int(bool(silu))
+    a.y = y.data_ptr()
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = ws_bytes
+    _raise(L.kq_gated_feed_forward(gate_up.handle, down.handle, ctypes.byref(a), _stream()))
+    return y.reshape(*x.shape[:-1], down.rows)
+
+
 def _identity(t: torch.Tensor | None):
     if t is None:
         return None
@@ -245,4 +273,31 @@ class Context:
         host = not input.is_cuda
         x = input.to(self.device) if host else input
         y = dw.linear(x, input_scale, output_scale, gelu_gate=True)
+        return y.cpu() if host else y
+
+    def gated_feed_forward(self, input: torch.Tensor, gate_up_weight: torch.Tensor, gate_up_scales: torch.Tensor,
+                           down_weight: torch.Tensor, down_scales: torch.Tensor, bits: int, input_size: int,
+                           intermediate_size: int, gate_up_input_scale: float, gate_up_output_scale: float,
+                           down_input_scale: float, down_output_scale: float, silu: bool = False) -> torch.Tensor:
+        """Context::gated_feed_forward (ops/context.cpp:970-996): per-channel packed gate_up [2I, K] and down [K, I]
+        (groups of input_size and intermediate_size columns, as the composed form passes them), GELU-tanh or SiLU
+        gating between, F32 [..., K] output."""
+        for v in (gate_up_input_scale, gate_up_output_scale, down_input_scale, down_output_scale):
+            if not math.isfinite(v) or v < 0:
+                raise Failure("INVALID_ARGUMENT", "invalid calibrated projection scales")
+        if input_size <= 0 or intermediate_size <= 0 or input.dim() < 2 or input.shape[-1] != input_size:
+            raise Failure("INVALID_ARGUMENT", "gated feed-forward shape mismatch")
+        if gate_up_weight.dim() != 2 or gate_up_weight.shape[0] != 2 * intermediate_size:
+            raise Failure("INVALID_ARGUMENT", "gated feed-forward shape mismatch")
+        self._validate(input, gate_up_weight, gate_up_scales, bits, input_size, gate_up_input_scale, gate_up_output_scale)
+        hidden = torch.empty((1, intermediate_size), dtype=torch.float32)  # h is F32 (shape check only)
+        self._validate(hidden, down_weight, down_scales, bits, intermediate_size, down_input_scale, down_output_scale)
+        if down_weight.shape[0] != input_size:
+            raise Failure("INVALID_ARGUMENT", "gated feed-forward shape mismatch")
+        gu = self._prepare(gate_up_weight, gate_up_scales, bits, input_size, None)
+        dn = self._prepare(down_weight, down_scales, bits, intermediate_size, None)
+        host = not input.is_cuda
+        x = input.to(self.device) if host else input
+        y = gated_feed_forward(gu, dn, x, gate_up_input_scale, gate_up_output_scale, down_input_scale,
+                               down_output_scale, silu)
         return y.cpu() if host else y

@@ -23,6 +23,7 @@
 //                           PARITY UNPINNED beyond its closed form (no reference test hits it with a tight
 //                           expected value); portable float path pinned to 1e-3 / 0.05 by eager_test.cpp:300-378.
 //   kqr_gelu_tanh           pinned by eager_test.cpp:431-452 (formula to 1e-5 and exact saturation values).
+//   kqr_silu_gate           pinned by eager_test.cpp:167-186 (g / (1 + exp(-g)) * up to 1e-5).
 //
 // Floating point: compiled with -ffp-contract=off so every a*b+c rounds twice, as ISO C++ evaluation does.
 
@@ -492,6 +493,17 @@ void kqr_gelu_gate(const float* gate_up, std::int64_t rows, std::int64_t width, 
             const float u = gate_up[r * 2 * width + width + i];
             const float inner = k0 * (g + 0.044715F * g * g * g);
             out[r * width + i] = 0.5F * g * (1.F + std::tanh(inner)) * u;
+        }
+}
+
+// SiLU gating h = g / (1 + exp(-g)) * up over [rows, 2*width] halves (Context::silu_gate / silu_multiply,
+// ops/context.cpp:964-969; formula eager_test.cpp:176-179).
+void kqr_silu_gate(const float* gate_up, std::int64_t rows, std::int64_t width, float* out) {
+    for (std::int64_t r = 0; r < rows; ++r)
+        for (std::int64_t i = 0; i < width; ++i) {
+            const float g = gate_up[r * 2 * width + i];
+            const float u = gate_up[r * 2 * width + width + i];
+            out[r * width + i] = g / (1.F + std::exp(-g)) * u;
         }
 }
 

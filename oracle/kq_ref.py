@@ -55,6 +55,8 @@ def lib() -> ctypes.CDLL:
         L.kqr_packed_linear.restype = i32
         L.kqr_gelu_gate.argtypes = [vp, i64, i64, vp]
         L.kqr_gelu_gate.restype = None
+        L.kqr_silu_gate.argtypes = [vp, i64, i64, vp]
+        L.kqr_silu_gate.restype = None
         _lib = L
     return _lib
 
@@ -198,6 +200,33 @@ def gelu_gate(gate_up: np.ndarray) -> np.ndarray:
     out = np.zeros(g.shape[:-1] + (width,), np.float32)
     lib().kqr_gelu_gate(_p(g), rows, width, _p(out))
     return out
+
+
+def silu_gate(gate_up: np.ndarray) -> np.ndarray:
+    """g / (1 + exp(-g)) * up over [..., 2I] halves (ops/context.cpp:964-969, eager_test.cpp:176-179)."""
+    g = np.ascontiguousarray(gate_up, dtype=np.float32)
+    rows = g.size // g.shape[-1]
+    width = g.shape[-1] // 2
+    out = np.zeros(g.shape[:-1] + (width,), np.float32)
+    lib().kqr_silu_gate(_p(g), rows, width, _p(out))
+    return out
+
+
+def gated_feed_forward(x: np.ndarray, gate_up_values: np.ndarray, gate_up_scales: np.ndarray, down_values: np.ndarray,
+                       down_scales: np.ndarray, bits: int, gate_up_group: int, down_group: int,
+                       gate_up_input_scale: float, gate_up_output_scale: float, down_input_scale: float,
+                       down_output_scale: float, silu: bool = False, gate_up_zero_points=None, down_zero_points=None,
+                       x_bf16: bool = False, threads: int = 1):
+    """Context::gated_feed_forward as its composed form (ops/context.cpp:977-984): the gate/up projection (rows
+    [gate; up]), GELU-tanh or SiLU gating, then the down projection of h (whose calibrated codes are
+    clamp(rint(h / down_input_scale)), what PackedFeedForward's mid tiles hold, runtime/ynn/operators.cpp:1437-1444).
+    Returns (y, h)."""
+    gu, _ = packed_linear(x, gate_up_values, gate_up_scales, bits, gate_up_group, gate_up_input_scale,
+                          gate_up_output_scale, zero_points=gate_up_zero_points, x_bf16=x_bf16, threads=threads)
+    h = silu_gate(gu) if silu else gelu_gate(gu)
+    y, _ = packed_linear(h, down_values, down_scales, bits, down_group, down_input_scale, down_output_scale,
+                         zero_points=down_zero_points, threads=threads)
+    return y, h
 
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
