@@ -158,6 +158,21 @@ typedef struct kq_ffn_args {
 size_t kq_ffn_workspace_size(const kq_weight* gate_up, const kq_weight* down, int64_t m);
 kq_status kq_gated_feed_forward(const kq_weight* gate_up, const kq_weight* down, const kq_ffn_args* args, void* stream);
 
+/* Greedy token: GREEDY_TOKEN (GreedyToken, runtime/ynn/operators.cpp:117-178; Context::greedy_token). tokens[r]
+ * is the first index of the maximum of row r of logits [rows, width] (device F32), or -1 when the row holds a NaN or
+ * an infinity (tests/kidi/layers/eager_test.cpp:231-252). tokens: device I32 [rows]. width must be positive. */
+size_t kq_greedy_workspace_size(int64_t rows, int64_t width);
+kq_status kq_greedy_token(const float* logits, int64_t rows, int64_t width, int32_t* tokens, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* The output head fused with greedy selection (the step after the head, Context::greedy_token on
+ * Context::packed_linear's logits): tokens [M] (device I32) of the projection kq_packed_linear computes. args->y
+ * may be NULL (the logits are then not stored). For decode shapes (M <= 8) each workgroup of the projection reduces
+ * its logits on chip; other shapes compute the logits, then select. args->workspace, when given, must hold
+ * kq_greedy_linear_workspace_size() bytes. No counterpart call exists in the reference; it composes the two ops. */
+size_t kq_greedy_linear_workspace_size(const kq_weight* weight, int64_t m);
+kq_status kq_packed_linear_greedy(const kq_weight* weight, const kq_linear_args* args, int32_t* tokens, void* stream);
+
 /* ---- parity instrumentation (same kernels as kq_packed_linear, with an extra store) --------------------- */
 
 /* Activation quantization exactly as the projection performs it: codes int8 [M, K] (natural k order),

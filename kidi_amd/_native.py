@@ -25,6 +25,7 @@ EXPORTS = (
     "kq_select_path", "kq_linear_workspace_size", "kq_packed_linear", "kq_weight_pack_concat",
     "kq_packed_linear_gelu_gate", "kq_debug_quantize", "kq_debug_partials", "kq_layout_bytes",
     "kq_layout_encode_host", "kq_layout_decode_host", "kq_ffn_workspace_size", "kq_gated_feed_forward",
+    "kq_greedy_workspace_size", "kq_greedy_token", "kq_greedy_linear_workspace_size", "kq_packed_linear_greedy",
 )
 
 
@@ -117,6 +118,14 @@ def load() -> ctypes.CDLL:
     L.kq_ffn_workspace_size.restype = sz
     L.kq_gated_feed_forward.argtypes = [vp, vp, ctypes.POINTER(FfnArgs), vp]
     L.kq_gated_feed_forward.restype = ctypes.c_int
+    L.kq_greedy_workspace_size.argtypes = [i64, i64]
+    L.kq_greedy_workspace_size.restype = sz
+    L.kq_greedy_token.argtypes = [vp, i64, i64, vp, vp, sz, vp]
+    L.kq_greedy_token.restype = ctypes.c_int
+    L.kq_greedy_linear_workspace_size.argtypes = [vp, i64]
+    L.kq_greedy_linear_workspace_size.restype = sz
+    L.kq_packed_linear_greedy.argtypes = [vp, ctypes.POINTER(LinearArgs), vp, vp]
+    L.kq_packed_linear_greedy.restype = ctypes.c_int
     L.kq_debug_quantize.argtypes = [vp, vp, ctypes.c_int, i64, f32, vp, vp, vp, vp, vp]
     L.kq_debug_quantize.restype = ctypes.c_int
     L.kq_debug_partials.argtypes = [vp, ctypes.POINTER(LinearArgs), vp, vp]

@@ -95,6 +95,7 @@ std::mutex g_scratch_mutex;
 std::map<int, Scratch> g_scratch;
 std::map<int, Scratch> g_gelu_scratch;
 std::map<int, Scratch> g_ffn_scratch;
+std::map<int, Scratch> g_greedy_scratch;
 
 kq_status device_scratch(std::map<int, Scratch>& pool, std::size_t bytes, void** out) {
     int dev = 0;
@@ -452,6 +453,21 @@ kq_status ffn_validate(const kq_weight* gate_up, const kq_weight* down, const kq
     return KQ_OK;
 }
 
+// Greedy-head workspace: the projection's workspace, logits [M, N] (when the caller keeps none), and the selection
+// partials (at most one per row tile and row: decode workgroups and 4096-column chunks are both fewer).
+struct GreedyLayout {
+    std::size_t lin = 0, logits = 0, parts = 0;
+    std::size_t total() const { return lin + logits + parts; }
+};
+GreedyLayout greedy_layout(const kq::Weight& w, std::int64_t M) {
+    GreedyLayout l;
+    l.lin = align_up(kq::workspace_bytes(w, M));
+    l.logits = align_up(static_cast<std::size_t>(M * w.geo.rows) * 4);
+    const std::int64_t parts = std::max<std::int64_t>(w.geo.n_tiles, kq::greedy_chunk_count(w.geo.rows));
+    l.parts = align_up(static_cast<std::size_t>(M * parts) * 16);
+    return l;
+}
+
 }  // namespace
 
 namespace kq {
@@ -605,6 +621,79 @@ kq_status kq_gated_feed_forward(const kq_weight* gate_up, const kq_weight* down,
     a.output_scale = args->down_output_scale;
     a.y = args->y;
     return kq_packed_linear(down, &a, stream);
+}
+
+size_t kq_greedy_workspace_size(int64_t rows, int64_t width) {
+    if (rows < 0 || width < 1) return 0;
+    return align_up(static_cast<std::size_t>(rows * kq::greedy_chunk_count(width)) * 16);
+}
+
+kq_status kq_greedy_token(const float* logits, int64_t rows, int64_t width, int32_t* tokens, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+    if (rows < 0 || width < 1) return fail(KQ_INVALID_ARGUMENT, "greedy selection requires [rows, width > 0] logits");
+    if (rows == 0) return KQ_OK;
+    if (!logits || !tokens) return fail(KQ_INVALID_ARGUMENT, "null logits or tokens");
+    const std::size_t need = kq_greedy_workspace_size(rows, width);
+    void* ws = workspace;
+    if (ws) {
+        if (workspace_bytes < need) return fail(KQ_INVALID_ARGUMENT, "workspace too small");
+    } else if (kq_status s = device_scratch(g_greedy_scratch, need, &ws); s != KQ_OK) {
+        return s;
+    }
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    auto* parts = static_cast<int4*>(ws);
+    if (hipError_t e = kq::launch_greedy_chunks(logits, rows, width, parts, st); e != hipSuccess) return hip_fail(e, "greedy launch");
+    if (hipError_t e = kq::launch_greedy_reduce(parts, rows, kq::greedy_chunk_count(width), tokens, st); e != hipSuccess)
+        return hip_fail(e, "greedy launch");
+    return KQ_OK;
+}
+
+size_t kq_greedy_linear_workspace_size(const kq_weight* weight, int64_t m) {
+    if (!weight || m < 0) return 0;
+    return greedy_layout(*as_weight(weight), m).total();
+}
+
+kq_status kq_packed_linear_greedy(const kq_weight* weight, const kq_linear_args* args, int32_t* tokens, void* stream) {
+    if (!weight || !args) return fail(KQ_INVALID_ARGUMENT, "null weight or arguments");
+    if (args->m > 0 && !tokens) return fail(KQ_INVALID_ARGUMENT, "null tokens");
+    const kq::Weight& w = *as_weight(weight);
+    const GreedyLayout l = greedy_layout(w, std::max<int64_t>(args->m, 0));
+    void* ws = args->workspace;
+    if (args->m > 0) {
+        if (ws) {
+            if (args->workspace_bytes < l.total()) return fail(KQ_INVALID_ARGUMENT, "workspace too small");
+        } else if (kq_status s = device_scratch(g_greedy_scratch, l.total(), &ws); s != KQ_OK) {
+            return s;
+        }
+    }
+    auto* base = static_cast<std::uint8_t*>(ws);
+    kq_linear_args la = *args;
+    la.workspace = base;
+    la.workspace_bytes = l.lin;
+    if (!la.y && base) la.y = reinterpret_cast<float*>(base + l.lin);
+    kq::LinearCall c;
+    std::size_t need = 0;
+    if (kq_status s = prepare_call(weight, &la, false, c, &need); s != KQ_OK) return s;
+    if (c.M == 0) return KQ_OK;
+    auto* parts = reinterpret_cast<int4*>(base + l.lin + l.logits);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev != w.device) return fail(KQ_INVALID_ARGUMENT, "weight was packed on another device");
+    if (kq::decode_fits(c)) {
+        int count = 0;
+        c.y = args->y;  // NULL: the logits stay on chip
+        c.greedy = parts;
+        c.greedy_parts = &count;
+        if (hipError_t e = kq::launch_decode(c, st); e != hipSuccess) return hip_fail(e, "decode projection launch");
+        if (hipError_t e = kq::launch_greedy_reduce(parts, c.M, count, tokens, st); e != hipSuccess) return hip_fail(e, "greedy launch");
+        return KQ_OK;
+    }
+    if (kq_status s = run_call(c, &la, need, st); s != KQ_OK) return s;
+    if (hipError_t e = kq::launch_greedy_chunks(la.y, c.M, w.geo.rows, parts, st); e != hipSuccess) return hip_fail(e, "greedy launch");
+    if (hipError_t e = kq::launch_greedy_reduce(parts, c.M, kq::greedy_chunk_count(w.geo.rows), tokens, st); e != hipSuccess)
+        return hip_fail(e, "greedy launch");
+    return KQ_OK;
 }
 
 kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_dtype, int64_t m, float input_scale,

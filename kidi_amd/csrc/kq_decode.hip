@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cstdint>
 #include <cstdlib>
 
@@ -51,6 +52,7 @@ struct DecodeArgs {
     std::int32_t* dq_zeros;
     int M, K, N, k_tiles, n_tiles, groups_p, groups;
     int pairs, total_pairs;  // row-tile pairs per workgroup (consecutive), pairs in the projection
+    int4* greedy;            // greedy selection: per row and workgroup {max, first index, non-finite seen} [M][grid]
     int x_f32, scale_half, aux_half;
     float input_scale, output_scale;
 };
@@ -88,7 +90,7 @@ __device__ __forceinline__ v4i block_codes(const uint4 w) {
 
 // MR: rows of the variant (4 or 8); WMAX: most waves per workgroup (4 for K <= 2048, 16 up to K = 8192), which
 // sets the register budget (512 / (WMAX / 4) VGPRs per lane)
-template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, int MR, int WMAX>
+template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, int MR, int WMAX, bool GREEDY = false>
 __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     constexpr int H = MR / 4;            // MFMA row halves: rows 4 h .. 4 h + 3
     constexpr int RT = (WMAX > 4 && !GELU) ? 1 : 2;  // row tiles per unit: one when K > 2048 (more workgroups)
@@ -247,6 +249,15 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
 
     // ---- 3-4 per pair of row tiles: MFMA with one epilogue per quad of groups, then the reductions ----
     float* red = reinterpret_cast<float*>(lds + W * WAVE_BYTES);  // [W][RT][MR][16]
+    // greedy selection: running {max, first index, non-finite seen} per row over this workgroup's columns
+    int* gbest = reinterpret_cast<int*>(lds + W * WAVE_BYTES + W * 2 * MR * 16 * 4);  // [MR][4]
+    if constexpr (GREEDY) {
+        if (threadIdx.x < MR) {
+            gbest[4 * threadIdx.x] = __float_as_int(-__builtin_inff());
+            gbest[4 * threadIdx.x + 1] = INT_MAX;
+            gbest[4 * threadIdx.x + 2] = 0;
+        }
+    }
     for (int pair = pair0; pair < pend; ++pair) {
     if (pair != pair0) {  // the first pair's loads went out before the quantization
         set_pair(pair);
@@ -353,7 +364,8 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < (GELU ? 1 : RT) * M * 16; idx += blockDim.x) {
-        const int r = idx / (M * 16), i = (idx / 16) % M, c = idx % 16;
+        // (greedy: a row's RT x 16 columns on consecutive lanes, in column order)
+        const int r = GREEDY ? (idx / 16) % RT : idx / (M * 16), i = GREEDY ? idx / (RT * 16) : (idx / 16) % M, c = idx % 16;
         float v[2] = {0.F, 0.F};
 #pragma unroll
         for (int h = 0; h < (GELU ? 2 : 1); ++h) {
@@ -369,32 +381,63 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
         } else {
             const int nt = r == 0 ? cur_nt0 : cur_nt1;
             const int n = nt * kTileRows + c;
-            if (nt < a.n_tiles && n < a.N) a.y[static_cast<std::int64_t>(i) * a.N + n] = v[0];
+            const bool valid = nt < a.n_tiles && n < a.N;
+            if (valid && (!GREEDY || a.y)) a.y[static_cast<std::int64_t>(i) * a.N + n] = v[0];
+            if constexpr (GREEDY) {
+                // this pair's best of row i over its RT x 16 lanes (larger value, then lower column), merged into
+                // the running best with strict > (earlier pairs hold lower columns)
+                float bv = valid ? v[0] : -__builtin_inff();
+                int bn = valid ? n : INT_MAX, bad = valid && !__builtin_isfinite(v[0]);
+#pragma unroll
+                for (int off = 1; off < 16 * RT; off <<= 1) {
+                    const float ov = __shfl_xor(bv, off);
+                    const int on = __shfl_xor(bn, off), ob = __shfl_xor(bad, off);
+                    if (ov > bv || (ov == bv && on < bn)) {
+                        bv = ov;
+                        bn = on;
+                    }
+                    bad |= ob;
+                }
+                if (idx % (16 * RT) == 0) {
+                    if (bv > __int_as_float(gbest[4 * i])) {
+                        gbest[4 * i] = __float_as_int(bv);
+                        gbest[4 * i + 1] = bn;
+                    }
+                    gbest[4 * i + 2] |= bad;
+                }
+            }
         }
     }
     __syncthreads();  // the reduction buffer is reused by the next pair
     }
+    if constexpr (GREEDY) {
+        if (threadIdx.x < M)
+            a.greedy[static_cast<std::int64_t>(threadIdx.x) * gridDim.x + blockIdx.x] =
+                make_int4(gbest[4 * threadIdx.x], gbest[4 * threadIdx.x + 1], gbest[4 * threadIdx.x + 2], 0);
+    }
 }
 
-template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG>
+template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, bool GREEDY = false>
 hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds, hipStream_t stream) {
     const bool wide = block.x > 256 || DBG;  // debug variants: one register budget for every K
     if (a.M <= 4) {
-        if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, 16>), grid, block, lds, stream, a);
-        else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, (DBG ? 16 : 4)>), grid, block, lds, stream, a);
+        if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, 16, GREEDY>), grid, block, lds, stream, a);
+        else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, (DBG ? 16 : 4), GREEDY>), grid, block, lds, stream, a);
     } else {
-        if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 8, 16>), grid, block, lds, stream, a);
-        else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 8, (DBG ? 16 : 4)>), grid, block, lds, stream, a);
+        if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 8, 16, GREEDY>), grid, block, lds, stream, a);
+        else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 8, (DBG ? 16 : 4), GREEDY>), grid, block, lds, stream, a);
     }
     return hipGetLastError();
 }
 
 template <int BITS, int ZM, int QM>
-hipError_t launch_modes(const DecodeArgs& a, int g, bool gelu, bool dbg, dim3 grid, dim3 block, std::size_t lds, hipStream_t stream) {
+hipError_t launch_modes(const DecodeArgs& a, int g, bool gelu, bool dbg, bool greedy, dim3 grid, dim3 block, std::size_t lds,
+                        hipStream_t stream) {
 #define KQ_DEC(G)                                                                                       \
     do {                                                                                                \
         if (gelu) return launch_g<BITS, G, true, ZM, QM, false>(a, grid, block, lds, stream);           \
         if (dbg) return launch_g<BITS, G, false, ZM, QM, true>(a, grid, block, lds, stream);            \
+        if (greedy) return launch_g<BITS, G, false, ZM, QM, false, true>(a, grid, block, lds, stream);  \
         return launch_g<BITS, G, false, ZM, QM, false>(a, grid, block, lds, stream);                    \
     } while (0)
     if (g == 32) KQ_DEC(32);
@@ -463,20 +506,22 @@ hipError_t launch_decode(const LinearCall& c, hipStream_t stream) {
     const int blocks = (a.total_pairs + a.pairs - 1) / a.pairs;
     const dim3 grid(static_cast<unsigned>(blocks)), block(64 * W);
     const int mr = c.M <= 4 ? 4 : 8;
-    const std::size_t lds = static_cast<std::size_t>(W * wave_bytes(w.geo.group, mr) + W * 2 * mr * 16 * 4);
+    const std::size_t lds = static_cast<std::size_t>(W * wave_bytes(w.geo.group, mr) + W * 2 * mr * 16 * 4 + mr * 16);
+    a.greedy = c.greedy;
+    if (c.greedy && c.greedy_parts) *c.greedy_parts = blocks;
     const bool dbg = c.dump || c.dq_codes || c.dq_scales || c.dq_sums || c.dq_zeros;
     const bool stat = c.path == PATH_SYMMETRIC;
     const int g = w.geo.group;
     switch (w.geo.bits) {
-    case 2: return launch_modes<2, ZERO_NONE, dev::QUANT_STATIC>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
+    case 2: return launch_modes<2, ZERO_NONE, dev::QUANT_STATIC>(a, g, c.gelu_gate, dbg, c.greedy != nullptr, grid, block, lds, stream);
     case 4:
-        if (stat) return launch_modes<4, ZERO_NONE, dev::QUANT_STATIC>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
-        if (w.zero_mode == ZERO_POINT) return launch_modes<4, ZERO_POINT, dev::QUANT_DYN_SYM>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
-        if (w.zero_mode == ZERO_FLOAT) return launch_modes<4, ZERO_FLOAT, dev::QUANT_DYN_SYM>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
-        return launch_modes<4, ZERO_NONE, dev::QUANT_DYN_SYM>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
+        if (stat) return launch_modes<4, ZERO_NONE, dev::QUANT_STATIC>(a, g, c.gelu_gate, dbg, c.greedy != nullptr, grid, block, lds, stream);
+        if (w.zero_mode == ZERO_POINT) return launch_modes<4, ZERO_POINT, dev::QUANT_DYN_SYM>(a, g, c.gelu_gate, dbg, c.greedy != nullptr, grid, block, lds, stream);
+        if (w.zero_mode == ZERO_FLOAT) return launch_modes<4, ZERO_FLOAT, dev::QUANT_DYN_SYM>(a, g, c.gelu_gate, dbg, c.greedy != nullptr, grid, block, lds, stream);
+        return launch_modes<4, ZERO_NONE, dev::QUANT_DYN_SYM>(a, g, c.gelu_gate, dbg, c.greedy != nullptr, grid, block, lds, stream);
     default:
-        if (stat) return launch_modes<8, ZERO_NONE, dev::QUANT_STATIC>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
-        return launch_modes<8, ZERO_NONE, dev::QUANT_DYN_ASYM>(a, g, c.gelu_gate, dbg, grid, block, lds, stream);
+        if (stat) return launch_modes<8, ZERO_NONE, dev::QUANT_STATIC>(a, g, c.gelu_gate, dbg, c.greedy != nullptr, grid, block, lds, stream);
+        return launch_modes<8, ZERO_NONE, dev::QUANT_DYN_ASYM>(a, g, c.gelu_gate, dbg, c.greedy != nullptr, grid, block, lds, stream);
     }
 }
 

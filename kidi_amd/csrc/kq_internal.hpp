@@ -59,6 +59,9 @@ struct LinearCall {
     float* dq_scales = nullptr;
     std::int32_t* dq_sums = nullptr;
     std::int32_t* dq_zeros = nullptr;
+    // greedy selection from the decode epilogue: partials [M][workgroups] (kq_greedy.hip), their count per row
+    int4* greedy = nullptr;
+    int* greedy_parts = nullptr;
 };
 
 // Launch plan of the skinny (decode, M <= 16) projection with fused activation quantization (kq_skinny.hip).
@@ -72,7 +75,7 @@ struct SkinnyPlan {
 
 bool skinny_plan(const LinearCall& c, SkinnyPlan& p);
 
-// Decode projection for M <= 4 and K a multiple of 512 with g in {32, 64, 128} (kq_decode.hip).
+// Decode projection for M <= 8 and K a multiple of 512 (at most 8192) with g in {32, 64, 128} (kq_decode.hip).
 bool decode_fits(const LinearCall& c);
 hipError_t launch_decode(const LinearCall& c, hipStream_t stream);
 hipError_t launch_skinny(const LinearCall& c, const SkinnyPlan& p, hipStream_t stream);
@@ -97,6 +100,12 @@ hipError_t launch_quantize(const LinearCall& c, hipStream_t stream);
 hipError_t launch_linear(const LinearCall& c, hipStream_t stream);
 hipError_t launch_gelu_gate(const float* in, std::int64_t M, std::int64_t I, float* out, hipStream_t stream);
 hipError_t launch_silu_gate(const float* in, std::int64_t M, std::int64_t I, float* out, hipStream_t stream);
+
+// Greedy token selection (kq_greedy.hip): partials {max, first index, non-finite} per (row, 4096-column chunk) of
+// F32 logits, then one token per row from a row's partials in column order (-1 for a non-finite row).
+int greedy_chunk_count(std::int64_t width);
+hipError_t launch_greedy_chunks(const float* logits, std::int64_t rows, std::int64_t width, int4* parts, hipStream_t stream);
+hipError_t launch_greedy_reduce(const int4* parts, std::int64_t rows, int count, std::int32_t* tokens, hipStream_t stream);
 hipError_t launch_unpermute_codes(const Weight& w, const ActBuffers& act, std::int64_t M, std::int8_t* codes,
                                   hipStream_t stream);
 hipError_t launch_copy_block_stats(const Weight& w, const ActBuffers& act, std::int64_t M, float* scales,

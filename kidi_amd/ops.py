@@ -145,6 +145,32 @@ class DeviceWeight:
         _raise(fn(self.handle, ctypes.byref(a), _stream()))
         return y.reshape(*x.shape[:-1], width)
 
+    def linear_greedy(self, x: torch.Tensor, input_scale: float = 0.0, output_scale: float = 0.0,
+                      keep_logits: bool = False):
+        """(tokens int32 [...], logits [..., N] or None): the projection fused with greedy selection
+        (kq_packed_linear_greedy); without keep_logits the decode kernel keeps the logits on chip."""
+        if x.dim() < 1 or x.shape[-1] != self.cols:
+            raise Failure("INVALID_ARGUMENT", "packed linear shape or dtype mismatch")
+        x2 = x.reshape(-1, self.cols).contiguous()
+        m = x2.shape[0]
+        y = torch.empty((m, self.rows), dtype=torch.float32, device=x.device) if keep_logits else None
+        tokens = torch.empty((m,), dtype=torch.int32, device=x.device)
+        L = N.load()
+        ws_bytes = L.kq_greedy_linear_workspace_size(self.handle, m)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+        a = N.LinearArgs()
+        a.x = x2.data_ptr()
+        a.x_dtype = N.KQ_BF16 if x2.dtype == torch.bfloat16 else (N.KQ_F32 if x2.dtype == torch.float32 else 99)
+        a.m = m
+        a.input_scale = input_scale
+        a.output_scale = output_scale
+        a.y = y.data_ptr() if y is not None else None
+        a.workspace = ws.data_ptr()
+        a.workspace_bytes = ws_bytes
+        _raise(L.kq_packed_linear_greedy(self.handle, ctypes.byref(a), tokens.data_ptr(), _stream()))
+        tokens = tokens.reshape(x.shape[:-1])
+        return tokens, (y.reshape(*x.shape[:-1], self.rows) if y is not None else None)
+
     def debug_partials(self, x: torch.Tensor, input_scale: float = 0.0, output_scale: float = 0.0):
         """(y, int32 partials [M, N, K/g]) from the same kernel as ``linear``."""
         x2 = x.reshape(-1, self.cols).contiguous()
@@ -196,6 +222,20 @@ def gated_feed_forward(gate_up: DeviceWeight, down: DeviceWeight, x: torch.Tenso
     a.workspace_bytes = ws_bytes
     _raise(L.kq_gated_feed_forward(gate_up.handle, down.handle, ctypes.byref(a), _stream()))
     return y.reshape(*x.shape[:-1], down.rows)
+
+
+def greedy_token(logits: torch.Tensor) -> torch.Tensor:
+    """Greedy token per row of device F32 logits [..., width] (kq_greedy_token): int32 [...]."""
+    if logits.dim() < 1 or logits.shape[-1] < 1 or logits.dtype != torch.float32:
+        raise Failure("INVALID_ARGUMENT", "greedy selection requires F32 [..., width > 0] logits")
+    x = logits.reshape(-1, logits.shape[-1]).contiguous()
+    rows, width = x.shape
+    tokens = torch.empty((rows,), dtype=torch.int32, device=logits.device)
+    L = N.load()
+    ws_bytes = L.kq_greedy_workspace_size(rows, width)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=logits.device)
+    _raise(L.kq_greedy_token(x.data_ptr(), rows, width, tokens.data_ptr(), ws.data_ptr(), ws_bytes, _stream()))
+    return tokens.reshape(logits.shape[:-1])
 
 
 def _identity(t: torch.Tensor | None):
@@ -301,3 +341,13 @@ class Context:
         y = gated_feed_forward(gu, dn, x, gate_up_input_scale, gate_up_output_scale, down_input_scale,
                                down_output_scale, silu)
         return y.cpu() if host else y
+
+    def greedy_token(self, logits: torch.Tensor) -> torch.Tensor:
+        """Context::greedy_token: I32 [...] of F32 logits [..., width]; a scalar is INVALID_ARGUMENT
+        (eager_test.cpp:254-260). Host logits return host tokens."""
+        if logits.dim() == 0 or logits.shape[-1] == 0:
+            raise Failure("INVALID_ARGUMENT", "greedy selection requires [..., width > 0] logits")
+        host = not logits.is_cuda
+        x = logits.to(self.device, torch.float32) if host else logits.float()
+        t = greedy_token(x)
+        return t.cpu() if host else t

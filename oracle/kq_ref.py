@@ -229,6 +229,19 @@ def gated_feed_forward(x: np.ndarray, gate_up_values: np.ndarray, gate_up_scales
     return y, h
 
 
+def greedy_token(logits: np.ndarray) -> np.ndarray:
+    """GREEDY_TOKEN (runtime/ynn/operators.cpp:117-178): per row of [..., width] logits the first index of the maximum
+    (strict >, so -0 and 0 tie to the earlier), -1 when the row holds a NaN or an infinity (eager_test.cpp:231-252)."""
+    x = np.asarray(logits, dtype=np.float32)
+    if x.ndim == 0 or x.shape[-1] == 0:
+        raise ValueError("greedy selection requires [..., width > 0] logits")
+    rows = x.reshape(-1, x.shape[-1])
+    out = np.empty(rows.shape[0], np.int32)
+    for r, row in enumerate(rows):
+        out[r] = -1 if not np.all(np.isfinite(row)) else int(np.argmax(row))  # argmax returns the first maximum
+    return out.reshape(x.shape[:-1])
+
+
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
     """Round-to-nearest-even float32 -> bf16 bit patterns (uint16); NaN stays NaN."""
     b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)

@@ -15,7 +15,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["kq_gemm.hip", "kq_decode.hip", "kq_skinny.hip", "kq_kernels.hip"]
+SOURCES = ["kq_gemm.hip", "kq_decode.hip", "kq_skinny.hip", "kq_kernels.hip", "kq_greedy.hip"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S"]
 
