@@ -173,6 +173,14 @@ kq_status kq_greedy_token(const float* logits, int64_t rows, int64_t width, int3
 size_t kq_greedy_linear_workspace_size(const kq_weight* weight, int64_t m);
 kq_status kq_packed_linear_greedy(const kq_weight* weight, const kq_linear_args* args, int32_t* tokens, void* stream);
 
+/* Persisted gfx950 layout, the role of Kidi's packed-operator cache (runtime/ynn/feed_forward_cache.h:11-38,
+ * feed_forward_cache.cpp): a packed weight as one host blob (header + the device image) and back, so a later load
+ * skips validation and re-layout. The blob holds the layout version and the weight's geometry; kq_weight_import
+ * rejects a blob of another version or a malformed one with KQ_INVALID_MANIFEST. Both calls are synchronous. */
+size_t kq_weight_export_size(const kq_weight* weight);
+kq_status kq_weight_export(const kq_weight* weight, void* host, size_t bytes, void* stream);
+kq_status kq_weight_import(const void* host, size_t bytes, void* stream, kq_weight** out);
+
 /* ---- parity instrumentation (same kernels as kq_packed_linear, with an extra store) --------------------- */
 
 /* Activation quantization exactly as the projection performs it: codes int8 [M, K] (natural k order),

@@ -26,6 +26,7 @@ EXPORTS = (
     "kq_packed_linear_gelu_gate", "kq_debug_quantize", "kq_debug_partials", "kq_layout_bytes",
     "kq_layout_encode_host", "kq_layout_decode_host", "kq_ffn_workspace_size", "kq_gated_feed_forward",
     "kq_greedy_workspace_size", "kq_greedy_token", "kq_greedy_linear_workspace_size", "kq_packed_linear_greedy",
+    "kq_weight_export_size", "kq_weight_export", "kq_weight_import",
 )
 
 
@@ -118,6 +119,12 @@ def load() -> ctypes.CDLL:
     L.kq_ffn_workspace_size.restype = sz
     L.kq_gated_feed_forward.argtypes = [vp, vp, ctypes.POINTER(FfnArgs), vp]
     L.kq_gated_feed_forward.restype = ctypes.c_int
+    L.kq_weight_export_size.argtypes = [vp]
+    L.kq_weight_export_size.restype = sz
+    L.kq_weight_export.argtypes = [vp, vp, sz, vp]
+    L.kq_weight_export.restype = ctypes.c_int
+    L.kq_weight_import.argtypes = [vp, sz, vp, ctypes.POINTER(vp)]
+    L.kq_weight_import.restype = ctypes.c_int
     L.kq_greedy_workspace_size.argtypes = [i64, i64]
     L.kq_greedy_workspace_size.restype = sz
     L.kq_greedy_token.argtypes = [vp, i64, i64, vp, vp, sz, vp]

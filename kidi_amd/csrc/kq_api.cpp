@@ -453,6 +453,19 @@ kq_status ffn_validate(const kq_weight* gate_up, const kq_weight* down, const kq
     return KQ_OK;
 }
 
+// Persisted layout blob: this header, then the weight's device image (one allocation; sub-buffers at offsets).
+constexpr char kBlobMagic[8] = {'K', 'Q', 'G', 'F', 'X', '9', '5', '0'};
+constexpr std::uint32_t kBlobVersion = 1;  // bump with any change to the tile layout or this header
+struct BlobHeader {
+    char magic[8];
+    std::uint32_t version;
+    std::int32_t bits, group;
+    std::int64_t rows, cols;
+    std::int32_t tiled, scale_type, zero_mode, zero_type;
+    std::int64_t tiles, scales, zero_points, zeros, code_sums;  // byte offsets in the image, -1 when absent
+    std::uint64_t bytes;                                         // image size
+};
+
 // Greedy-head workspace: the projection's workspace, logits [M, N] (when the caller keeps none), and the selection
 // partials (at most one per row tile and row: decode workgroups and 4096-column chunks are both fewer).
 struct GreedyLayout {
@@ -530,6 +543,96 @@ kq_status kq_weight_pack(const kq_pack_desc* desc, void* stream, kq_weight** out
 
 kq_status kq_weight_pack_concat(const kq_pack_desc* descs, int32_t count, void* stream, kq_weight** out) {
     return pack_impl(descs, count, stream, out);
+}
+
+size_t kq_weight_export_size(const kq_weight* weight) {
+    if (!weight) return 0;
+    return sizeof(BlobHeader) + as_weight(weight)->bytes;
+}
+
+kq_status kq_weight_export(const kq_weight* weight, void* host, size_t bytes, void* stream) {
+    if (!weight || !host) return fail(KQ_INVALID_ARGUMENT, "null weight or buffer");
+    const kq::Weight& w = *as_weight(weight);
+    if (bytes < sizeof(BlobHeader) + w.bytes) return fail(KQ_INVALID_ARGUMENT, "export buffer too small");
+    BlobHeader h{};
+    std::memcpy(h.magic, kBlobMagic, sizeof(h.magic));
+    h.version = kBlobVersion;
+    h.bits = w.geo.bits;
+    h.group = w.geo.group;
+    h.rows = w.geo.rows;
+    h.cols = w.geo.cols;
+    h.tiled = w.tiled;
+    h.scale_type = w.scale_type;
+    h.zero_mode = w.zero_mode;
+    h.zero_type = w.zero_type;
+    const auto* base = static_cast<const std::uint8_t*>(w.allocation);
+    auto off = [&](const void* p) { return p ? static_cast<std::int64_t>(static_cast<const std::uint8_t*>(p) - base) : -1; };
+    h.tiles = off(w.tiles);
+    h.scales = off(w.scales);
+    h.zero_points = off(w.zero_points);
+    h.zeros = off(w.zeros);
+    h.code_sums = off(w.code_sums);
+    h.bytes = w.bytes;
+    std::memcpy(host, &h, sizeof(h));
+    auto* dst = static_cast<std::uint8_t*>(host) + sizeof(h);
+    hipError_t e = hipMemcpyAsync(dst, w.allocation, w.bytes, hipMemcpyDeviceToHost, static_cast<hipStream_t>(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "export weight");
+    return KQ_OK;
+}
+
+kq_status kq_weight_import(const void* host, size_t bytes, void* stream, kq_weight** out) {
+    if (!host || !out) return fail(KQ_INVALID_ARGUMENT, "null blob or output");
+    *out = nullptr;
+    BlobHeader h{};
+    if (bytes < sizeof(h)) return fail(KQ_INVALID_MANIFEST, "packed weight blob too short");
+    std::memcpy(&h, host, sizeof(h));
+    if (std::memcmp(h.magic, kBlobMagic, sizeof(h.magic)) != 0 || h.version != kBlobVersion)
+        return fail(KQ_INVALID_MANIFEST, "not a packed weight blob of this layout version");
+    const bool ok_bits = h.bits == 2 || h.bits == 4 || h.bits == 8;
+    if (!ok_bits || h.group <= 0 || h.rows <= 0 || h.cols <= 0 || h.cols % h.group || bytes != sizeof(h) + h.bytes ||
+        h.bytes == 0)
+        return fail(KQ_INVALID_MANIFEST, "malformed packed weight blob");
+    auto* w = new kq::Weight{};
+    w->geo = kq::Geometry::make(h.bits, h.group, h.rows, h.cols);
+    w->tiled = h.tiled != 0;
+    w->scale_type = h.scale_type;
+    w->zero_mode = h.zero_mode;
+    w->zero_type = h.zero_type;
+    for (std::int64_t o : {h.tiles, h.scales, h.zero_points, h.zeros, h.code_sums}) {
+        if (o < -1 || o >= static_cast<std::int64_t>(h.bytes)) {
+            delete w;
+            return fail(KQ_INVALID_MANIFEST, "malformed packed weight blob");
+        }
+    }
+    if (h.tiles < 0 || h.scales < 0) {
+        delete w;
+        return fail(KQ_INVALID_MANIFEST, "malformed packed weight blob");
+    }
+    hipError_t e = hipGetDevice(&w->device);
+    if (e == hipSuccess) e = hipMalloc(&w->allocation, h.bytes);
+    if (e != hipSuccess) {
+        delete w;
+        return hip_fail(e, "hipMalloc(weight)");
+    }
+    auto* base = static_cast<std::uint8_t*>(w->allocation);
+    e = hipMemcpyAsync(base, static_cast<const std::uint8_t*>(host) + sizeof(h), h.bytes, hipMemcpyHostToDevice,
+                       static_cast<hipStream_t>(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+        (void)hipFree(w->allocation);
+        delete w;
+        return hip_fail(e, "import weight");
+    }
+    w->bytes = h.bytes;
+    auto at = [&](std::int64_t o) -> std::uint8_t* { return o < 0 ? nullptr : base + o; };
+    w->tiles = at(h.tiles);
+    w->scales = at(h.scales);
+    w->zero_points = at(h.zero_points);
+    w->zeros = at(h.zeros);
+    w->code_sums = reinterpret_cast<std::int32_t*>(at(h.code_sums));
+    *out = reinterpret_cast<kq_weight*>(w);
+    return KQ_OK;
 }
 
 void kq_weight_free(kq_weight* weight) {

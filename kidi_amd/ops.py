@@ -105,6 +105,33 @@ class DeviceWeight:
         self.cols = descs[0].cols
         self.has_zeros = parts[0][2] is not None
 
+    @classmethod
+    def from_handle(cls, handle: ctypes.c_void_p) -> "DeviceWeight":
+        """Adopt a kq_weight (e.g. one kq_weight_import made); the object frees it."""
+        self = cls.__new__(cls)
+        self.handle = handle
+        b, g, r, c, z = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int32()
+        _raise(N.load().kq_weight_info(handle, ctypes.byref(b), ctypes.byref(g), ctypes.byref(r), ctypes.byref(c),
+                                       ctypes.byref(z), None))
+        self.bits, self.group_size, self.rows, self.cols, self.has_zeros = b.value, g.value, r.value, c.value, bool(z.value)
+        return self
+
+    def export(self) -> bytes:
+        """The packed gfx950 layout as one host blob (kq_weight_export)."""
+        L = N.load()
+        n = L.kq_weight_export_size(self.handle)
+        buf = (ctypes.c_uint8 * n)()
+        _raise(L.kq_weight_export(self.handle, buf, n, _stream()))
+        return bytes(buf)
+
+    @classmethod
+    def import_blob(cls, blob: bytes) -> "DeviceWeight":
+        """A weight from a kq_weight_export blob, uploaded to the current device without re-layout."""
+        handle = ctypes.c_void_p()
+        buf = (ctypes.c_uint8 * len(blob)).from_buffer_copy(blob)
+        _raise(N.load().kq_weight_import(buf, len(blob), _stream(), ctypes.byref(handle)))
+        return cls.from_handle(handle)
+
     def __del__(self):
         h = getattr(self, "handle", None)
         if h is not None and h.value:
