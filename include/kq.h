@@ -173,6 +173,52 @@ kq_status kq_greedy_token(const float* logits, int64_t rows, int64_t width, int3
 size_t kq_greedy_linear_workspace_size(const kq_weight* weight, int64_t m);
 kq_status kq_packed_linear_greedy(const kq_weight* weight, const kq_linear_args* args, int32_t* tokens, void* stream);
 
+/* RMS normalization over the last axis: RMS_NORM / RMS_NORM_RESIDUAL (Context::rms_norm and
+ * Context::rms_norm_residual, src/kidi/ops/context.cpp:1043-1049, :1103-1122; the CPU RmsNorm operator,
+ * runtime/ynn/operators.cpp:553-620):
+ *   plain:    y[r, i] = x[r, i] * inv_r * weight[i]
+ *   residual: y[r, i] = (residual[r, i] + x[r, i] * inv_r * weight[i]) * output_scale   (no scaling when NULL)
+ * with inv_r = 1 / sqrt(sum_i x[r, i]^2 / width + epsilon); epsilon must be finite and > 0 (context.cpp:1108). The
+ * sum of squares has one fixed order in this library (8-column pieces in column order, a pairwise tree over the 64
+ * pieces of each 512-column segment, segments in order), shared by the fused projection below. */
+typedef struct kq_rms_args {
+    const void* x;             /* device [rows, width] */
+    kq_dtype x_dtype;          /* KQ_F32 or KQ_BF16 */
+    int64_t rows;
+    int64_t width;
+    const float* weight;       /* device F32 [width] */
+    const void* residual;      /* NULL (RMS_NORM) or device [rows, width] of x_dtype (RMS_NORM_RESIDUAL) */
+    const float* output_scale; /* NULL or device F32 [1]; residual form only (the layer scalar, layers/gemma4.cpp:416) */
+    float epsilon;
+    float* y;                  /* device F32 [rows, width] */
+} kq_rms_args;
+kq_status kq_rms_norm(const kq_rms_args* args, void* stream);
+
+/* A projection of an RMS-normalized input, the normalization fused into the activation quantization: Kidi's
+ * decoder layer runs Context::rms_norm right before each projection group (input_layernorm before q_proj/kv_proj,
+ * pre_feedforward_layernorm before gate_up_proj, src/kidi/layers/gemma4.cpp:405, :410-413), and before that norm the
+ * residual add of the previous block (post_attention_layernorm's rms_norm_residual, :407). With `residual` NULL:
+ *   y = PACKED_LINEAR(rms_norm(x; weight, epsilon))
+ * With `residual` set (the residual chain of gemma4.cpp:407-410):
+ *   hidden = rms_norm_residual(x; residual_weight, residual, residual_epsilon, residual_scale)   (stored to `hidden`)
+ *   y      = PACKED_LINEAR(rms_norm(hidden; weight, epsilon))
+ * gelu_gate != 0 applies kq_packed_linear_gelu_gate's gating. Decode shapes (M <= 8, K <= 2048, 16-byte aligned norm
+ * operands) run as one launch; the prefill path computes per-row statistics, then quantizes normalized rows; other
+ * shapes normalize into the workspace first. Every path yields the bits of kq_rms_norm followed by the projection.
+ * args->workspace, when given, must hold kq_rms_linear_workspace_size() bytes. */
+typedef struct kq_norm_desc {
+    const float* weight;          /* device F32 [K]: the norm weight of the projection input */
+    float epsilon;
+    const void* residual;         /* NULL, or device [M, K] of args->x_dtype */
+    const float* residual_weight; /* device F32 [K] (residual form) */
+    const float* residual_scale;  /* NULL or device F32 [1] (residual form) */
+    float residual_epsilon;
+    float* hidden;                /* device F32 [M, K]: receives hidden (residual form) */
+} kq_norm_desc;
+size_t kq_rms_linear_workspace_size(const kq_weight* weight, int64_t m);
+kq_status kq_packed_linear_rms(const kq_weight* weight, const kq_linear_args* args, const kq_norm_desc* norm,
+                               int32_t gelu_gate, void* stream);
+
 /* Persisted gfx950 layout, the role of Kidi's packed-operator cache (runtime/ynn/feed_forward_cache.h:11-38,
  * feed_forward_cache.cpp): a packed weight as one host blob (header + the device image) and back, so a later load
  * skips validation and re-layout. The blob holds the layout version and the weight's geometry; kq_weight_import

@@ -26,7 +26,8 @@ EXPORTS = (
     "kq_packed_linear_gelu_gate", "kq_debug_quantize", "kq_debug_partials", "kq_layout_bytes",
     "kq_layout_encode_host", "kq_layout_decode_host", "kq_ffn_workspace_size", "kq_gated_feed_forward",
     "kq_greedy_workspace_size", "kq_greedy_token", "kq_greedy_linear_workspace_size", "kq_packed_linear_greedy",
-    "kq_weight_export_size", "kq_weight_export", "kq_weight_import",
+    "kq_weight_export_size", "kq_weight_export", "kq_weight_import", "kq_rms_norm", "kq_rms_linear_workspace_size",
+    "kq_packed_linear_rms",
 )
 
 
@@ -72,6 +73,32 @@ class LinearArgs(ctypes.Structure):
         ("y", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class RmsArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("x_dtype", ctypes.c_int),
+        ("rows", ctypes.c_int64),
+        ("width", ctypes.c_int64),
+        ("weight", ctypes.c_void_p),
+        ("residual", ctypes.c_void_p),
+        ("output_scale", ctypes.c_void_p),
+        ("epsilon", ctypes.c_float),
+        ("y", ctypes.c_void_p),
+    ]
+
+
+class NormDesc(ctypes.Structure):
+    _fields_ = [
+        ("weight", ctypes.c_void_p),
+        ("epsilon", ctypes.c_float),
+        ("residual", ctypes.c_void_p),
+        ("residual_weight", ctypes.c_void_p),
+        ("residual_scale", ctypes.c_void_p),
+        ("residual_epsilon", ctypes.c_float),
+        ("hidden", ctypes.c_void_p),
     ]
 
 
@@ -133,6 +160,12 @@ def load() -> ctypes.CDLL:
     L.kq_greedy_linear_workspace_size.restype = sz
     L.kq_packed_linear_greedy.argtypes = [vp, ctypes.POINTER(LinearArgs), vp, vp]
     L.kq_packed_linear_greedy.restype = ctypes.c_int
+    L.kq_rms_norm.argtypes = [ctypes.POINTER(RmsArgs), vp]
+    L.kq_rms_norm.restype = ctypes.c_int
+    L.kq_rms_linear_workspace_size.argtypes = [vp, i64]
+    L.kq_rms_linear_workspace_size.restype = sz
+    L.kq_packed_linear_rms.argtypes = [vp, ctypes.POINTER(LinearArgs), ctypes.POINTER(NormDesc), i32, vp]
+    L.kq_packed_linear_rms.restype = ctypes.c_int
     L.kq_debug_quantize.argtypes = [vp, vp, ctypes.c_int, i64, f32, vp, vp, vp, vp, vp]
     L.kq_debug_quantize.restype = ctypes.c_int
     L.kq_debug_partials.argtypes = [vp, ctypes.POINTER(LinearArgs), vp, vp]

@@ -96,6 +96,7 @@ std::map<int, Scratch> g_scratch;
 std::map<int, Scratch> g_gelu_scratch;
 std::map<int, Scratch> g_ffn_scratch;
 std::map<int, Scratch> g_greedy_scratch;
+std::map<int, Scratch> g_norm_scratch;
 
 kq_status device_scratch(std::map<int, Scratch>& pool, std::size_t bytes, void** out) {
     int dev = 0;
@@ -481,6 +482,31 @@ GreedyLayout greedy_layout(const kq::Weight& w, std::int64_t M) {
     return l;
 }
 
+// Normalized-projection workspace: the projection's own workspace, the normalized input [M, K] F32 (paths without a
+// fused normalization), the per-row inverse RMS [M] (prefill quantizer).
+struct RmsLayout {
+    std::size_t lin = 0, norm = 0, inv = 0;
+    std::size_t total() const { return lin + norm + inv; }
+};
+RmsLayout rms_layout(const kq::Weight& w, std::int64_t M) {
+    RmsLayout l;
+    l.lin = align_up(kq::workspace_bytes(w, M));
+    l.norm = align_up(static_cast<std::size_t>(M * w.geo.cols) * 4);
+    l.inv = align_up(static_cast<std::size_t>(M) * 4);
+    return l;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
+
+// Context::rms_norm / rms_norm_residual operand checks (ops/context.cpp:1103-1112): epsilon finite and > 0.
+kq_status norm_validate(const kq_norm_desc* n) {
+    if (!n || !n->weight) return fail(KQ_INVALID_ARGUMENT, "invalid RMS residual normalization operands");
+    if (!std::isfinite(n->epsilon) || n->epsilon <= 0) return fail(KQ_INVALID_ARGUMENT, "invalid RMS residual normalization operands");
+    if (n->residual && (!n->residual_weight || !n->hidden || !std::isfinite(n->residual_epsilon) || n->residual_epsilon <= 0))
+        return fail(KQ_INVALID_ARGUMENT, "invalid RMS residual normalization operands");
+    return KQ_OK;
+}
+
 }  // namespace
 
 namespace kq {
@@ -797,6 +823,111 @@ kq_status kq_packed_linear_greedy(const kq_weight* weight, const kq_linear_args*
     if (hipError_t e = kq::launch_greedy_reduce(parts, c.M, kq::greedy_chunk_count(w.geo.rows), tokens, st); e != hipSuccess)
         return hip_fail(e, "greedy launch");
     return KQ_OK;
+}
+
+kq_status kq_rms_norm(const kq_rms_args* args, void* stream) {
+    if (!args) return fail(KQ_INVALID_ARGUMENT, "null arguments");
+    if (args->rows < 0 || args->width <= 0 || (args->x_dtype != KQ_F32 && args->x_dtype != KQ_BF16) || !args->weight ||
+        !std::isfinite(args->epsilon) || args->epsilon <= 0)
+        return fail(KQ_INVALID_ARGUMENT, "invalid RMS residual normalization operands");
+    if (args->rows == 0) return KQ_OK;
+    if (!args->x || !args->y) return fail(KQ_INVALID_ARGUMENT, "null input or output");
+    if (args->output_scale && !args->residual)
+        return fail(KQ_INVALID_ARGUMENT, "an output scale needs the residual form");
+    kq::NormLaunch n;
+    n.x = args->x;
+    n.x_type = args->x_dtype == KQ_BF16 ? kq::ACT_BF16 : kq::ACT_F32;
+    n.residual = args->residual;
+    n.w1 = args->weight;
+    n.scale = args->output_scale;
+    n.out1 = args->y;
+    n.rows = args->rows;
+    n.width = args->width;
+    n.eps1 = args->epsilon;
+    if (hipError_t e = kq::launch_rms_norm(n, static_cast<hipStream_t>(stream)); e != hipSuccess)
+        return hip_fail(e, "RMS normalization launch");
+    return KQ_OK;
+}
+
+size_t kq_rms_linear_workspace_size(const kq_weight* weight, int64_t m) {
+    if (!weight || m < 0) return 0;
+    return rms_layout(*as_weight(weight), m).total();
+}
+
+kq_status kq_packed_linear_rms(const kq_weight* weight, const kq_linear_args* args, const kq_norm_desc* norm,
+                               int32_t gelu_gate, void* stream) {
+    kq::LinearCall c;
+    std::size_t ws_lin = 0;
+    if (kq_status s = prepare_call(weight, args, gelu_gate != 0, c, &ws_lin); s != KQ_OK) return s;
+    if (kq_status s = norm_validate(norm); s != KQ_OK) return s;
+    if (c.M == 0) return KQ_OK;
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev != c.w->device) return fail(KQ_INVALID_ARGUMENT, "weight was packed on another device");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool res = norm->residual != nullptr;
+    const std::int64_t K = c.w->geo.cols;
+    // Decode (M <= 8, K <= 2048): the projection kernel normalizes its own input (one launch).
+    c.norm = res ? 2 : 1;
+    c.norm_w1 = res ? norm->residual_weight : norm->weight;
+    c.norm_w2 = res ? norm->weight : nullptr;
+    c.norm_res = norm->residual;
+    c.norm_scale = norm->residual_scale;
+    c.norm_hidden = norm->hidden;
+    c.norm_eps1 = res ? norm->residual_epsilon : norm->epsilon;
+    c.norm_eps2 = norm->epsilon;
+    const bool aligned = aligned16(c.norm_w1) && (!res || (aligned16(norm->weight) && aligned16(norm->hidden) &&
+                                                           aligned16(norm->residual)));
+    if (aligned && kq::decode_fits(c)) {
+        if (hipError_t e = kq::launch_decode(c, st); e != hipSuccess) return hip_fail(e, "decode projection launch");
+        return KQ_OK;
+    }
+    c.norm = 0;
+    const RmsLayout l = rms_layout(*c.w, c.M);
+    void* ws = args->workspace;
+    if (ws) {
+        if (args->workspace_bytes < l.total()) return fail(KQ_INVALID_ARGUMENT, "workspace too small");
+    } else if (kq_status s = device_scratch(g_norm_scratch, l.total(), &ws); s != KQ_OK) {
+        return s;
+    }
+    auto* base = static_cast<std::uint8_t*>(ws);
+    float* normed = reinterpret_cast<float*>(base + l.lin);
+    float* inv = reinterpret_cast<float*>(base + l.lin + l.norm);
+    kq::NormLaunch n;
+    n.x = args->x;
+    n.x_type = c.x_type;
+    n.residual = norm->residual;
+    n.w1 = c.norm_w1;
+    n.scale = norm->residual_scale;
+    n.rows = c.M;
+    n.width = K;
+    n.eps1 = c.norm_eps1;
+    n.eps2 = norm->epsilon;
+    // Prefill 4-bit g = 128: per-row statistics (and h), then the row quantizer normalizes while it quantizes.
+    if (ws_lin) c.act = kq::carve_workspace(*c.w, c.M, base);
+    if (kq::gemm_i4_fits(c) && aligned16(norm->weight)) {
+        n.out1 = res ? norm->hidden : nullptr;
+        n.w2 = res ? norm->weight : nullptr;
+        n.inv_out = inv;
+        if (hipError_t e = kq::launch_rms_norm(n, st); e != hipSuccess) return hip_fail(e, "RMS normalization launch");
+        c.x = res ? static_cast<const void*>(norm->hidden) : args->x;
+        c.x_type = res ? kq::ACT_F32 : c.x_type;
+        c.norm_inv = inv;
+        c.norm_w1 = norm->weight;
+        if (hipError_t e = kq::launch_gemm_i4(c, c.act, st); e != hipSuccess) return hip_fail(e, "prefill projection launch");
+        return KQ_OK;
+    }
+    // Other shapes: the normalized input to the workspace, then the plain projection of it.
+    n.out1 = res ? norm->hidden : normed;
+    n.w2 = res ? norm->weight : nullptr;
+    n.out2 = res ? normed : nullptr;
+    if (hipError_t e = kq::launch_rms_norm(n, st); e != hipSuccess) return hip_fail(e, "RMS normalization launch");
+    kq_linear_args a = *args;
+    a.x = normed;
+    a.x_dtype = KQ_F32;
+    a.workspace = ws_lin ? base : nullptr;
+    a.workspace_bytes = l.lin;
+    return gelu_gate ? kq_packed_linear_gelu_gate(weight, &a, stream) : kq_packed_linear(weight, &a, stream);
 }
 
 kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_dtype, int64_t m, float input_scale,

@@ -55,6 +55,14 @@ struct DecodeArgs {
     int4* greedy;            // greedy selection: per row and workgroup {max, first index, non-finite seen} [M][grid]
     int x_f32, scale_half, aux_half;
     float input_scale, output_scale;
+    // fused RMS normalization of the input (LinearCall::norm): 0 none, 1 plain, 2 residual form then plain
+    int norm;
+    const float* norm_w1;
+    const float* norm_w2;
+    const void* norm_res;
+    const float* norm_scale;
+    float* norm_hidden;
+    float norm_eps1, norm_eps2;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, std::uint32_t bytes) {
@@ -88,9 +96,38 @@ __device__ __forceinline__ v4i block_codes(const uint4 w) {
     return v4i{o[0], o[1], o[2], o[3]};
 }
 
+// Eight activations of one lane's piece from their raw loads (two 16-byte words for F32, one for BF16).
+__device__ __forceinline__ void decode_piece(const uint4 (&r)[2], bool f32, float (&v)[8]) {
+    if (f32) {
+        const std::uint32_t w8[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w8[i]);
+    } else {
+        const std::uint32_t w4[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w4[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w4[i] & 0xFFFF0000u);
+        }
+    }
+}
+
+// Sum of squares of a 512-column segment in the library's fixed order: each lane's 8 columns in column order, then
+// a balanced pairwise tree over the 64 lanes in lane order (DPP xor-1 and xor-2, the two mirrors, which pair whole
+// quads and half rows once those hold equal values, then xor 16 and xor 32). Every lane returns the segment sum.
+__device__ __forceinline__ float segment_sum_squares(const float (&v)[8]) {
+    float s = v[0] * v[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) s = s + v[i] * v[i];
+    s = __int_as_float(row_reduce<4>(__float_as_int(s), [](int p, int q) { return __float_as_int(__int_as_float(p) + __int_as_float(q)); }));
+    s = s + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(s), 0x401F));  // xor 16
+    s = s + __shfl_xor(s, 32);
+    return s;
+}
+
 // MR: rows of the variant (4 or 8); WMAX: most waves per workgroup (4 for K <= 2048, 16 up to K = 8192), which
 // sets the register budget (512 / (WMAX / 4) VGPRs per lane)
-template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, int MR, int WMAX, bool GREEDY = false>
+template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, int MR, int WMAX, bool GREEDY = false, bool NORM = false>
 __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     constexpr int H = MR / 4;            // MFMA row halves: rows 4 h .. 4 h + 3
     constexpr int RT = (WMAX > 4 && !GELU) ? 1 : 2;  // row tiles per unit: one when K > 2048 (more workgroups)
@@ -152,6 +189,35 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
             xr[m][1] = ld16(xres, a.x_f32 ? off + 16 : off);
         }
     }
+    // fused RMS normalization (variants of up to 2048 columns): norm weights and residual rows of this lane's piece
+    constexpr bool NORM_OK = NORM;
+    static_assert(!NORM || (WMAX == 4 && !DBG), "fused normalization: 4-wave variants without dumps");
+    float4 nw1[2], nw2[2];
+    uint4 nr[NORM_OK ? MR : 1][2];
+    float nscale = 1.F;
+    if constexpr (NORM_OK) {
+        if (a.norm) {
+            const float4* p1 = reinterpret_cast<const float4*>(a.norm_w1 + kb + 8 * lane);
+            nw1[0] = p1[0];
+            nw1[1] = p1[1];
+            if (a.norm == 2) {
+                const float4* p2 = reinterpret_cast<const float4*>(a.norm_w2 + kb + 8 * lane);
+                nw2[0] = p2[0];
+                nw2[1] = p2[1];
+                const __amdgpu_buffer_rsrc_t rres = rsrc(a.norm_res, static_cast<std::uint32_t>(M * a.K * (a.x_f32 ? 4 : 2)));
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    if (m < M) {
+                        const std::uint32_t e = static_cast<std::uint32_t>(m * a.K + kb + 8 * lane);
+                        const std::uint32_t off = a.x_f32 ? 4 * e : 2 * e;
+                        nr[m][0] = ld16(rres, off);
+                        nr[m][1] = ld16(rres, a.x_f32 ? off + 16 : off);
+                    }
+                }
+                if (a.norm_scale) nscale = a.norm_scale[0];
+            }
+        }
+    }
     // metadata entry of quad q for this lane: group 4q + L of the wave, row nn; one 16-byte slot per weight tile
     const std::uint32_t meta_n = static_cast<std::uint32_t>(a.n_tiles * a.groups_p * kTileRows);
     const __amdgpu_buffer_rsrc_t sres = rsrc(a.scales, meta_n * (a.scale_half ? 2 : 4));
@@ -189,23 +255,84 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     };
     load_pair();
 
+    // ---- 1b. fused RMS normalization: row sums of squares over the workgroup's waves (= the whole row) ----
+    float ninv1[MR], ninv2[MR];
+    // h = (r + x * inv1 * w1) [* s] of this lane's piece of row m (the residual form's output)
+    auto hidden_piece = [&](int m, float (&h)[8]) {
+        float v[8];
+        decode_piece(xr[m], a.x_f32 != 0, v);
+        decode_piece(nr[NORM_OK ? m : 0], a.x_f32 != 0, h);
+        const float w[8] = {nw1[0].x, nw1[0].y, nw1[0].z, nw1[0].w, nw1[1].x, nw1[1].y, nw1[1].z, nw1[1].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h[i] = (h[i] + v[i] * ninv1[m] * w[i]) * nscale;
+    };
+    if constexpr (NORM_OK) {
+        if (a.norm) {
+            float* nsum = reinterpret_cast<float*>(lds + W * WAVE_BYTES + W * 2 * MR * 16 * 4 + MR * 16);  // [2][W][MR]
+            const float kf = static_cast<float>(a.K);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                if (m < M) {
+                    float v[8];
+                    decode_piece(xr[m], a.x_f32 != 0, v);
+                    const float t = segment_sum_squares(v);
+                    if (lane == 0) nsum[wave * MR + m] = t;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                if (m < M) {
+                    float t = nsum[m];
+                    for (int w = 1; w < W; ++w) t = t + nsum[w * MR + m];
+                    ninv1[m] = 1.F / sqrtf(t / kf + a.norm_eps1);
+                }
+            }
+            if (a.norm == 2) {
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    if (m < M) {
+                        float h[8];
+                        hidden_piece(m, h);
+                        if (blockIdx.x == 0) {
+                            float4* hp = reinterpret_cast<float4*>(a.norm_hidden + static_cast<std::int64_t>(m) * a.K + kb + 8 * lane);
+                            hp[0] = make_float4(h[0], h[1], h[2], h[3]);
+                            hp[1] = make_float4(h[4], h[5], h[6], h[7]);
+                        }
+                        const float t = segment_sum_squares(h);
+                        if (lane == 0) nsum[(W + wave) * MR + m] = t;
+                    }
+                }
+                __syncthreads();
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    if (m < M) {
+                        float t = nsum[W * MR + m];
+                        for (int w = 1; w < W; ++w) t = t + nsum[(W + w) * MR + m];
+                        ninv2[m] = 1.F / sqrtf(t / kf + a.norm_eps2);
+                    }
+                }
+            }
+        }
+    }
+
     // ---- 2. quantize this wave's 512 columns of each row: lane = 8-column piece, 2^LGC lanes = one group ----
     const bool dump_block = DBG && blockIdx.x == 0;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
         if (m < M) {
             float v[8];
-            if (a.x_f32) {
-                const std::uint32_t w8[8] = {xr[m][0].x, xr[m][0].y, xr[m][0].z, xr[m][0].w,
-                                             xr[m][1].x, xr[m][1].y, xr[m][1].z, xr[m][1].w};
+            decode_piece(xr[m], a.x_f32 != 0, v);
+            if constexpr (NORM_OK) {
+                if (a.norm == 1) {
+                    const float w[8] = {nw1[0].x, nw1[0].y, nw1[0].z, nw1[0].w, nw1[1].x, nw1[1].y, nw1[1].z, nw1[1].w};
 #pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w8[i]);
-            } else {
-                const std::uint32_t w4[4] = {xr[m][0].x, xr[m][0].y, xr[m][0].z, xr[m][0].w};
+                    for (int i = 0; i < 8; ++i) v[i] = v[i] * ninv1[m] * w[i];
+                } else if (a.norm == 2) {
+                    hidden_piece(m, v);
+                    const float w[8] = {nw2[0].x, nw2[0].y, nw2[0].z, nw2[0].w, nw2[1].x, nw2[1].y, nw2[1].z, nw2[1].w};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    v[2 * i] = __uint_as_float(w4[i] << 16);
-                    v[2 * i + 1] = __uint_as_float(w4[i] & 0xFFFF0000u);
+                    for (int i = 0; i < 8; ++i) v[i] = v[i] * ninv2[m] * w[i];
                 }
             }
             float mx = 0.F, mn = 0.F;
@@ -420,6 +547,14 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
 template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, bool GREEDY = false>
 hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds, hipStream_t stream) {
     const bool wide = block.x > 256 || DBG;  // debug variants: one register budget for every K
+    if constexpr (!DBG && !GREEDY) {
+        if (a.norm) {  // decode_fits admits the fused normalization only for the 4-wave variants
+            if (wide) return hipErrorInvalidValue;
+            if (a.M <= 4) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 4, false, true>), grid, block, lds, stream, a);
+            else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 8, 4, false, true>), grid, block, lds, stream, a);
+            return hipGetLastError();
+        }
+    }
     if (a.M <= 4) {
         if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, 16, GREEDY>), grid, block, lds, stream, a);
         else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, (DBG ? 16 : 4), GREEDY>), grid, block, lds, stream, a);
@@ -453,6 +588,8 @@ int wave_bytes(int g, int mr) { return mr * 512 + 3 * 4 * mr * (512 / g) + 16; }
 bool decode_fits(const LinearCall& c) {
     const Weight& w = *c.w;
     if (!w.tiled || c.path == PATH_PORTABLE || c.M < 1 || c.M > kMaxRows) return false;
+    // the fused normalization lives in the 4-wave variants (K <= 2048) without debug dumps
+    if (c.norm && (w.geo.cols > 2048 || c.greedy || c.dump || c.dq_codes || c.dq_scales || c.dq_sums || c.dq_zeros)) return false;
     const int bits = w.geo.bits, g = w.geo.group;
     if (g != 32 && g != 64 && g != 128) return false;
     if (w.geo.cols % 512 || w.geo.cols / 512 > 16) return false;
@@ -490,6 +627,14 @@ hipError_t launch_decode(const LinearCall& c, hipStream_t stream) {
     a.aux_half = w.zero_type == META_F16;
     a.input_scale = c.input_scale;
     a.output_scale = c.output_scale;
+    a.norm = c.norm;
+    a.norm_w1 = c.norm_w1;
+    a.norm_w2 = c.norm_w2;
+    a.norm_res = c.norm_res;
+    a.norm_scale = c.norm_scale;
+    a.norm_hidden = c.norm_hidden;
+    a.norm_eps1 = c.norm_eps1;
+    a.norm_eps2 = c.norm_eps2;
     const int W = static_cast<int>(w.geo.cols / 512);
     // units of one workgroup iteration: pairs of row tiles, or single row tiles for the variants with the wide
     // register budget (K > 2048, i.e. more than 4 waves, and every debug variant) without gating
@@ -506,7 +651,8 @@ hipError_t launch_decode(const LinearCall& c, hipStream_t stream) {
     const int blocks = (a.total_pairs + a.pairs - 1) / a.pairs;
     const dim3 grid(static_cast<unsigned>(blocks)), block(64 * W);
     const int mr = c.M <= 4 ? 4 : 8;
-    const std::size_t lds = static_cast<std::size_t>(W * wave_bytes(w.geo.group, mr) + W * 2 * mr * 16 * 4 + mr * 16);
+    const std::size_t lds = static_cast<std::size_t>(W * wave_bytes(w.geo.group, mr) + W * 2 * mr * 16 * 4 + mr * 16 +
+                                                     (c.norm ? 2 * W * mr * 4 : 0));
     a.greedy = c.greedy;
     if (c.greedy && c.greedy_parts) *c.greedy_parts = blocks;
     const bool dbg = c.dump || c.dq_codes || c.dq_scales || c.dq_sums || c.dq_zeros;

@@ -142,6 +142,8 @@ struct QRowArgs {
     std::int8_t* q;      // [M_p][K] permuted
     float* scale_t;      // [K/128][M_p]
     std::int32_t* sum_t; // [K/128][M_p] (optional)
+    const float* ninv;   // NORM: per-row inverse RMS [M]
+    const float* nw;     // NORM: norm weight [K]
 };
 
 // g = 128. One lane per 32 columns of a row: the pieces [16 a, 16 a + 16) and [32 + 16 a, 32 + 16 a + 16) of 64-column
@@ -149,7 +151,7 @@ struct QRowArgs {
 // a 64-column block at 16 L + 8 h + i), and a group is one lane quad (2 DPP steps reduce it). Codes are packed with
 // v_cvt_pk_u8_f32 on rint(x * inverse) + 128 (an integer in [1, 255]; calibrated codes clamped to [-128, 127]
 // first), then the bias is flipped off per byte.
-template <int QM, bool F32>
+template <int QM, bool F32, bool NORM>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(QRowArgs a) {
     const int units = a.K / 32;  // lanes per row (a multiple of 16: rows never share a lane quad)
     const int t = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
@@ -183,6 +185,22 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(QRowArgs a) {
                     v[16 * p + 8 * i + 2 * d] = __uint_as_float(w4[d] << 16);
                     v[16 * p + 8 * i + 2 * d + 1] = __uint_as_float(w4[d] & 0xFFFF0000u);
                 }
+            }
+        }
+    }
+    if constexpr (NORM) {
+        // fused RMS normalization: x * inv[m] * w[k] (the row's inverse RMS comes from rms_norm_kernel)
+        const float inv = live ? a.ninv[m] : 0.F;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const float4* wp = reinterpret_cast<const float4*>(a.nw + col0 + 32 * p);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 w = wp[i];
+                v[16 * p + 4 * i] = v[16 * p + 4 * i] * inv * w.x;
+                v[16 * p + 4 * i + 1] = v[16 * p + 4 * i + 1] * inv * w.y;
+                v[16 * p + 4 * i + 2] = v[16 * p + 4 * i + 2] * inv * w.z;
+                v[16 * p + 4 * i + 3] = v[16 * p + 4 * i + 3] * inv * w.w;
             }
         }
     }
@@ -247,13 +265,19 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(QRowArgs a) {
 // launch over M_p rows x K / 32 lanes
 inline void launch_quantize_rows(const QRowArgs& q, bool calibrated, bool x_f32, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(static_cast<std::int64_t>(q.M_p) * (q.K / 32) / 256)), block(256);
+#define KQ_QR(QM, F, NM) hipLaunchKernelGGL((quantize_rows_kernel<QM, F, NM>), grid, block, 0, stream, q)
+#define KQ_QRN(QM, F) \
+    if (q.ninv) KQ_QR(QM, F, true); \
+    else KQ_QR(QM, F, false)
     if (calibrated) {
-        if (x_f32) hipLaunchKernelGGL((quantize_rows_kernel<dev::QUANT_STATIC, true>), grid, block, 0, stream, q);
-        else hipLaunchKernelGGL((quantize_rows_kernel<dev::QUANT_STATIC, false>), grid, block, 0, stream, q);
+        if (x_f32) { KQ_QRN(dev::QUANT_STATIC, true); }
+        else { KQ_QRN(dev::QUANT_STATIC, false); }
     } else {
-        if (x_f32) hipLaunchKernelGGL((quantize_rows_kernel<dev::QUANT_DYN_SYM, true>), grid, block, 0, stream, q);
-        else hipLaunchKernelGGL((quantize_rows_kernel<dev::QUANT_DYN_SYM, false>), grid, block, 0, stream, q);
+        if (x_f32) { KQ_QRN(dev::QUANT_DYN_SYM, true); }
+        else { KQ_QRN(dev::QUANT_DYN_SYM, false); }
     }
+#undef KQ_QRN
+#undef KQ_QR
 }
 
 struct GemmArgs {
@@ -909,6 +933,8 @@ hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_
     q.q = act.q;
     q.scale_t = act.scale;
     q.sum_t = nullptr;
+    q.ninv = c.norm_inv;
+    q.nw = c.norm_inv ? c.norm_w1 : nullptr;
     const GemmPlan plan = gemm_i4_plan(w, c.M, c.gelu_gate);
     launch_quantize_rows(q, stat, q.x_f32 != 0, stream);
     hipError_t e = hipGetLastError();

@@ -62,7 +62,36 @@ struct LinearCall {
     // greedy selection from the decode epilogue: partials [M][workgroups] (kq_greedy.hip), their count per row
     int4* greedy = nullptr;
     int* greedy_parts = nullptr;
+    // RMS normalization fused into the activation quantization (decode kernel prologue, prefill row quantizer):
+    //   norm 1: the projection input is x * inv(x) * norm_w1
+    //   norm 2: h = (norm_res + x * inv(x) * norm_w1) [* norm_scale] (stored to norm_hidden by one workgroup), the
+    //           projection input is h * inv(h) * norm_w2
+    // norm_inv (prefill): per-row inverse RMS already computed; the quantizer applies x * norm_inv[m] * norm_w1.
+    int norm = 0;
+    const float* norm_w1 = nullptr;
+    const float* norm_w2 = nullptr;
+    const void* norm_res = nullptr;
+    const float* norm_scale = nullptr;
+    float* norm_hidden = nullptr;
+    float norm_eps1 = 0.F, norm_eps2 = 0.F;
+    const float* norm_inv = nullptr;
 };
+
+// RMS normalization kernel (kq_norm.hip): see the modes there.
+struct NormLaunch {
+    const void* x = nullptr;
+    int x_type = ACT_F32;
+    const void* residual = nullptr;
+    const float* w1 = nullptr;
+    const float* scale = nullptr;
+    const float* w2 = nullptr;
+    float* out1 = nullptr;
+    float* out2 = nullptr;
+    float* inv_out = nullptr;
+    std::int64_t rows = 0, width = 0;
+    float eps1 = 0.F, eps2 = 0.F;
+};
+hipError_t launch_rms_norm(const NormLaunch& n, hipStream_t stream);
 
 // Launch plan of the skinny (decode, M <= 16) projection with fused activation quantization (kq_skinny.hip).
 struct SkinnyPlan {

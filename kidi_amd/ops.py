@@ -198,6 +198,55 @@ class DeviceWeight:
         tokens = tokens.reshape(x.shape[:-1])
         return tokens, (y.reshape(*x.shape[:-1], self.rows) if y is not None else None)
 
+    def linear_rms(self, x: torch.Tensor, norm_weight: torch.Tensor, epsilon: float,
+                   residual: torch.Tensor | None = None, residual_weight: torch.Tensor | None = None,
+                   residual_scale: torch.Tensor | None = None, residual_epsilon: float | None = None,
+                   input_scale: float = 0.0, output_scale: float = 0.0, gelu_gate: bool = False):
+        """(y, hidden): the projection of rms_norm(x) (or, with a residual, of rms_norm(hidden) where hidden =
+        rms_norm_residual(x, residual_weight, residual, residual_epsilon, residual_scale)), the normalization
+        fused into the activation quantization (kq_packed_linear_rms). hidden is None without a residual."""
+        if x.dim() < 1 or x.shape[-1] != self.cols:
+            raise Failure("INVALID_ARGUMENT", "packed linear shape or dtype mismatch")
+        x2 = x.reshape(-1, self.cols).contiguous()
+        m = x2.shape[0]
+        width = self.rows // 2 if gelu_gate else self.rows
+        y = torch.empty((m, width), dtype=torch.float32, device=x.device)
+        L = N.load()
+        ws_bytes = L.kq_rms_linear_workspace_size(self.handle, m)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+        a = N.LinearArgs()
+        a.x = x2.data_ptr()
+        a.x_dtype = N.KQ_BF16 if x2.dtype == torch.bfloat16 else (N.KQ_F32 if x2.dtype == torch.float32 else 99)
+        a.m = m
+        a.input_scale = input_scale
+        a.output_scale = output_scale
+        a.y = y.data_ptr()
+        a.workspace = ws.data_ptr()
+        a.workspace_bytes = ws_bytes
+        d = N.NormDesc()
+        w = norm_weight.contiguous()
+        d.weight = w.data_ptr()
+        d.epsilon = epsilon
+        keep = [w]
+        hidden = None
+        if residual is not None:
+            r = residual.reshape(-1, self.cols).contiguous()
+            if r.shape != x2.shape or r.dtype != x2.dtype or residual_weight is None:
+                raise Failure("INVALID_ARGUMENT", "invalid RMS residual normalization operands")
+            rw = residual_weight.contiguous()
+            hidden = torch.empty((m, self.cols), dtype=torch.float32, device=x.device)
+            d.residual = r.data_ptr()
+            d.residual_weight = rw.data_ptr()
+            d.residual_scale = residual_scale.data_ptr() if residual_scale is not None else None
+            d.residual_epsilon = epsilon if residual_epsilon is None else residual_epsilon
+            d.hidden = hidden.data_ptr()
+            keep += [r, rw]
+        fn = L.kq_packed_linear_rms
+        _raise(fn(self.handle, ctypes.byref(a), ctypes.byref(d), int(bool(gelu_gate)), _stream()))
+        del keep
+        y = y.reshape(*x.shape[:-1], width)
+        return y, (hidden.reshape(x.shape) if hidden is not None else None)
+
     def debug_partials(self, x: torch.Tensor, input_scale: float = 0.0, output_scale: float = 0.0):
         """(y, int32 partials [M, N, K/g]) from the same kernel as ``linear``."""
         x2 = x.reshape(-1, self.cols).contiguous()
@@ -263,6 +312,28 @@ def greedy_token(logits: torch.Tensor) -> torch.Tensor:
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=logits.device)
     _raise(L.kq_greedy_token(x.data_ptr(), rows, width, tokens.data_ptr(), ws.data_ptr(), ws_bytes, _stream()))
     return tokens.reshape(logits.shape[:-1])
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, epsilon: float, residual: torch.Tensor | None = None,
+             output_scale: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """RMS_NORM / RMS_NORM_RESIDUAL over the last axis of device F32/BF16 x (kq_rms_norm): F32 output."""
+    width = x.shape[-1]
+    x2 = x.reshape(-1, width).contiguous()
+    y = out if out is not None else torch.empty(x2.shape, dtype=torch.float32, device=x.device)
+    a = N.RmsArgs()
+    a.x = x2.data_ptr()
+    a.x_dtype = N.KQ_BF16 if x2.dtype == torch.bfloat16 else (N.KQ_F32 if x2.dtype == torch.float32 else 99)
+    a.rows = x2.shape[0]
+    a.width = width
+    w = weight.contiguous()
+    a.weight = w.data_ptr()
+    r = residual.reshape(-1, width).contiguous() if residual is not None else None
+    a.residual = r.data_ptr() if r is not None else None
+    a.output_scale = output_scale.data_ptr() if output_scale is not None else None
+    a.epsilon = epsilon
+    a.y = y.data_ptr()
+    _raise(N.load().kq_rms_norm(ctypes.byref(a), _stream()))
+    return y.reshape(x.shape)
 
 
 def _identity(t: torch.Tensor | None):
@@ -367,6 +438,39 @@ class Context:
         x = input.to(self.device) if host else input
         y = gated_feed_forward(gu, dn, x, gate_up_input_scale, gate_up_output_scale, down_input_scale,
                                down_output_scale, silu)
+        return y.cpu() if host else y
+
+    @staticmethod
+    def _validate_norm(input, scale, epsilon, residual=None, output_scale=None):
+        # Context::rms_norm_residual (ops/context.cpp:1106-1112) and Impl::run's RMS_NORM checks (:317-330)
+        if (input is None or input.dim() == 0 or input.dtype not in (torch.float32, torch.bfloat16) or scale is None
+                or scale.dim() != 1 or scale.shape[0] != input.shape[-1] or scale.dtype != torch.float32
+                or not math.isfinite(epsilon) or epsilon <= 0):
+            raise Failure("INVALID_ARGUMENT", "invalid RMS residual normalization operands")
+        if residual is not None and (residual.dtype != input.dtype or tuple(residual.shape) != tuple(input.shape)):
+            raise Failure("INVALID_ARGUMENT", "invalid RMS residual normalization operands")
+        if output_scale is not None and (output_scale.dtype != torch.float32 or output_scale.numel() != 1):
+            raise Failure("INVALID_ARGUMENT", "invalid RMS residual normalization operands")
+
+    def rms_norm(self, input: torch.Tensor, scale: torch.Tensor, epsilon: float) -> torch.Tensor:
+        """Context::rms_norm (ops/context.cpp:1043-1049): F32 output; host tensors return host results."""
+        self._validate_norm(input, scale, epsilon)
+        host = not input.is_cuda
+        x = input.to(self.device) if host else input
+        y = rms_norm(x, scale.to(self.device), epsilon)
+        return y.cpu() if host else y
+
+    def rms_norm_residual(self, input: torch.Tensor, scale: torch.Tensor, residual: torch.Tensor, epsilon: float,
+                          output_scale: torch.Tensor | None = None) -> torch.Tensor:
+        """Context::rms_norm_residual (ops/context.cpp:1103-1122): (residual + rms_norm(input)) [* output_scale]."""
+        if residual is None:
+            raise Failure("INVALID_ARGUMENT", "invalid RMS residual normalization operands")
+        self._validate_norm(input, scale, epsilon, residual, output_scale)
+        host = not input.is_cuda
+        x = input.to(self.device) if host else input
+        r = residual.to(self.device) if host else residual
+        o = output_scale.to(self.device).reshape(1) if output_scale is not None else None
+        y = rms_norm(x, scale.to(self.device), epsilon, residual=r, output_scale=o)
         return y.cpu() if host else y
 
     def greedy_token(self, logits: torch.Tensor) -> torch.Tensor:

@@ -24,6 +24,11 @@
 //                           expected value); portable float path pinned to 1e-3 / 0.05 by eager_test.cpp:300-378.
 //   kqr_gelu_tanh           pinned by eager_test.cpp:431-452 (formula to 1e-5 and exact saturation values).
 //   kqr_silu_gate           pinned by eager_test.cpp:167-186 (g / (1 + exp(-g)) * up to 1e-5).
+//   kqr_rms_norm            pinned: eager_test.cpp:388-412 KAT (plain, 2x weight, residual, scaled; zero row
+//                           exactly 0), cuda/operators_test.cpp:346-350 identity (residual form == (norm + r) * s
+//                           exactly), float64 closed form to a few ulp, power-of-two weight scaling exact. The
+//                           summation order of the sum of squares is this build's definition (Kidi's
+//                           ynn::rms_norm_f32 order is unknown); the GPU paths follow the same order.
 //
 // Floating point: compiled with -ffp-contract=off so every a*b+c rounds twice, as ISO C++ evaluation does.
 
@@ -505,6 +510,60 @@ void kqr_silu_gate(const float* gate_up, std::int64_t rows, std::int64_t width, 
             const float u = gate_up[r * 2 * width + width + i];
             out[r * width + i] = g / (1.F + std::exp(-g)) * u;
         }
+}
+
+// RMS normalization over the last axis (Context::rms_norm / rms_norm_residual, ops/context.cpp:1043-1049,
+// :1103-1122; Kidi's CPU RmsNorm operator, runtime/ynn/operators.cpp:553-620, whose parity form :598-614 reads
+//   inverse = 1 / sqrt(sum / width + epsilon);  y = x * inverse * weight;  residual: y = (r + x * inverse * weight)
+//   [* scale]).
+// The sum of squares has one fixed order: the row is cut into 512-column segments and each segment into 64
+// pieces of 8 columns (columns past the width count as 0, which adds exactly nothing); a piece is summed in column
+// order (s = x0*x0, s = s + x1*x1, ...), the 64 pieces of a segment pairwise as a balanced tree in piece order
+// (pieces 2i and 2i+1 first, then pairs of those, ...), the segments in order.
+float rms_sum_squares(const float* x, std::int64_t width) {
+    float total = 0.F;
+    for (std::int64_t seg = 0; seg * 512 < width; ++seg) {
+        float piece[64];
+        for (int l = 0; l < 64; ++l) {
+            float s = 0.F;
+            for (int i = 0; i < 8; ++i) {
+                const std::int64_t k = seg * 512 + 8 * l + i;
+                const float v = k < width ? x[k] : 0.F;
+                s = i == 0 ? v * v : s + v * v;
+            }
+            piece[l] = s;
+        }
+        for (int span = 1; span < 64; span *= 2)
+            for (int l = 0; l < 64; l += 2 * span) piece[l] = piece[l] + piece[l + span];
+        total = seg == 0 ? piece[0] : total + piece[0];
+    }
+    return total;
+}
+
+// x and residual are F32 or BF16 [rows, width] (residual may be NULL: RMS_NORM); weight F32 [width]; scale NULL or
+// one float (the residual form's scalar). y F32 [rows, width]. inverse (optional) receives 1 / rms per row.
+// Returns -1 for INVALID_ARGUMENT (epsilon not finite or <= 0, context.cpp:1108).
+int kqr_rms_norm(const void* x, int x_dtype, std::int64_t rows, std::int64_t width, const float* weight,
+                 const void* residual, const float* scale, float epsilon, float* y, float* inverse) {
+    if ((x_dtype != F32 && x_dtype != BF16) || rows < 0 || width <= 0 || !std::isfinite(epsilon) || epsilon <= 0)
+        return -1;
+    std::vector<float> row(static_cast<std::size_t>(width));
+    for (std::int64_t r = 0; r < rows; ++r) {
+        for (std::int64_t i = 0; i < width; ++i) row[static_cast<std::size_t>(i)] = load_float(x, x_dtype, static_cast<std::size_t>(r * width + i));
+        const float sum = rms_sum_squares(row.data(), width);
+        const float inv = 1.F / std::sqrt(sum / static_cast<float>(width) + epsilon);
+        if (inverse) inverse[r] = inv;
+        for (std::int64_t i = 0; i < width; ++i) {
+            const float n = row[static_cast<std::size_t>(i)] * inv * weight[i];
+            if (!residual) {
+                y[r * width + i] = n;
+                continue;
+            }
+            const float v = load_float(residual, x_dtype, static_cast<std::size_t>(r * width + i)) + n;
+            y[r * width + i] = scale ? v * scale[0] : v;
+        }
+    }
+    return 0;
 }
 
 }  // extern "C"

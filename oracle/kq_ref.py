@@ -57,6 +57,8 @@ def lib() -> ctypes.CDLL:
         L.kqr_gelu_gate.restype = None
         L.kqr_silu_gate.argtypes = [vp, i64, i64, vp]
         L.kqr_silu_gate.restype = None
+        L.kqr_rms_norm.argtypes = [vp, i32, i64, i64, vp, vp, vp, f32, vp, vp]
+        L.kqr_rms_norm.restype = i32
         _lib = L
     return _lib
 
@@ -240,6 +242,28 @@ def greedy_token(logits: np.ndarray) -> np.ndarray:
     for r, row in enumerate(rows):
         out[r] = -1 if not np.all(np.isfinite(row)) else int(np.argmax(row))  # argmax returns the first maximum
     return out.reshape(x.shape[:-1])
+
+
+def rms_norm(x: np.ndarray, weight: np.ndarray, epsilon: float, residual: np.ndarray | None = None,
+             scale: float | None = None, x_bf16: bool = False):
+    """RMS normalization over the last axis (Context::rms_norm / rms_norm_residual, ops/context.cpp:1043-1049,
+    :1103-1122; RmsNorm, runtime/ynn/operators.cpp:553-620): y = x * inv * weight, or with a residual
+    (r + x * inv * weight) [* scale], inv = 1 / sqrt(sum(x^2) / width + epsilon) in the fixed summation order of
+    kq_ref.cpp. x (and residual) are float32, or bf16 bit patterns (uint16) with x_bf16. Returns (y, inv per row)."""
+    xa = np.ascontiguousarray(x, dtype=np.uint16 if x_bf16 else np.float32)
+    width = xa.shape[-1]
+    rows = xa.size // width if width else 0
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    r = None if residual is None else np.ascontiguousarray(residual, dtype=xa.dtype)
+    if r is not None and r.shape != xa.shape:
+        raise ValueError("residual shape mismatch")
+    s = None if scale is None else np.array([scale], np.float32)
+    y = np.zeros(xa.shape, np.float32)
+    inv = np.zeros(max(rows, 1), np.float32)
+    rc = lib().kqr_rms_norm(_p(xa), BF16 if x_bf16 else F32, rows, width, _p(w), _p(r), _p(s), epsilon, _p(y), _p(inv))
+    if rc != 0:
+        raise ValueError("invalid RMS normalization operands")
+    return y, inv[:rows]
 
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
