@@ -50,6 +50,8 @@ def parse():
     p.add_argument("--prefill-steps", type=int, default=50)
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget (0 = skip)")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-extras", action="store_true",
+                   help="skip the configs[3]/configs[4] projections and the fused-operator timings")
     p.add_argument("--pmc-workload", action="store_true",
                    help="run the HBM-traffic workload for rocprofv3 --pmc passes (a plain 256 MiB copy for calibration, "
                         "then every rotated decode projection twice, one launch each, no graphs) and exit")
@@ -311,6 +313,8 @@ def main():
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(torch, *first_cpu, x_cpu, G_DEC, args.cpu_seconds)
 
+    extras = None if args.no_extras else bench_extras(torch, N_, lib, dev, gen)
+
     out = {
         "metric": "int4 GEMV GB/s (% HBM peak) at M=1; prefill GEMM TOPS (% MFMA peak)",
         "value": round(value, 2),
@@ -336,8 +340,203 @@ def main():
                     "mfma_frac": round(pre_tops / INT8_PEAK_TOPS, 4), "parity_ok": bool(pre_ok),
                     "max_abs_err": pre_err},
         "cpu_baseline": cpu,
+        "extras": extras,
     }
     print(json.dumps(out), flush=True)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Extras: configs[3] (decoder-layer projections) and configs[4] (mixed 2/4/8-bit stack, int8 output head), and the
+# fused operators beside the plain projection. Each figure is the average device time per call over HIP-graph
+# replays of R rotated weights whose combined size exceeds the 256 MB Infinity Cache.
+
+def layer_bytes(M, K, N, g, bits, asym, out_cols=None):
+    """Algorithmic bytes of one projection call: codes + fp16 scales [+ uint4 zero points] + bf16 x + fp32 y."""
+    return N * K * bits // 8 + N * (K // g) * 2 + (N * (K // g) // 2 if asym else 0) + M * K * 2 + M * (out_cols or N) * 4
+
+
+class Extras:
+    def __init__(self, torch, N_, lib, dev, gen):
+        self.torch, self.N_, self.lib, self.dev, self.gen = torch, N_, lib, dev, gen
+        self.stream_ptr = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def weight(self, N, K, bits, g, asym, code_bytes=None):
+        from kidi_amd.ops import DeviceWeight
+
+        t, dev, gen = self.torch, self.dev, self.gen
+        values = t.randint(0, 256, (N, K * bits // 8), dtype=t.uint8, device=dev, generator=gen)
+        scales = (t.rand((N, K // g), device=dev, generator=gen) * 0.018 + 0.002).to(t.float16)
+        zp = t.randint(0, 16, (N, K // g), dtype=t.uint8, device=dev, generator=gen) if asym else None
+        return DeviceWeight(values, scales, bits, g, zp)
+
+    def weights(self, N, K, bits, g, asym, rotate=None):
+        one = layer_bytes(0, K, N, g, bits, asym)
+        R = rotate or max(1, min(64, -(-600_000_000 // one)))
+        return [self.weight(N, K, bits, g, asym) for _ in range(R)]
+
+    def x(self, M, K):
+        return make_x(self.torch, self.dev, self.gen, M, K)
+
+    def args(self, dw, x, M, y, input_scale=0.0, ws_bytes=None):
+        t, N_ = self.torch, self.N_
+        if ws_bytes is None:
+            ws_bytes = self.lib.kq_linear_workspace_size(dw.handle, M)
+        ws = t.empty(max(ws_bytes, 1), dtype=t.uint8, device=self.dev)
+        a = N_.LinearArgs()
+        a.x = x.data_ptr()
+        a.x_dtype = N_.KQ_BF16
+        a.m = M
+        a.input_scale = input_scale
+        a.output_scale = 0.0
+        a.y = y.data_ptr() if y is not None else None
+        a.workspace = ws.data_ptr()
+        a.workspace_bytes = ws_bytes
+        return a, ws
+
+    def time_calls(self, calls, reps):
+        """Average device time (us) per call of `calls`, replayed from one HIP graph `reps` times."""
+        t = self.torch
+        for c in calls:  # eager once: errors surface here, not inside the capture
+            c(self.stream_ptr())
+        t.cuda.synchronize()
+        g = capture(t, calls, self.stream_ptr)
+        g.replay()
+        t.cuda.synchronize()
+        stream = t.cuda.current_stream()
+        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        t.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * len(calls))
+
+    def linear_calls(self, dws, x, M, out_cols, fn="kq_packed_linear", input_scale=0.0):
+        """Calls of `fn` over `dws`, plus `keep`: every tensor and argument block the calls point into. The caller
+        must hold `keep` while the calls (or a graph of them) can run: torch.cuda.graph() empties the allocator
+        cache on entry, so an output whose tensor was dropped would be unmapped under the replayed kernels."""
+        t, lib = self.torch, self.lib
+        calls = []
+        y = t.empty((M, out_cols), dtype=t.float32, device=self.dev)
+        keep = [x, y]
+        for dw in dws:
+            a, ws = self.args(dw, x, M, y, input_scale)
+            keep += [a, ws]
+            f = getattr(lib, fn)
+            calls.append(lambda s, h=dw.handle, p=ctypes.byref(a), f=f: _ok(lib, f(h, p, s)))
+        return calls, keep
+
+
+def _ok(lib, status):
+    if status != 0:
+        raise RuntimeError(lib.kq_last_error().decode())
+
+
+def bench_extras(torch, N_, lib, dev, gen):
+    E = Extras(torch, N_, lib, dev, gen)
+    out = {}
+    H, I, KV = 2048, 8192, 2048 + 256 + 256
+    # configs[3]: decoder-layer projections, M = 1 (GB/s) and M = 2048 (TOP/s)
+    qkv = E.weights(KV, H, 4, 32, False)
+    gate_up = E.weights(2 * I, H, 4, 128, True)
+    down = E.weights(H, I, 4, 128, True)
+    layer = {}
+    for M in (1, 2048):
+        xh, xi = E.x(M, H), E.x(M, I)
+        rows = {}
+        for name, dws, x, K, N, g, asym, fn, cols in (
+                ("qkv_g32", qkv, xh, H, KV, 32, False, "kq_packed_linear", KV),
+                ("gate_up_gelu_g128", gate_up, xh, H, 2 * I, 128, True, "kq_packed_linear_gelu_gate", I),
+                ("down_g128", down, xi, I, H, 128, True, "kq_packed_linear", H)):
+            use = dws if M == 1 else dws[:2]
+            calls, keep = E.linear_calls(use, x, M, cols, fn)
+            us = E.time_calls(calls, 20 if M == 1 else 3)
+            b = layer_bytes(M, K, N, g, 4, asym, cols)
+            ops = 2 * M * N * K
+            rows[name] = {"us": round(us, 3), "gbs": round(b / us / 1e3, 1), "tops": round(ops / us / 1e6, 1),
+                          "rotated": len(use)}
+            del calls, keep
+        # the three projections of one layer back to back (rotating layers)
+        if M == 1:
+            calls, keep = [], []
+            for i in range(len(down)):
+                for dws, x, cols, fn in ((qkv, xh, KV, "kq_packed_linear"), (gate_up, xh, I, "kq_packed_linear_gelu_gate"),
+                                         (down, xi, H, "kq_packed_linear")):
+                    c, k = E.linear_calls([dws[i % len(dws)]], x, M, cols, fn)
+                    calls += c
+                    keep += k
+            rows["layer_us"] = round(E.time_calls(calls, 5) * 3, 3)
+            del calls, keep
+        layer[f"M{M}"] = rows
+    out["configs3_layer"] = layer
+
+    # fused RMS normalization before the projection (kq_packed_linear_rms) against norm + projection, M = 1
+    x1, r1 = E.x(1, H), E.x(1, H)
+    wn = torch.rand(H, device=dev, generator=gen) + 0.5
+    hidden = torch.empty((1, H), dtype=torch.float32, device=dev)
+    normed = torch.empty((1, H), dtype=torch.float32, device=dev)
+    y = torch.empty((1, I), dtype=torch.float32, device=dev)
+    keep = []
+    fused, composed = [], []
+    for dw in gate_up:
+        a, ws = E.args(dw, x1, 1, y, ws_bytes=lib.kq_rms_linear_workspace_size(dw.handle, 1))
+        d = N_.NormDesc()
+        d.weight, d.epsilon = wn.data_ptr(), 1e-6
+        d.residual, d.residual_weight, d.residual_epsilon, d.hidden = r1.data_ptr(), wn.data_ptr(), 1e-6, hidden.data_ptr()
+        keep += [a, ws, d]
+        fused.append(lambda s, h=dw.handle, p=ctypes.byref(a), q=ctypes.byref(d):
+                     _ok(lib, lib.kq_packed_linear_rms(h, p, q, 1, s)))
+        ra = N_.RmsArgs()
+        ra.x, ra.x_dtype, ra.rows, ra.width = x1.data_ptr(), N_.KQ_BF16, 1, H
+        ra.weight, ra.residual, ra.epsilon, ra.y = wn.data_ptr(), r1.data_ptr(), 1e-6, hidden.data_ptr()
+        rb = N_.RmsArgs()
+        rb.x, rb.x_dtype, rb.rows, rb.width = hidden.data_ptr(), N_.KQ_F32, 1, H
+        rb.weight, rb.epsilon, rb.y = wn.data_ptr(), 1e-6, normed.data_ptr()
+        a2, ws2 = E.args(dw, normed, 1, y)
+        a2.x_dtype = N_.KQ_F32
+        keep += [ra, rb, a2, ws2]
+        composed += [lambda s, p=ctypes.byref(ra): _ok(lib, lib.kq_rms_norm(p, s)),
+                     lambda s, p=ctypes.byref(rb): _ok(lib, lib.kq_rms_norm(p, s)),
+                     lambda s, h=dw.handle, p=ctypes.byref(a2): _ok(lib, lib.kq_packed_linear_gelu_gate(h, p, s))]
+    out["rms_residual_gate_up_M1"] = {"fused_us": round(E.time_calls(fused, 20), 3),
+                                      "composed_us": round(E.time_calls(composed, 20) * 3, 3),
+                                      "composed": "kq_rms_norm (residual) + kq_rms_norm + kq_packed_linear_gelu_gate"}
+    del fused, composed, keep, gate_up, qkv, down
+    torch.cuda.empty_cache()
+
+    # configs[4]: mixed 2/4/8-bit projections K = 2048, N = 8192 at M = 1; output head int8 g = 32, N = 262,144
+    mixed = {}
+    xm = E.x(1, 2048)
+    for name, bits, g, asym, in_s in (("int2_g32_calibrated", 2, 32, False, 0.03), ("int4_g128_asym", 4, 128, True, 0.0),
+                                      ("int8_g32_sym", 8, 32, False, 0.0)):
+        dws = E.weights(8192, 2048, bits, g, asym)
+        calls, keep = E.linear_calls(dws, xm, 1, 8192, input_scale=in_s)
+        us = E.time_calls(calls, 20)
+        b = layer_bytes(1, 2048, 8192, g, bits, asym)
+        mixed[name] = {"us": round(us, 3), "gbs": round(b / us / 1e3, 1), "rotated": len(dws)}
+        del calls, keep, dws
+    head = E.weights(262144, 2048, 8, 32, False, rotate=2)
+    for M in (1, 8):
+        xh = E.x(M, 2048)
+        calls, keep = E.linear_calls(head, xh, M, 262144)
+        us = E.time_calls(calls, 10)
+        b = layer_bytes(M, 2048, 262144, 32, 8, False)
+        tok = torch.empty((M,), dtype=torch.int32, device=dev)
+        keep += [xh, tok]
+        gcalls = []
+        for dw in head:
+            a, ws = E.args(dw, xh, M, None, ws_bytes=lib.kq_greedy_linear_workspace_size(dw.handle, M))
+            keep += [a, ws]
+            gcalls.append(lambda s, h=dw.handle, p=ctypes.byref(a): _ok(lib, lib.kq_packed_linear_greedy(h, p, tok.data_ptr(), s)))
+        gus = E.time_calls(gcalls, 10)
+        mixed[f"head_int8_g32_M{M}"] = {"us": round(us, 3), "gbs": round(b / us / 1e3, 1),
+                                        "greedy_us": round(gus, 3),
+                                        "greedy_gbs": round((b - M * 262144 * 4) / gus / 1e3, 1)}
+        del calls, gcalls, keep
+    out["configs4_mixed"] = mixed
+    del head
+    torch.cuda.empty_cache()
+    return out
 
 
 def load_traffic():
