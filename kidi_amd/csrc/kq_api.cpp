@@ -402,6 +402,12 @@ kq_status run_call(kq::LinearCall& c, const kq_linear_args* args, std::size_t ws
         if (e != hipSuccess) return hip_fail(e, "prefill projection launch");
         return KQ_OK;
     }
+    // Prefill, 4-bit g = 32 / 64 (fused QKV): quantizer + two-stage int8 MFMA GEMM.
+    if (kq::gemm_i4g_fits(c)) {
+        e = kq::launch_gemm_i4g(c, stream);
+        if (e != hipSuccess) return hip_fail(e, "prefill projection launch");
+        return KQ_OK;
+    }
     // GELU gating is fused into the tiled GEMV/GEMM when the gate and up halves are whole tiles; otherwise the
     // full projection goes to a scratch buffer and a gating kernel follows.
     const bool fused_gelu = c.gelu_gate && c.path != kq::PATH_PORTABLE && c.w->tiled && (c.w->geo.rows / 2) % kq::kTileRows == 0;

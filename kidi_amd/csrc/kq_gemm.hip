@@ -715,6 +715,9 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
             mfmas(blk, cn, kn4);
             if (blk == 4) raw = unpack_read(s1, s1);
             if (blk == 6) unpack_write(raw, (kt - kofs + 1) & 1);
+            // block 0's partials: only block 1's MFMAs lie between them and their first VALU read, fewer than the
+            // 8 wait states an int8 MFMA result needs (the hazard recognizer does not see into inline assembly)
+            if (blk == 1 && !DBG) KQ_ASM("s_nop 7");
             epilogue(cp, kp, blk - 1, kt);
             cp = cn;
             kp = kn4;

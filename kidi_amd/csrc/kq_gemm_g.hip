@@ -1,0 +1,388 @@
+// Prefill projection (M > 16) for 4-bit weights with small groups, g = 32 or 64 (the fused QKV of a decoder layer is
+// g = 32): Kidi's BlockwiseLinear / SymmetricPackedLinear closed forms (runtime/ynn/operators.cpp:1118-1169,
+// :1250-1308) over int8 activation codes from quantize_kernel ([M_p][K] in the tiles' permuted order, block scales
+// [M_p][K/g]).
+//
+// Workgroup tile 128 rows x 128 output columns (8 weight row tiles), 4 waves of 64 x 64 (16 blocks of 16 x 16), one
+// 128-column k step per iteration = 128/g groups. LDS holds two stages; each step the next step's operands travel
+// global -> registers (issued before the step's MFMAs) -> LDS (after them): activation codes XOR-swizzled by row so
+// the A-operand reads spread over the banks, packed int4 tiles unpacked to int8 with the zero point of each byte's
+// group folded in (byte = u - zp), weight scales as f32 [group][wave column][row][tile], activation scales
+// [group][128] with the four rows a lane scales adjacent. Per 16 x 16 block and group: one int8 MFMA gives the exact
+// partial P' = sum q (u - zp) of the group (v_mfma_i32_16x16x32_i8 on the 8 bytes of a lane that belong to a
+// 32-column group, v_mfma_i32_16x16x64_i8 for g = 64), one v_mfma_f32_4x4x1 gives a_s * s in the accumulator's
+// lane layout, and acc += (a_s * s) * P' is the epilogue. The epilogue runs once per group, so small groups make
+// this kernel VALU-bound: two VALU per output element and group against one int8 MAC pass of 32 or 64 columns.
+// Two workgroups fit a CU (72 KB of LDS at g = 32), so a 2048 x 2560 projection (320 tiles) runs in one wave of
+// workgroups.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kq_device.hpp"
+#include "kq_internal.hpp"
+
+namespace kq {
+namespace {
+
+using namespace dev;
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// (the host pass sees the kernel bodies too; the assembly is device-only)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define KQ_GASM(...) asm volatile(__VA_ARGS__)
+#else
+#define KQ_GASM(...) (void)0
+#endif
+
+constexpr int kBM = 128, kBK = 128, kSlots = 8;  // rows, columns per step, row tiles per workgroup
+
+template <int G>
+struct GShape {
+    static constexpr int GPS = kBK / G;                  // groups per step
+    static constexpr int A_BYTES = kBM * kBK;            // codes [row][128], 16-byte chunks swizzled
+    static constexpr int B_BYTES = kSlots * 2048;        // unpacked int8 [slot][64-column half][lane][16 B]
+    static constexpr int WS_BYTES = GPS * 2 * 16 * 4 * 4;  // f32 [group][wave column][row nn][tile ni]
+    static constexpr int AS_BYTES = GPS * kBM * 4;       // f32 [group][row position]
+    static constexpr int B_OFF = A_BYTES, WS_OFF = B_OFF + B_BYTES, AS_OFF = WS_OFF + WS_BYTES;
+    static constexpr int STAGE = AS_OFF + AS_BYTES;
+    static constexpr int LDS = 2 * STAGE;
+    static constexpr int META_PER_THREAD = GPS * kBM / 256;  // weight scales (and activation scales) per thread
+    static_assert(LDS <= 80 * 1024, "two workgroups per CU");
+};
+
+struct GArgs {
+    const std::int8_t* q;      // [M_p][K] permuted codes
+    const float* a_scale;      // [M_p][groups_p]
+    const std::uint8_t* tiles;
+    const void* scales;        // [n_tiles][groups_p][16] F16|F32
+    const std::uint8_t* zero_points;  // [n_tiles][groups_p][8] nibble pairs, or null (symmetric: 8)
+    float* y;
+    std::int32_t* dump;        // optional int32 partials [M][N][groups]
+    int M, M_p, N, K, k_tiles, n_tiles, groups_p, groups;
+    float input_scale, output_scale;
+    int m_blocks, n_blocks;
+};
+
+// position of row r (0..127) in the activation-scale stage: rows 16 q + t of a 64-row half at 4 t + q, so a lane's
+// four rows 16 mi + t (mi = 0..3) are one 16-byte read
+__device__ __forceinline__ int as_pos(int r) { return (r & 64) | ((r & 15) << 2) | ((r >> 4) & 3); }
+
+template <int G, int QM, bool ZP, bool SH, bool DBG>
+__global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
+    using S = GShape<G>;
+    constexpr int GPS = S::GPS;
+    extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int nn = lane & 15, L = lane >> 4;
+
+    // workgroup -> tile; each XCD (every 8th workgroup) takes a contiguous range of tiles, column-block major, so its
+    // L2 holds few weight column blocks
+    const int total = a.m_blocks * a.n_blocks;
+    int bid = blockIdx.x;
+    if (total % 8 == 0) bid = (bid % 8) * (total / 8) + bid / 8;
+    const int mb = bid % a.m_blocks, nb = bid / a.m_blocks;
+    const int m0 = mb * kBM;
+
+    // ---- per-thread copy assignments (fixed for the whole K loop) ----
+    // activation codes: chunks c = tid + 256 i of 16 bytes, row c / 8, chunk c % 8
+    const std::int8_t* a_src[4];
+    int a_dst[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = tid + 256 * i, r = c >> 3, ch = c & 7;
+        a_src[i] = a.q + static_cast<std::int64_t>(m0 + r) * a.K + ch * 16;
+        a_dst[i] = r * kBK + ((ch ^ (r & 7)) << 4);
+    }
+    // packed tiles: lane slots c = tid + 256 i of the 8 tiles: tile slot c / 64, lane slot s = c % 64 (row s % 16)
+    const std::uint8_t* b_src[2];
+    int b_nt[2], b_dst[2], b_row[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = tid + 256 * i, t = c >> 6, s = c & 63;
+        const int nt = nb * kSlots + t;
+        b_nt[i] = nt < a.n_tiles ? nt : -1;
+        b_src[i] = a.tiles + static_cast<std::int64_t>(nt < a.n_tiles ? nt : 0) * a.k_tiles * kTileBytes + s * 16;
+        b_dst[i] = S::B_OFF + t * 2048 + s * 16;
+        b_row[i] = s & 15;
+    }
+    // metadata: values v = tid + 256 i: group v / 128, then (weight scales) tile slot (v / 16) % 8 and row v % 16,
+    // or (activation scales) row v % 128
+    int m_g[S::META_PER_THREAD], m_t[S::META_PER_THREAD], m_r[S::META_PER_THREAD];
+#pragma unroll
+    for (int i = 0; i < S::META_PER_THREAD; ++i) {
+        const int v = tid + 256 * i;
+        m_g[i] = v >> 7;
+        m_t[i] = (v >> 4) & 7;
+        m_r[i] = v & 127;
+    }
+
+    // the next step's operands, held in registers while the current step computes
+    v4u pa[4], pb[2];
+    std::uint32_t pz[2][GPS];
+    float pws[S::META_PER_THREAD], pas[S::META_PER_THREAD];
+    auto load = [&](int k) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pa[i] = *reinterpret_cast<const v4u*>(a_src[i] + k * kBK);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            pb[i] = b_nt[i] >= 0 ? __builtin_nontemporal_load(reinterpret_cast<const v4u*>(b_src[i] + static_cast<std::int64_t>(k) * kTileBytes))
+                                 : v4u{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int h = 0; h < GPS; ++h) {
+                pz[i][h] = 8;
+                if (ZP && b_nt[i] >= 0)
+                    pz[i][h] = a.zero_points[(static_cast<std::int64_t>(b_nt[i]) * a.groups_p + k * GPS + h) * 8 + (b_row[i] >> 1)];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < S::META_PER_THREAD; ++i) {
+            const int nt = nb * kSlots + m_t[i];
+            float s = 0.F;
+            if (nt < a.n_tiles) {
+                const std::int64_t mi = (static_cast<std::int64_t>(nt) * a.groups_p + k * GPS + m_g[i]) * kTileRows + (m_r[i] & 15);
+                s = SH ? __half2float(static_cast<const __half*>(a.scales)[mi]) : static_cast<const float*>(a.scales)[mi];
+            }
+            pws[i] = s;
+            pas[i] = QM == QUANT_STATIC ? 0.F : a.a_scale[static_cast<std::int64_t>(m0 + m_r[i]) * a.groups_p + k * GPS + m_g[i]];
+        }
+    };
+    auto store = [&](int stage) {
+        std::uint8_t* st = lds + stage * S::STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<v4u*>(st + a_dst[i]) = pa[i];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            // 64-column half j: dwords 2j, 2j + 1 hold its 16 codes (low nibbles, then high nibbles); bytes 0-7 of
+            // the unpacked half are its first 32 columns, bytes 8-15 the second
+            const std::uint32_t w[4] = {pb[i].x, pb[i].y, pb[i].z, pb[i].w};
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                std::uint32_t z0, z1;  // zero point (in every byte) of bytes 0-7 and of bytes 8-15
+                if constexpr (G == 32) {
+                    z0 = (pz[i][2 * j] >> (4 * (b_row[i] & 1))) & 15u;
+                    z1 = (pz[i][2 * j + 1] >> (4 * (b_row[i] & 1))) & 15u;
+                } else {
+                    z0 = z1 = (pz[i][j] >> (4 * (b_row[i] & 1))) & 15u;
+                }
+                if (!ZP) z0 = z1 = 8u;
+                const std::uint32_t zz0 = z0 * 0x01010101u, zz1 = z1 * 0x01010101u;
+                const std::uint32_t d0 = w[2 * j], d1 = w[2 * j + 1];
+                uint4 o;
+                o.x = (((d0 & 0x0F0F0F0Fu) | 0x80808080u) - zz0) ^ 0x80808080u;
+                o.y = ((((d0 >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - zz0) ^ 0x80808080u;
+                o.z = (((d1 & 0x0F0F0F0Fu) | 0x80808080u) - zz1) ^ 0x80808080u;
+                o.w = ((((d1 >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - zz1) ^ 0x80808080u;
+                *reinterpret_cast<uint4*>(st + b_dst[i] + j * 1024) = o;
+            }
+        }
+        float* ws = reinterpret_cast<float*>(st + S::WS_OFF);
+        float* as = reinterpret_cast<float*>(st + S::AS_OFF);
+#pragma unroll
+        for (int i = 0; i < S::META_PER_THREAD; ++i) {
+            ws[((m_g[i] * 2 + (m_t[i] >> 2)) * 16 + (m_r[i] & 15)) * 4 + (m_t[i] & 3)] = pws[i];
+            as[m_g[i] * kBM + as_pos(m_r[i])] = pas[i];
+        }
+    };
+
+    float acc[4][4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[mi][ni][r] = 0.F;
+    const v4f zerof = {0.F, 0.F, 0.F, 0.F};
+    const v4i zero = {0, 0, 0, 0};
+
+    load(0);
+    store(0);
+    __syncthreads();
+
+    for (int k = 0; k < a.k_tiles; ++k) {
+        const bool more = k + 1 < a.k_tiles;
+        if (more) load(k + 1);
+        const std::uint8_t* st = lds + (k & 1) * S::STAGE;
+        const float* ws = reinterpret_cast<const float*>(st + S::WS_OFF);
+        const float* as = reinterpret_cast<const float*>(st + S::AS_OFF);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            v4i A[4], B[4];
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                const int row = wm * 64 + mi * 16 + nn;
+                A[mi] = *reinterpret_cast<const v4i*>(st + row * kBK + (((4 * j + L) ^ (row & 7)) << 4));
+            }
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni)
+                B[ni] = *reinterpret_cast<const v4i*>(st + S::B_OFF + (4 * wn + ni) * 2048 + j * 1024 + lane * 16);
+            constexpr int HALVES = G == 32 ? 2 : 1;  // groups in this 64-column half
+#pragma unroll
+            for (int h = 0; h < HALVES; ++h) {
+                const int gi = G == 32 ? 2 * j + h : j;  // group of the step
+                const v4f sv4 = *reinterpret_cast<const v4f*>(ws + ((gi * 2 + wn) * 16 + nn) * 4);
+                v4f as4 = zerof;
+                if constexpr (QM != QUANT_STATIC) as4 = *reinterpret_cast<const v4f*>(as + gi * kBM + wm * 64 + 4 * (4 * L + (lane & 3)));
+                // block blk = 4 mi + ni: the exact group partial and (dynamic) a_s * s in the accumulator layout.
+                // The MFMAs and the epilogue are volatile assembly so their issue order stays as written (the
+                // compiler would hoist every MFMA of the step above the first epilogue and spill the results);
+                // the debug variant, which stores partials, uses the builtins.
+                auto mfmas = [&](int blk, v4i& c, v4f& kk) {
+                    const int mi = blk >> 2, ni = blk & 3;
+                    const long av = (static_cast<long>(static_cast<std::uint32_t>(A[mi][2 * h + 1])) << 32) |
+                                    static_cast<std::uint32_t>(A[mi][2 * h]);
+                    const long bv = (static_cast<long>(static_cast<std::uint32_t>(B[ni][2 * h + 1])) << 32) |
+                                    static_cast<std::uint32_t>(B[ni][2 * h]);
+                    if constexpr (!DBG) {
+                        if constexpr (G == 32) KQ_GASM("v_mfma_i32_16x16x32_i8 %0, %1, %2, 0" : "=&v"(c) : "v"(av), "v"(bv));
+                        else KQ_GASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=&v"(c) : "v"(A[mi]), "v"(B[ni]));
+                        if constexpr (QM != QUANT_STATIC)
+                            KQ_GASM("v_mfma_f32_4x4x1_16b_f32 %0, %1, %2, 0" : "=&v"(kk) : "v"(as4[mi]), "v"(sv4[ni]));
+                        return;
+                    }
+                    if constexpr (G == 32) c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, zero, 0, 0, 0);
+                    else c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], B[ni], zero, 0, 0, 0);
+                    if constexpr (QM != QUANT_STATIC) kk = __builtin_amdgcn_mfma_f32_4x4x1f32(as4[mi], sv4[ni], zerof, 0, 0, 0);
+                };
+                auto epilogue = [&](int blk, const v4i& c, const v4f& kk) {
+                    const int mi = blk >> 2, ni = blk & 3;
+                    if constexpr (!DBG) {
+                        float t[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) KQ_GASM("v_cvt_f32_i32 %0, %1" : "=v"(t[r]) : "v"(c[r]));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float scale = QM == QUANT_STATIC ? sv4[ni] : kk[r];
+                            KQ_GASM("v_fmac_f32 %0, %1, %2" : "+v"(acc[mi][ni][r]) : "v"(scale), "v"(t[r]));
+                        }
+                        return;
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int row = m0 + wm * 64 + mi * 16 + 4 * L + r;
+                        const int nt = nb * kSlots + 4 * wn + ni, col = nt * kTileRows + nn;
+                        const int b = k * GPS + gi;
+                        if (a.dump && row < a.M && nt < a.n_tiles && col < a.N && b < a.groups)
+                            a.dump[(static_cast<std::int64_t>(row) * a.N + col) * a.groups + b] = c[r];
+                        const float scale = QM == QUANT_STATIC ? sv4[ni] : kk[r];
+                        acc[mi][ni][r] = __builtin_fmaf(scale, static_cast<float>(c[r]), acc[mi][ni][r]);
+                    }
+                };
+                // Software pipeline: block blk's MFMAs, then block blk - 1's epilogue. An int8 MFMA result needs 8
+                // wait states before a VALU reads it (what the compiler inserts for the builtin) and the hazard
+                // recognizer does not look into inline assembly, so the distances are kept here: from block 1 on
+                // the previous epilogue (8 VALU) and the next block's MFMAs lie between an MFMA and its epilogue
+                // (plus 2 wait states per block with calibrated inputs, whose blocks have one MFMA); block 0's
+                // epilogue and block 15's wait on s_nop.
+                v4i cp;
+                v4f kp = zerof;
+                mfmas(0, cp, kp);
+#pragma unroll
+                for (int blk = 1; blk < 16; ++blk) {
+                    v4i cn;
+                    v4f kn = zerof;
+                    mfmas(blk, cn, kn);
+                    if (blk == 1) KQ_GASM("s_nop 7");
+                    else if (QM == QUANT_STATIC) KQ_GASM("s_nop 1");
+                    epilogue(blk - 1, cp, kp);
+                    cp = cn;
+                    kp = kn;
+                }
+                KQ_GASM("s_nop 7\n\ts_nop 7");
+                epilogue(15, cp, kp);
+            }
+        }
+        if (more) {
+            store((k + 1) & 1);  // the other stage: its last readers passed the previous barrier
+            __syncthreads();
+        }
+    }
+
+    // ---- output ----
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = m0 + wm * 64 + mi * 16 + 4 * L + r;
+            if (row >= a.M) continue;
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const int nt = nb * kSlots + 4 * wn + ni, col = nt * kTileRows + nn;
+                if (nt >= a.n_tiles || col >= a.N) continue;
+                float v = acc[mi][ni][r];
+                if (QM == QUANT_STATIC) v = v * a.input_scale;
+                a.y[static_cast<std::int64_t>(row) * a.N + col] = calibrate_output(v, a.output_scale);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool gemm_i4g_fits(const LinearCall& c) {
+    const Weight& w = *c.w;
+    if (!w.tiled || w.geo.bits != 4 || (w.geo.group != 32 && w.geo.group != 64) || c.M <= 16 || c.gelu_gate) return false;
+    if (c.path != PATH_BLOCKWISE && c.path != PATH_SYMMETRIC) return false;
+    if (w.zero_mode == ZERO_FLOAT) return false;
+    if (w.geo.cols % kBK || w.geo.cols_p != w.geo.cols) return false;
+    const std::int64_t M_p = c.act.rows_p ? c.act.rows_p : round_up(c.M, 256);
+    if (M_p % kBM || M_p * w.geo.cols >= (std::int64_t{1} << 31) || M_p * w.geo.groups_p >= (std::int64_t{1} << 31) ||
+        w.geo.n_tiles * w.geo.k_tiles * kTileBytes >= (std::int64_t{1} << 46) || c.M * w.geo.rows >= (std::int64_t{1} << 31) ||
+        (c.dump && c.M * w.geo.rows * (w.geo.cols / w.geo.group) >= (std::int64_t{1} << 62)))
+        return false;
+    return true;
+}
+
+hipError_t launch_gemm_i4g(const LinearCall& c, hipStream_t stream) {
+    const Weight& w = *c.w;
+    hipError_t e = launch_quantize(c, stream);  // codes [rows_p][K] permuted, block scales [rows_p][groups_p]
+    if (e != hipSuccess) return e;
+    GArgs a{};
+    a.q = c.act.q;
+    a.a_scale = c.act.scale;
+    a.tiles = w.tiles;
+    a.scales = w.scales;
+    a.zero_points = w.zero_mode == ZERO_POINT ? w.zero_points : nullptr;
+    a.y = c.y;
+    a.dump = c.dump;
+    a.M = static_cast<int>(c.M);
+    a.M_p = static_cast<int>(c.act.rows_p);
+    a.N = static_cast<int>(w.geo.rows);
+    a.K = static_cast<int>(w.geo.cols);
+    a.k_tiles = static_cast<int>(w.geo.k_tiles);
+    a.n_tiles = static_cast<int>(w.geo.n_tiles);
+    a.groups_p = static_cast<int>(w.geo.groups_p);
+    a.groups = static_cast<int>(w.geo.cols / w.geo.group);
+    a.input_scale = c.input_scale;
+    a.output_scale = c.output_scale;
+    a.m_blocks = static_cast<int>((c.M + kBM - 1) / kBM);
+    a.n_blocks = static_cast<int>((w.geo.n_tiles + kSlots - 1) / kSlots);
+    if (a.m_blocks * kBM > a.M_p) return hipErrorInvalidValue;  // the activation panel must cover every tile row
+    const dim3 grid(static_cast<unsigned>(a.m_blocks * a.n_blocks)), block(256);
+    const bool stat = c.path == PATH_SYMMETRIC, zp = w.zero_mode == ZERO_POINT, sh = w.scale_type == META_F16;
+    const bool dbg = c.dump != nullptr;
+#define KQ_GG(G, QM, Z, H, D) hipLaunchKernelGGL((gemm_i4g_kernel<G, QM, Z, H, D>), grid, block, GShape<G>::LDS, stream, a)
+#define KQ_GGD(G, QM, Z, H) \
+    if (dbg) KQ_GG(G, QM, Z, H, true); \
+    else KQ_GG(G, QM, Z, H, false)
+#define KQ_GGH(G, QM, Z) \
+    if (sh) { KQ_GGD(G, QM, Z, true); } \
+    else { KQ_GGD(G, QM, Z, false); }
+#define KQ_GGQ(G)                                      \
+    if (stat) { KQ_GGH(G, dev::QUANT_STATIC, false) } \
+    else if (zp) { KQ_GGH(G, dev::QUANT_DYN_SYM, true) } \
+    else { KQ_GGH(G, dev::QUANT_DYN_SYM, false) }
+    if (w.geo.group == 32) { KQ_GGQ(32) }
+    else { KQ_GGQ(64) }
+#undef KQ_GGQ
+#undef KQ_GGH
+#undef KQ_GGD
+#undef KQ_GG
+    return hipGetLastError();
+}
+
+}  // namespace kq

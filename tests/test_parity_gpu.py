@@ -103,6 +103,13 @@ CASES = [
     (4, 128, 64, 4096, 256, "zp", 0.0, True, 0.0),
     (4, 128, 300, 8192, 256, None, 0.0, False, 0.001),
     (4, 128, 40, 8192, 144, None, 0.05, False, 0.0),
+    # 4-bit g = 32 / 64 prefill GEMM (two-stage LDS int8 MFMA kernel): fused-QKV-like K, ragged M and N, zero points,
+    # calibrated inputs, a single k step
+    (4, 32, 300, 2048, 640, None, 0.0, True, 0.001),
+    (4, 32, 64, 1024, 272, "zp", 0.0, True, 0.0),
+    (4, 64, 140, 1536, 400, "zp", 0.0, False, 0.001),
+    (4, 64, 33, 512, 128, None, 0.05, False, 0.0),
+    (4, 32, 129, 128, 256, None, 0.0, False, 0.0),
     # group sizes the tiles cannot carry (row-major integer path)
     (4, 96, 3, 384, 256, "zp", 0.0, False, 0.0),
     (8, 48, 2, 288, 96, None, 0.0, False, 0.0),
@@ -372,3 +379,20 @@ def test_baseline_prefill_rows(dev, ref):
     rows = np.sort(rng.choice(M, size=16, replace=False))
     y_ref, _ = ref.packed_linear(x[rows], values, scales, 4, 128, zero_points=zp, threads=8)
     check_close(y[rows], y_ref)
+
+
+def test_fused_qkv_prefill_rows(dev, ref):
+    """configs[3] fused QKV at prefill size (M = 2048, K = 2048, N = 2048 + 256 + 256, 4-bit g = 32): sampled rows
+    against the oracle (the g = 32 prefill GEMM)."""
+    M, K, N, g = 2048, 2048, 2560, 32
+    rng = np.random.default_rng(33)
+    values, scales, _, _ = weights(rng, N, K, 4, g)
+    x = activations(rng, M, K, 0.001)
+    dw = device_weight(values, scales, 4, g, dev)
+    y = dw.linear(to_dev(x, dev).to(torch.bfloat16))
+    torch.cuda.synchronize()
+    rows = np.array([0, 1, 127, 128, 1000, M - 1])
+    xb = ref.f32_to_bf16_bits(x[rows])
+    y_ref, path = ref.packed_linear(xb, values, scales, 4, g, x_bf16=True, threads=8)
+    assert path == ref.PATH_BLOCKWISE
+    check_close(y[torch.from_numpy(rows).to(dev)], y_ref)
