@@ -628,11 +628,12 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
     KQ_READ_A(3, 0);
 
     float sv[4], asel[4];  // weight and activation scales of the current step
-    // Block b: two int8 MFMAs give the exact partials P' of the step's group; a 4x4x1 f32 MFMA (16 outer products
-    // of 4 rows x 4 columns) gives k = a_s * s in the same lane layout (lane = column nn + 16 L, register r = row
-    // 4 L + r). The epilogue of block b (acc += k * P', two VALU per element) is issued after the MFMAs of block
-    // b + 1.
-    auto mfmas = [&](int blk, v4i& c, v4f& k) {
+    // Block b: two int8 MFMAs give the exact partials P' of the step's group. The epilogue of block b, issued after
+    // the MFMAs of block b + 1, forms k = a_s * s in the accumulator's lane layout (lane = column nn + 16 L,
+    // register r = row 4 L + r): the lane quad 4 (lane / 4) .. + 3 holds a_s of rows 16 mi + 4 L + 0..3 (one per
+    // lane), so v_mul_f32 with a DPP quad broadcast of lane r gives k[r] in one VALU instruction (an f32 4x4x1 MFMA
+    // for the same products costs more issue time, measured); then acc += k * P' (cvt, fmac).
+    auto mfmas = [&](int blk, v4i& c) {
         const int mi = blk >> 2, ni = blk & 3;
         // reads return in order: after B0 come B1, B2, B3 and A3 (8 reads)
         if (blk == 0) {
@@ -652,29 +653,34 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
             // issue order pinned (see the epilogue)
             KQ_ASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=&v"(c) : "v"(A[mi][0]), "v"(B[ni][0]));
             KQ_ASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(c) : "v"(A[mi][1]), "v"(B[ni][1]));
-            if constexpr (QM != QUANT_STATIC) KQ_ASM("v_mfma_f32_4x4x1_16b_f32 %0, %1, %2, 0" : "=&v"(k) : "v"(asel[mi]), "v"(sv[ni]));
             return;
         }
 #endif
         c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi][0], B[ni][0], zero, 0, 0, 0);
         c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi][1], B[ni][1], c, 0, 0, 0);
-        if constexpr (QM != QUANT_STATIC) k = __builtin_amdgcn_mfma_f32_4x4x1f32(asel[mi], sv[ni], zerof, 0, 0, 0);
     };
-    auto epilogue = [&](const v4i& c, const v4f& k, int blk, int kt) {
+    auto epilogue = [&](const v4i& c, int blk, int kt) {
         const int mi = blk >> 2, ni = blk & 3;
 #if defined(__HIP_DEVICE_COMPILE__)
         if constexpr (!DBG) {
-            // Inline assembly keeps this block's conversions and FMAs after the MFMAs of the next block (the
+            // Inline assembly keeps this block's products, conversions and FMAs after the MFMAs of the next block (the
             // compiler would pull them up behind their own MFMAs and stall on the results); by then at least ten
             // instructions separate every MFMA result from its first VALU read, beyond the dependency window.
-            float t[4];
+            // (asel is last written at the step's first block, long before these DPP reads.)
+            float kk[4], t[4];
+            if constexpr (QM == QUANT_STATIC) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) kk[r] = sv[ni];
+            } else {
+                KQ_ASM("v_mul_f32_dpp %0, %1, %2 quad_perm:[0,0,0,0] row_mask:0xf bank_mask:0xf" : "=v"(kk[0]) : "v"(asel[mi]), "v"(sv[ni]));
+                KQ_ASM("v_mul_f32_dpp %0, %1, %2 quad_perm:[1,1,1,1] row_mask:0xf bank_mask:0xf" : "=v"(kk[1]) : "v"(asel[mi]), "v"(sv[ni]));
+                KQ_ASM("v_mul_f32_dpp %0, %1, %2 quad_perm:[2,2,2,2] row_mask:0xf bank_mask:0xf" : "=v"(kk[2]) : "v"(asel[mi]), "v"(sv[ni]));
+                KQ_ASM("v_mul_f32_dpp %0, %1, %2 quad_perm:[3,3,3,3] row_mask:0xf bank_mask:0xf" : "=v"(kk[3]) : "v"(asel[mi]), "v"(sv[ni]));
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) KQ_ASM("v_cvt_f32_i32 %0, %1" : "=v"(t[r]) : "v"(c[r]));
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float kk = QM == QUANT_STATIC ? sv[ni] : k[r];
-                KQ_ASM("v_fmac_f32 %0, %1, %2" : "+v"(acc[mi][ni][r]) : "v"(kk), "v"(t[r]));
-            }
+            for (int r = 0; r < 4; ++r) KQ_ASM("v_fmac_f32 %0, %1, %2" : "+v"(acc[mi][ni][r]) : "v"(kk[r]), "v"(t[r]));
             return;
         }
 #endif
@@ -686,41 +692,48 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
                 if (row < a.M && col_nt[ni] < a.n_tiles && col < a.N)
                     a.dump[(static_cast<std::int64_t>(row) * a.N + col) * a.groups + kt] = P;
             }
-            const float kk = QM == QUANT_STATIC ? sv[ni] : k[r];
+            float kk = sv[ni];
+            if constexpr (QM != QUANT_STATIC) {
+                // a_s of row 16 mi + 4 L + r: quad lane r's value (quad_perm [r, r, r, r])
+                const int ctrl = 0x55 * r;
+                const int bits = __float_as_int(asel[mi]);
+                const int rs = ctrl == 0 ? __builtin_amdgcn_mov_dpp(bits, 0x00, 0xF, 0xF, false)
+                               : ctrl == 0x55 ? __builtin_amdgcn_mov_dpp(bits, 0x55, 0xF, 0xF, false)
+                               : ctrl == 0xAA ? __builtin_amdgcn_mov_dpp(bits, 0xAA, 0xF, 0xF, false)
+                                              : __builtin_amdgcn_mov_dpp(bits, 0xFF, 0xF, 0xF, false);
+                kk = __int_as_float(rs) * sv[ni];
+            }
             acc[mi][ni][r] = __builtin_fmaf(kk, static_cast<float>(P), acc[mi][ni][r]);
         }
     };
     auto sched_blocks = [&]() {
         if constexpr (!DBG) {
-            // one block: 3 MFMAs (2 with static activations), then the 8 VALU of the previous block's epilogue
+            // one block: 2 MFMAs, then the 12 VALU of the previous block's epilogue (8 with static activations)
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
-                __builtin_amdgcn_sched_group_barrier(0x008, QM == QUANT_STATIC ? 2 : 3, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, QM == QUANT_STATIC ? 8 : 12, 0);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
     v4i cp;  // MFMA results of the block whose epilogue is pending
-    v4f kp = zerof;
     // First half of step kt (slot s1 = step kt + 1): blocks 0-7, step kt + 1's tiles unpacked into B slot
     // (kt + 1) % 2, then the step's barrier.
     auto phase1 = [&](int kt, int s1) {
         v4i cn;
-        v4f kn4 = zerof;
         Raw raw;
-        mfmas(0, cp, kp);
+        mfmas(0, cp);
 #pragma unroll
         for (int blk = 1; blk < 8; ++blk) {
-            mfmas(blk, cn, kn4);
+            mfmas(blk, cn);
             if (blk == 4) raw = unpack_read(s1, s1);
             if (blk == 6) unpack_write(raw, (kt - kofs + 1) & 1);
             // block 0's partials: only block 1's MFMAs lie between them and their first VALU read, fewer than the
             // 8 wait states an int8 MFMA result needs (the hazard recognizer does not see into inline assembly)
             if (blk == 1 && !DBG) KQ_ASM("s_nop 7");
-            epilogue(cp, kp, blk - 1, kt);
+            epilogue(cp, blk - 1, kt);
             cp = cn;
-            kp = kn4;
         }
         sched_blocks();
         // all LDS traffic of the loop is explicit: the wait covers it, so a bare barrier (no fence) suffices
@@ -736,7 +749,6 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
         const std::uint32_t aslot1 = s1 * S::A_BYTES, mslot1 = s1 * S::META_BYTES;
         const std::uint32_t bslot1 = ((kt - kofs + 1) & 1) * kBBytes;
         v4i cn;
-        v4f kn4 = zerof;
         if (next) {
             read_meta(mslot1);
             KQ_READ_A(0, aslot1);
@@ -744,7 +756,7 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
         }
 #pragma unroll
         for (int blk = 8; blk <= 16; ++blk) {
-            if (blk < 16) mfmas(blk, cn, kn4);
+            if (blk < 16) mfmas(blk, cn);
             if (blk <= 11) issue_a(k3, s0, blk - 8);
             if (blk == 12) {
                 issue_raw(k4, s1);
@@ -760,11 +772,8 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
                 KQ_READ_B(3, bslot1);
                 KQ_READ_A(3, aslot1);
             }
-            epilogue(cp, kp, blk - 1, kt);
-            if (blk < 16) {
-                cp = cn;
-                kp = kn4;
-            }
+            epilogue(cp, blk - 1, kt);
+            if (blk < 16) cp = cn;
         }
         sched_blocks();
     };

@@ -8,11 +8,11 @@
 // global -> registers (issued before the step's MFMAs) -> LDS (after them): activation codes XOR-swizzled by row so
 // the A-operand reads spread over the banks, packed int4 tiles unpacked to int8 with the zero point of each byte's
 // group folded in (byte = u - zp), weight scales as f32 [group][wave column][row][tile], activation scales
-// [group][128] with the four rows a lane scales adjacent. Per 16 x 16 block and group: one int8 MFMA gives the exact
-// partial P' = sum q (u - zp) of the group (v_mfma_i32_16x16x32_i8 on the 8 bytes of a lane that belong to a
-// 32-column group, v_mfma_i32_16x16x64_i8 for g = 64), one v_mfma_f32_4x4x1 gives a_s * s in the accumulator's
-// lane layout, and acc += (a_s * s) * P' is the epilogue. The epilogue runs once per group, so small groups make
-// this kernel VALU-bound: two VALU per output element and group against one int8 MAC pass of 32 or 64 columns.
+// [group][128 rows]. Per 16 x 16 block and group: one int8 MFMA gives the exact partial P' = sum q (u - zp) of the
+// group (v_mfma_i32_16x16x32_i8 on the 8 bytes of a lane that belong to a 32-column group, v_mfma_i32_16x16x64_i8
+// for g = 64), and the epilogue is k = a_s * s (v_mul), acc += k * P' (cvt, fmac). The epilogue runs once per
+// group, so small groups make this kernel VALU-bound: three VALU per output element and group against one int8
+// MFMA over 32 or 64 columns.
 // Two workgroups fit a CU (72 KB of LDS at g = 32), so a 2048 x 2560 projection (320 tiles) runs in one wave of
 // workgroups.
 #include <hip/hip_fp16.h>
@@ -45,7 +45,7 @@ struct GShape {
     static constexpr int A_BYTES = kBM * kBK;            // codes [row][128], 16-byte chunks swizzled
     static constexpr int B_BYTES = kSlots * 2048;        // unpacked int8 [slot][64-column half][lane][16 B]
     static constexpr int WS_BYTES = GPS * 2 * 16 * 4 * 4;  // f32 [group][wave column][row nn][tile ni]
-    static constexpr int AS_BYTES = GPS * kBM * 4;       // f32 [group][row position]
+    static constexpr int AS_BYTES = GPS * kBM * 4;       // f32 [group][row]
     static constexpr int B_OFF = A_BYTES, WS_OFF = B_OFF + B_BYTES, AS_OFF = WS_OFF + WS_BYTES;
     static constexpr int STAGE = AS_OFF + AS_BYTES;
     static constexpr int LDS = 2 * STAGE;
@@ -65,10 +65,6 @@ struct GArgs {
     float input_scale, output_scale;
     int m_blocks, n_blocks;
 };
-
-// position of row r (0..127) in the activation-scale stage: rows 16 q + t of a 64-row half at 4 t + q, so a lane's
-// four rows 16 mi + t (mi = 0..3) are one 16-byte read
-__device__ __forceinline__ int as_pos(int r) { return (r & 64) | ((r & 15) << 2) | ((r >> 4) & 3); }
 
 template <int G, int QM, bool ZP, bool SH, bool DBG>
 __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
@@ -185,7 +181,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
 #pragma unroll
         for (int i = 0; i < S::META_PER_THREAD; ++i) {
             ws[((m_g[i] * 2 + (m_t[i] >> 2)) * 16 + (m_r[i] & 15)) * 4 + (m_t[i] & 3)] = pws[i];
-            as[m_g[i] * kBM + as_pos(m_r[i])] = pas[i];
+            as[m_g[i] * kBM + m_r[i]] = pas[i];
         }
     };
 
@@ -225,13 +221,18 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
             for (int h = 0; h < HALVES; ++h) {
                 const int gi = G == 32 ? 2 * j + h : j;  // group of the step
                 const v4f sv4 = *reinterpret_cast<const v4f*>(ws + ((gi * 2 + wn) * 16 + nn) * 4);
-                v4f as4 = zerof;
-                if constexpr (QM != QUANT_STATIC) as4 = *reinterpret_cast<const v4f*>(as + gi * kBM + wm * 64 + 4 * (4 * L + (lane & 3)));
-                // block blk = 4 mi + ni: the exact group partial and (dynamic) a_s * s in the accumulator layout.
-                // The MFMAs and the epilogue are volatile assembly so their issue order stays as written (the
-                // compiler would hoist every MFMA of the step above the first epilogue and spill the results);
-                // the debug variant, which stores partials, uses the builtins.
-                auto mfmas = [&](int blk, v4i& c, v4f& kk) {
+                v4f as4[4];  // activation scales of rows 16 mi + 4 L + r, r = 0..3 (the accumulator's rows)
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi) {
+                    as4[mi] = zerof;
+                    if constexpr (QM != QUANT_STATIC) as4[mi] = *reinterpret_cast<const v4f*>(as + gi * kBM + wm * 64 + 16 * mi + 4 * L);
+                }
+                // block blk = 4 mi + ni: one int8 MFMA gives the exact group partial; the epilogue forms a_s * s on
+                // the VALU (four v_mul_f32: an f32 4x4x1 MFMA for the same products costs more issue time than the
+                // multiplies), converts the partial and accumulates. MFMAs and epilogue are volatile assembly so
+                // their issue order stays as written (the compiler would hoist every MFMA of the step above the first
+                // epilogue and spill the results); the debug variant, which stores partials, uses the builtins.
+                auto mfmas = [&](int blk, v4i& c) {
                     const int mi = blk >> 2, ni = blk & 3;
                     const long av = (static_cast<long>(static_cast<std::uint32_t>(A[mi][2 * h + 1])) << 32) |
                                     static_cast<std::uint32_t>(A[mi][2 * h]);
@@ -240,25 +241,24 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
                     if constexpr (!DBG) {
                         if constexpr (G == 32) KQ_GASM("v_mfma_i32_16x16x32_i8 %0, %1, %2, 0" : "=&v"(c) : "v"(av), "v"(bv));
                         else KQ_GASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=&v"(c) : "v"(A[mi]), "v"(B[ni]));
-                        if constexpr (QM != QUANT_STATIC)
-                            KQ_GASM("v_mfma_f32_4x4x1_16b_f32 %0, %1, %2, 0" : "=&v"(kk) : "v"(as4[mi]), "v"(sv4[ni]));
                         return;
                     }
                     if constexpr (G == 32) c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, zero, 0, 0, 0);
                     else c = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mi], B[ni], zero, 0, 0, 0);
-                    if constexpr (QM != QUANT_STATIC) kk = __builtin_amdgcn_mfma_f32_4x4x1f32(as4[mi], sv4[ni], zerof, 0, 0, 0);
                 };
-                auto epilogue = [&](int blk, const v4i& c, const v4f& kk) {
+                auto epilogue = [&](int blk, const v4i& c) {
                     const int mi = blk >> 2, ni = blk & 3;
                     if constexpr (!DBG) {
-                        float t[4];
+                        float kk[4], t[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if constexpr (QM == QUANT_STATIC) kk[r] = sv4[ni];
+                            else KQ_GASM("v_mul_f32 %0, %1, %2" : "=v"(kk[r]) : "v"(as4[mi][r]), "v"(sv4[ni]));
+                        }
 #pragma unroll
                         for (int r = 0; r < 4; ++r) KQ_GASM("v_cvt_f32_i32 %0, %1" : "=v"(t[r]) : "v"(c[r]));
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const float scale = QM == QUANT_STATIC ? sv4[ni] : kk[r];
-                            KQ_GASM("v_fmac_f32 %0, %1, %2" : "+v"(acc[mi][ni][r]) : "v"(scale), "v"(t[r]));
-                        }
+                        for (int r = 0; r < 4; ++r) KQ_GASM("v_fmac_f32 %0, %1, %2" : "+v"(acc[mi][ni][r]) : "v"(kk[r]), "v"(t[r]));
                         return;
                     }
 #pragma unroll
@@ -268,32 +268,28 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
                         const int b = k * GPS + gi;
                         if (a.dump && row < a.M && nt < a.n_tiles && col < a.N && b < a.groups)
                             a.dump[(static_cast<std::int64_t>(row) * a.N + col) * a.groups + b] = c[r];
-                        const float scale = QM == QUANT_STATIC ? sv4[ni] : kk[r];
+                        const float scale = QM == QUANT_STATIC ? sv4[ni] : as4[mi][r] * sv4[ni];
                         acc[mi][ni][r] = __builtin_fmaf(scale, static_cast<float>(c[r]), acc[mi][ni][r]);
                     }
                 };
-                // Software pipeline: block blk's MFMAs, then block blk - 1's epilogue. An int8 MFMA result needs 8
+                // Software pipeline: block blk's MFMA, then block blk - 1's epilogue. An int8 MFMA result needs 8
                 // wait states before a VALU reads it (what the compiler inserts for the builtin) and the hazard
                 // recognizer does not look into inline assembly, so the distances are kept here: from block 1 on
-                // the previous epilogue (8 VALU) and the next block's MFMAs lie between an MFMA and its epilogue
-                // (plus 2 wait states per block with calibrated inputs, whose blocks have one MFMA); block 0's
-                // epilogue and block 15's wait on s_nop.
+                // the previous epilogue (12 VALU, 8 when calibrated, plus 2 wait states then) and the next block's
+                // MFMA lie between an MFMA and its epilogue; block 0's epilogue and block 15's wait on s_nop.
                 v4i cp;
-                v4f kp = zerof;
-                mfmas(0, cp, kp);
+                mfmas(0, cp);
 #pragma unroll
                 for (int blk = 1; blk < 16; ++blk) {
                     v4i cn;
-                    v4f kn = zerof;
-                    mfmas(blk, cn, kn);
+                    mfmas(blk, cn);
                     if (blk == 1) KQ_GASM("s_nop 7");
                     else if (QM == QUANT_STATIC) KQ_GASM("s_nop 1");
-                    epilogue(blk - 1, cp, kp);
+                    epilogue(blk - 1, cp);
                     cp = cn;
-                    kp = kn;
                 }
                 KQ_GASM("s_nop 7\n\ts_nop 7");
-                epilogue(15, cp, kp);
+                epilogue(15, cp);
             }
         }
         if (more) {
