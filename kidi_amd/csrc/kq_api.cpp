@@ -974,6 +974,11 @@ kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_d
         if (e != hipSuccess) return hip_fail(e, "debug quantize");
         return KQ_OK;
     }
+    if (kq::gemm_i4g_fits(c)) {
+        const hipError_t e = kq::launch_gemm_i4g_quantize_dump(c, codes, scales, sums, zero_points, st);
+        if (e != hipSuccess) return hip_fail(e, "debug quantize");
+        return KQ_OK;
+    }
     hipError_t e = kq::launch_quantize(c, st);
     if (e == hipSuccess && codes) e = kq::launch_unpermute_codes(*c.w, c.act, m, codes, st);
     if (e == hipSuccess) e = kq::launch_copy_block_stats(*c.w, c.act, m, scales, sums, zero_points, st);

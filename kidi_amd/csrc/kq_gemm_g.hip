@@ -1,9 +1,9 @@
 // Prefill projection (M > 16) for 4-bit weights with small groups, g = 32 or 64 (the fused QKV of a decoder layer is
 // g = 32): Kidi's BlockwiseLinear / SymmetricPackedLinear closed forms (runtime/ynn/operators.cpp:1118-1169,
-// :1250-1308) over int8 activation codes from quantize_kernel ([M_p][K] in the tiles' permuted order, block scales
-// [M_p][K/g]).
+// :1250-1308) over int8 activation codes from quantize_rows_g_kernel ([M_p][K] in the tiles' permuted order, block
+// scales [K/g][M_p]).
 //
-// Workgroup tile 128 rows x 128 output columns (8 weight row tiles), 4 waves of 64 x 64 (16 blocks of 16 x 16), one
+// Workgroup tile 128 rows x 128 output columns (8 weight row tiles), 8 waves of 32 x 64 (8 blocks of 16 x 16), one
 // 128-column k step per iteration = 128/g groups. LDS holds two stages; each step the next step's operands travel
 // global -> registers (issued before the step's MFMAs) -> LDS (after them): activation codes XOR-swizzled by row so
 // the A-operand reads spread over the banks, packed int4 tiles unpacked to int8 with the zero point of each byte's
@@ -13,8 +13,9 @@
 // for g = 64), and the epilogue is k = a_s * s (v_mul), acc += k * P' (cvt, fmac). The epilogue runs once per
 // group, so small groups make this kernel VALU-bound: three VALU per output element and group against one int8
 // MFMA over 32 or 64 columns.
-// Two workgroups fit a CU (72 KB of LDS at g = 32), so a 2048 x 2560 projection (320 tiles) runs in one wave of
-// workgroups.
+// Two workgroups fit a CU (72 KB of LDS at g = 32, at most 128 VGPRs), so a 2048 x 2560 projection (320 tiles) runs
+// in one wave of workgroups, and every SIMD holds at least two waves (one wave issues a VALU at most every other
+// slot).
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -38,6 +39,8 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 #endif
 
 constexpr int kBM = 128, kBK = 128, kSlots = 8;  // rows, columns per step, row tiles per workgroup
+constexpr int kWaves = 8;  // two per SIMD in every workgroup: a lone workgroup on a CU still issues VALU at the
+                           // two-wave rate (one wave issues a VALU at most every other slot)
 
 template <int G>
 struct GShape {
@@ -49,13 +52,20 @@ struct GShape {
     static constexpr int B_OFF = A_BYTES, WS_OFF = B_OFF + B_BYTES, AS_OFF = WS_OFF + WS_BYTES;
     static constexpr int STAGE = AS_OFF + AS_BYTES;
     static constexpr int LDS = 2 * STAGE;
-    static constexpr int META_PER_THREAD = GPS * kBM / 256;  // weight scales (and activation scales) per thread
     static_assert(LDS <= 80 * 1024, "two workgroups per CU");
+};
+
+// Waves of a workgroup: 2 columns of 64 output columns x WAVES/2 rows of WR output rows (MI blocks of 16 rows).
+template <int WAVES>
+struct GWaves {
+    static constexpr int THREADS = 64 * WAVES, WR = kBM / (WAVES / 2), MI = WR / 16;
+    static constexpr int A_PER = kBM * kBK / 16 / THREADS;  // 16-byte activation chunks per thread
+    static constexpr int B_PER = kSlots * 64 / THREADS;     // 16-byte packed-tile lane slots per thread
 };
 
 struct GArgs {
     const std::int8_t* q;      // [M_p][K] permuted codes
-    const float* a_scale;      // [M_p][groups_p]
+    const float* a_scale;      // [groups_p][M_p] (rows contiguous: a step's 128 rows are one coalesced read)
     const std::uint8_t* tiles;
     const void* scales;        // [n_tiles][groups_p][16] F16|F32
     const std::uint8_t* zero_points;  // [n_tiles][groups_p][8] nibble pairs, or null (symmetric: 8)
@@ -66,14 +76,16 @@ struct GArgs {
     int m_blocks, n_blocks;
 };
 
-template <int G, int QM, bool ZP, bool SH, bool DBG>
-__global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
+template <int G, int QM, bool ZP, bool SH, bool DBG, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, WAVES / 2) void gemm_i4g_kernel(GArgs a) {
     using S = GShape<G>;
-    constexpr int GPS = S::GPS;
+    using WV = GWaves<WAVES>;
+    constexpr int GPS = S::GPS, T = WV::THREADS, MI = WV::MI;
+    constexpr int META_PER_THREAD = (GPS * kBM + T - 1) / T;  // weight scales (and activation scales) per thread
     extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wm = wave % (WAVES / 2), wn = wave / (WAVES / 2);
     const int nn = lane & 15, L = lane >> 4;
 
     // workgroup -> tile; each XCD (every 8th workgroup) takes a contiguous range of tiles, column-block major, so its
@@ -85,47 +97,49 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
     const int m0 = mb * kBM;
 
     // ---- per-thread copy assignments (fixed for the whole K loop) ----
-    // activation codes: chunks c = tid + 256 i of 16 bytes, row c / 8, chunk c % 8
-    const std::int8_t* a_src[4];
-    int a_dst[4];
+    // activation codes: chunks c = tid + T i of 16 bytes, row c / 8, chunk c % 8
+    const std::int8_t* a_src[WV::A_PER];
+    int a_dst[WV::A_PER];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int c = tid + 256 * i, r = c >> 3, ch = c & 7;
+    for (int i = 0; i < WV::A_PER; ++i) {
+        const int c = tid + T * i, r = c >> 3, ch = c & 7;
         a_src[i] = a.q + static_cast<std::int64_t>(m0 + r) * a.K + ch * 16;
         a_dst[i] = r * kBK + ((ch ^ (r & 7)) << 4);
     }
-    // packed tiles: lane slots c = tid + 256 i of the 8 tiles: tile slot c / 64, lane slot s = c % 64 (row s % 16)
-    const std::uint8_t* b_src[2];
-    int b_nt[2], b_dst[2], b_row[2];
+    // packed tiles: lane slots c = tid + T i of the 8 tiles: tile slot c / 64, lane slot s = c % 64 (row s % 16)
+    const std::uint8_t* b_src[WV::B_PER];
+    int b_nt[WV::B_PER], b_dst[WV::B_PER], b_row[WV::B_PER];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = tid + 256 * i, t = c >> 6, s = c & 63;
+    for (int i = 0; i < WV::B_PER; ++i) {
+        const int c = tid + T * i, t = c >> 6, s = c & 63;
         const int nt = nb * kSlots + t;
         b_nt[i] = nt < a.n_tiles ? nt : -1;
         b_src[i] = a.tiles + static_cast<std::int64_t>(nt < a.n_tiles ? nt : 0) * a.k_tiles * kTileBytes + s * 16;
         b_dst[i] = S::B_OFF + t * 2048 + s * 16;
         b_row[i] = s & 15;
     }
-    // metadata: values v = tid + 256 i: group v / 128, then (weight scales) tile slot (v / 16) % 8 and row v % 16,
-    // or (activation scales) row v % 128
-    int m_g[S::META_PER_THREAD], m_t[S::META_PER_THREAD], m_r[S::META_PER_THREAD];
+    // metadata: values v = tid + T i < 128 GPS: group v / 128, then (weight scales) tile slot (v / 16) % 8 and row
+    // v % 16, or (activation scales) row v % 128
+    int m_g[META_PER_THREAD], m_t[META_PER_THREAD], m_r[META_PER_THREAD];
+    bool m_live[META_PER_THREAD];
 #pragma unroll
-    for (int i = 0; i < S::META_PER_THREAD; ++i) {
-        const int v = tid + 256 * i;
-        m_g[i] = v >> 7;
+    for (int i = 0; i < META_PER_THREAD; ++i) {
+        const int v = tid + T * i;
+        m_live[i] = v < GPS * kBM;
+        m_g[i] = m_live[i] ? v >> 7 : 0;
         m_t[i] = (v >> 4) & 7;
         m_r[i] = v & 127;
     }
 
     // the next step's operands, held in registers while the current step computes
-    v4u pa[4], pb[2];
-    std::uint32_t pz[2][GPS];
-    float pws[S::META_PER_THREAD], pas[S::META_PER_THREAD];
+    v4u pa[WV::A_PER], pb[WV::B_PER];
+    std::uint32_t pz[WV::B_PER][GPS];
+    float pws[META_PER_THREAD], pas[META_PER_THREAD];
     auto load = [&](int k) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pa[i] = *reinterpret_cast<const v4u*>(a_src[i] + k * kBK);
+        for (int i = 0; i < WV::A_PER; ++i) pa[i] = *reinterpret_cast<const v4u*>(a_src[i] + k * kBK);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < WV::B_PER; ++i) {
             pb[i] = b_nt[i] >= 0 ? __builtin_nontemporal_load(reinterpret_cast<const v4u*>(b_src[i] + static_cast<std::int64_t>(k) * kTileBytes))
                                  : v4u{0u, 0u, 0u, 0u};
 #pragma unroll
@@ -136,23 +150,23 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
             }
         }
 #pragma unroll
-        for (int i = 0; i < S::META_PER_THREAD; ++i) {
+        for (int i = 0; i < META_PER_THREAD; ++i) {
             const int nt = nb * kSlots + m_t[i];
             float s = 0.F;
-            if (nt < a.n_tiles) {
+            if (m_live[i] && nt < a.n_tiles) {
                 const std::int64_t mi = (static_cast<std::int64_t>(nt) * a.groups_p + k * GPS + m_g[i]) * kTileRows + (m_r[i] & 15);
                 s = SH ? __half2float(static_cast<const __half*>(a.scales)[mi]) : static_cast<const float*>(a.scales)[mi];
             }
             pws[i] = s;
-            pas[i] = QM == QUANT_STATIC ? 0.F : a.a_scale[static_cast<std::int64_t>(m0 + m_r[i]) * a.groups_p + k * GPS + m_g[i]];
+            pas[i] = (QM == QUANT_STATIC || !m_live[i]) ? 0.F : a.a_scale[static_cast<std::int64_t>(k * GPS + m_g[i]) * a.M_p + m0 + m_r[i]];
         }
     };
     auto store = [&](int stage) {
         std::uint8_t* st = lds + stage * S::STAGE;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<v4u*>(st + a_dst[i]) = pa[i];
+        for (int i = 0; i < WV::A_PER; ++i) *reinterpret_cast<v4u*>(st + a_dst[i]) = pa[i];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < WV::B_PER; ++i) {
             // 64-column half j: dwords 2j, 2j + 1 hold its 16 codes (low nibbles, then high nibbles); bytes 0-7 of
             // the unpacked half are its first 32 columns, bytes 8-15 the second
             const std::uint32_t w[4] = {pb[i].x, pb[i].y, pb[i].z, pb[i].w};
@@ -179,15 +193,16 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
         float* ws = reinterpret_cast<float*>(st + S::WS_OFF);
         float* as = reinterpret_cast<float*>(st + S::AS_OFF);
 #pragma unroll
-        for (int i = 0; i < S::META_PER_THREAD; ++i) {
+        for (int i = 0; i < META_PER_THREAD; ++i) {
+            if (!m_live[i]) continue;
             ws[((m_g[i] * 2 + (m_t[i] >> 2)) * 16 + (m_r[i] & 15)) * 4 + (m_t[i] & 3)] = pws[i];
             as[m_g[i] * kBM + m_r[i]] = pas[i];
         }
     };
 
-    float acc[4][4][4];
+    float acc[MI][4][4];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
@@ -207,10 +222,10 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
         const float* as = reinterpret_cast<const float*>(st + S::AS_OFF);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            v4i A[4], B[4];
+            v4i A[MI], B[4];
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
-                const int row = wm * 64 + mi * 16 + nn;
+            for (int mi = 0; mi < MI; ++mi) {
+                const int row = wm * WV::WR + mi * 16 + nn;
                 A[mi] = *reinterpret_cast<const v4i*>(st + row * kBK + (((4 * j + L) ^ (row & 7)) << 4));
             }
 #pragma unroll
@@ -221,11 +236,11 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
             for (int h = 0; h < HALVES; ++h) {
                 const int gi = G == 32 ? 2 * j + h : j;  // group of the step
                 const v4f sv4 = *reinterpret_cast<const v4f*>(ws + ((gi * 2 + wn) * 16 + nn) * 4);
-                v4f as4[4];  // activation scales of rows 16 mi + 4 L + r, r = 0..3 (the accumulator's rows)
+                v4f as4[MI];  // activation scales of rows 16 mi + 4 L + r, r = 0..3 (the accumulator's rows)
 #pragma unroll
-                for (int mi = 0; mi < 4; ++mi) {
+                for (int mi = 0; mi < MI; ++mi) {
                     as4[mi] = zerof;
-                    if constexpr (QM != QUANT_STATIC) as4[mi] = *reinterpret_cast<const v4f*>(as + gi * kBM + wm * 64 + 16 * mi + 4 * L);
+                    if constexpr (QM != QUANT_STATIC) as4[mi] = *reinterpret_cast<const v4f*>(as + gi * kBM + wm * WV::WR + 16 * mi + 4 * L);
                 }
                 // block blk = 4 mi + ni: one int8 MFMA gives the exact group partial; the epilogue forms a_s * s on
                 // the VALU (four v_mul_f32: an f32 4x4x1 MFMA for the same products costs more issue time than the
@@ -259,11 +274,13 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
                         for (int r = 0; r < 4; ++r) KQ_GASM("v_cvt_f32_i32 %0, %1" : "=v"(t[r]) : "v"(c[r]));
 #pragma unroll
                         for (int r = 0; r < 4; ++r) KQ_GASM("v_fmac_f32 %0, %1, %2" : "+v"(acc[mi][ni][r]) : "v"(kk[r]), "v"(t[r]));
+                        (void)kk;
+                        (void)t;  // (the host pass compiles the assembly out)
                         return;
                     }
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int row = m0 + wm * 64 + mi * 16 + 4 * L + r;
+                        const int row = m0 + wm * WV::WR + mi * 16 + 4 * L + r;
                         const int nt = nb * kSlots + 4 * wn + ni, col = nt * kTileRows + nn;
                         const int b = k * GPS + gi;
                         if (a.dump && row < a.M && nt < a.n_tiles && col < a.N && b < a.groups)
@@ -280,7 +297,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
                 v4i cp;
                 mfmas(0, cp);
 #pragma unroll
-                for (int blk = 1; blk < 16; ++blk) {
+                for (int blk = 1; blk < 4 * MI; ++blk) {
                     v4i cn;
                     mfmas(blk, cn);
                     if (blk == 1) KQ_GASM("s_nop 7");
@@ -289,7 +306,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
                     cp = cn;
                 }
                 KQ_GASM("s_nop 7\n\ts_nop 7");
-                epilogue(15, cp);
+                epilogue(4 * MI - 1, cp);
             }
         }
         if (more) {
@@ -300,10 +317,10 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
 
     // ---- output ----
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
+    for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int row = m0 + wm * 64 + mi * 16 + 4 * L + r;
+            const int row = m0 + wm * WV::WR + mi * 16 + 4 * L + r;
             if (row >= a.M) continue;
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni) {
@@ -317,6 +334,126 @@ __global__ __launch_bounds__(256, 2) void gemm_i4g_kernel(GArgs a) {
     }
 }
 
+// Row quantizer for the g = 32 / 64 GEMM: one lane per 32 columns of a row (a lane pair per group when g = 64, one
+// DPP step reduces it). The arithmetic is the shared quantizer's (quant_block / quant_code: Kidi's dynamic
+// symmetric form, hnsw_test.cpp:513-520, or the calibrated rint(x / input_scale)); codes go to [M_p][K] in the
+// tiles' permuted order (column 32 h + 8 L + i of a 64-column block at 16 L + 8 h + i: four 8-byte pieces per lane),
+// block scales (and, for the parity dump, code sums) to [K/g][M_p]. Rows M .. M_p - 1 get codes 0 and scale 0.
+struct QgArgs {
+    const void* x;
+    int x_f32;
+    int M, M_p, K, g;
+    float input_scale;
+    std::int8_t* q;
+    float* scale_t;
+    std::int32_t* sum_t;  // optional
+};
+
+template <int QM>
+__global__ __launch_bounds__(256) void quantize_rows_g_kernel(QgArgs a) {
+    const int units = a.K / 32;
+    const std::int64_t t = static_cast<std::int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const std::int64_t m = t / units;
+    const int j = static_cast<int>(t - m * units);
+    if (m >= a.M_p) return;  // whole lane pairs: units is even
+    const bool live = m < a.M;
+    float v[32];
+    const std::int64_t e0 = m * a.K + 32 * j;
+    if (live) {
+        if (a.x_f32) {
+            const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + e0);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 r = p[i];
+                v[4 * i] = r.x;
+                v[4 * i + 1] = r.y;
+                v[4 * i + 2] = r.z;
+                v[4 * i + 3] = r.w;
+            }
+        } else {
+            const uint4* p = reinterpret_cast<const uint4*>(static_cast<const std::uint16_t*>(a.x) + e0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint4 r = p[i];
+                const std::uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    v[8 * i + 2 * d] = __uint_as_float(w4[d] << 16);
+                    v[8 * i + 2 * d + 1] = __uint_as_float(w4[d] & 0xFFFF0000u);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i] = 0.F;
+    }
+    float mx = 0.F, mn = 0.F;
+    if constexpr (QM != QUANT_STATIC) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) quant_stat(QM, v[i], mx, mn);
+        if (a.g == 64) mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0xB1, 0xF, 0xF, true)));
+    }
+    const QuantBlock qb = quant_block(QM, mx, mn, a.input_scale, live);
+    const int blk = j >> 1, h = j & 1;
+    std::int8_t* row = a.q + m * a.K + 64 * blk + 8 * h;
+    int total = 0;
+#pragma unroll
+    for (int L = 0; L < 4; ++L) {
+        std::uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = live ? quant_code(QM, v[8 * L + i], qb, a.input_scale) : 0;
+            total += c;
+            if (i < 4) lo |= (static_cast<std::uint32_t>(c) & 0xFFu) << (8 * i);
+            else hi |= (static_cast<std::uint32_t>(c) & 0xFFu) << (8 * (i - 4));
+        }
+        *reinterpret_cast<uint2*>(row + 16 * L) = make_uint2(lo, hi);
+    }
+    if (a.g == 64) total += __builtin_amdgcn_mov_dpp(total, 0xB1, 0xF, 0xF, true);
+    if (a.g == 32 || h == 0) {
+        const std::int64_t o = static_cast<std::int64_t>(a.g == 32 ? j : j >> 1) * a.M_p + m;
+        a.scale_t[o] = qb.s;
+        if (a.sum_t) a.sum_t[o] = total;
+    }
+}
+
+// Parity dump: natural-order codes and [M][K/g] block statistics from the quantizer's outputs.
+__global__ __launch_bounds__(256) void unpermute_g_kernel(const std::int8_t* q, int M, int K, std::int8_t* codes) {
+    const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= static_cast<std::int64_t>(M) * K) return;
+    const std::int64_t m = id / K, k = id % K;
+    codes[id] = q[m * K + act_position(k)];
+}
+__global__ __launch_bounds__(256) void stats_g_kernel(const float* s_t, const std::int32_t* q_t, int M, int M_p, int groups,
+                                                      float* s, std::int32_t* q, std::int32_t* z) {
+    const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= static_cast<std::int64_t>(M) * groups) return;
+    const std::int64_t m = id / groups, b = id % groups;
+    if (s) s[id] = s_t[b * M_p + m];
+    if (q) q[id] = q_t[b * M_p + m];
+    if (z) z[id] = 0;
+}
+
+hipError_t launch_quantize_g(const LinearCall& c, std::int32_t* sums, hipStream_t stream) {
+    const Weight& w = *c.w;
+    QgArgs q{};
+    q.x = c.x;
+    q.x_f32 = c.x_type == ACT_F32;
+    q.M = static_cast<int>(c.M);
+    q.M_p = static_cast<int>(c.act.rows_p);
+    q.K = static_cast<int>(w.geo.cols);
+    q.g = w.geo.group;
+    q.input_scale = c.input_scale;
+    q.q = c.act.q;
+    q.scale_t = c.act.scale;
+    q.sum_t = sums;
+    const std::int64_t lanes = static_cast<std::int64_t>(q.M_p) * (q.K / 32);
+    const dim3 grid(static_cast<unsigned>((lanes + 255) / 256)), block(256);
+    if (c.path == PATH_SYMMETRIC) hipLaunchKernelGGL((quantize_rows_g_kernel<QUANT_STATIC>), grid, block, 0, stream, q);
+    else hipLaunchKernelGGL((quantize_rows_g_kernel<QUANT_DYN_SYM>), grid, block, 0, stream, q);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 bool gemm_i4g_fits(const LinearCall& c) {
@@ -325,6 +462,7 @@ bool gemm_i4g_fits(const LinearCall& c) {
     if (c.path != PATH_BLOCKWISE && c.path != PATH_SYMMETRIC) return false;
     if (w.zero_mode == ZERO_FLOAT) return false;
     if (w.geo.cols % kBK || w.geo.cols_p != w.geo.cols) return false;
+    if (reinterpret_cast<std::uintptr_t>(c.x) & 15u) return false;  // the row quantizer's 16-byte loads
     const std::int64_t M_p = c.act.rows_p ? c.act.rows_p : round_up(c.M, 256);
     if (M_p % kBM || M_p * w.geo.cols >= (std::int64_t{1} << 31) || M_p * w.geo.groups_p >= (std::int64_t{1} << 31) ||
         w.geo.n_tiles * w.geo.k_tiles * kTileBytes >= (std::int64_t{1} << 46) || c.M * w.geo.rows >= (std::int64_t{1} << 31) ||
@@ -335,7 +473,7 @@ bool gemm_i4g_fits(const LinearCall& c) {
 
 hipError_t launch_gemm_i4g(const LinearCall& c, hipStream_t stream) {
     const Weight& w = *c.w;
-    hipError_t e = launch_quantize(c, stream);  // codes [rows_p][K] permuted, block scales [rows_p][groups_p]
+    hipError_t e = launch_quantize_g(c, nullptr, stream);  // codes [rows_p][K] permuted, block scales [groups][rows_p]
     if (e != hipSuccess) return e;
     GArgs a{};
     a.q = c.act.q;
@@ -358,10 +496,10 @@ hipError_t launch_gemm_i4g(const LinearCall& c, hipStream_t stream) {
     a.m_blocks = static_cast<int>((c.M + kBM - 1) / kBM);
     a.n_blocks = static_cast<int>((w.geo.n_tiles + kSlots - 1) / kSlots);
     if (a.m_blocks * kBM > a.M_p) return hipErrorInvalidValue;  // the activation panel must cover every tile row
-    const dim3 grid(static_cast<unsigned>(a.m_blocks * a.n_blocks)), block(256);
+    const dim3 grid(static_cast<unsigned>(a.m_blocks * a.n_blocks)), block(64 * kWaves);
     const bool stat = c.path == PATH_SYMMETRIC, zp = w.zero_mode == ZERO_POINT, sh = w.scale_type == META_F16;
     const bool dbg = c.dump != nullptr;
-#define KQ_GG(G, QM, Z, H, D) hipLaunchKernelGGL((gemm_i4g_kernel<G, QM, Z, H, D>), grid, block, GShape<G>::LDS, stream, a)
+#define KQ_GG(G, QM, Z, H, D) hipLaunchKernelGGL((gemm_i4g_kernel<G, QM, Z, H, D, kWaves>), grid, block, GShape<G>::LDS, stream, a)
 #define KQ_GGD(G, QM, Z, H) \
     if (dbg) KQ_GG(G, QM, Z, H, true); \
     else KQ_GG(G, QM, Z, H, false)
@@ -378,6 +516,19 @@ hipError_t launch_gemm_i4g(const LinearCall& c, hipStream_t stream) {
 #undef KQ_GGH
 #undef KQ_GGD
 #undef KQ_GG
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_i4g_quantize_dump(const LinearCall& c, std::int8_t* codes, float* scales, std::int32_t* sums,
+                                         std::int32_t* zero_points, hipStream_t stream) {
+    hipError_t e = launch_quantize_g(c, c.act.sum, stream);
+    if (e != hipSuccess) return e;
+    const int M = static_cast<int>(c.M), K = static_cast<int>(c.w->geo.cols), groups = K / c.w->geo.group;
+    const std::int64_t total = static_cast<std::int64_t>(M) * K;
+    if (codes) hipLaunchKernelGGL(unpermute_g_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, c.act.q, M, K, codes);
+    const std::int64_t st = static_cast<std::int64_t>(M) * groups;
+    hipLaunchKernelGGL(stats_g_kernel, dim3(static_cast<unsigned>((st + 255) / 256)), dim3(256), 0, stream, c.act.scale, c.act.sum, M,
+                       static_cast<int>(c.act.rows_p), groups, scales, sums, zero_points);
     return hipGetLastError();
 }
 

@@ -121,10 +121,12 @@ hipError_t launch_gemm_i4(const LinearCall& c, const ActBuffers& act, hipStream_
 hipError_t launch_gemm_i4_quantize_dump(const LinearCall& c, const ActBuffers& act, std::int8_t* codes, float* scales,
                                         std::int32_t* sums, std::int32_t* zero_points, hipStream_t stream);
 
-// Prefill projection (M > 16) for 4-bit weights with g = 32 or 64, K a multiple of 128 (kq_gemm_g.hip): the
-// generic activation quantizer (launch_quantize) into c.act, then a two-stage LDS int8 MFMA GEMM.
+// Prefill projection (M > 16) for 4-bit weights with g = 32 or 64, K a multiple of 128 (kq_gemm_g.hip): a row
+// quantizer into c.act (codes [rows_p][K] permuted, block scales [K/g][rows_p]), then a two-stage LDS int8 MFMA GEMM.
 bool gemm_i4g_fits(const LinearCall& c);
 hipError_t launch_gemm_i4g(const LinearCall& c, hipStream_t stream);
+hipError_t launch_gemm_i4g_quantize_dump(const LinearCall& c, std::int8_t* codes, float* scales, std::int32_t* sums,
+                                         std::int32_t* zero_points, hipStream_t stream);
 
 std::size_t workspace_bytes(const Weight& w, std::int64_t M);
 ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base);
