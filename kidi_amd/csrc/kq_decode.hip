@@ -55,6 +55,7 @@ struct DecodeArgs {
     int4* greedy;            // greedy selection: per row and workgroup {max, first index, non-finite seen} [M][grid]
     int x_f32, scale_half, aux_half;
     float input_scale, output_scale;
+    int single_units;  // units of one row tile: the launch uses the variants with the wide register budget (RT = 1)
     // fused RMS normalization of the input (LinearCall::norm): 0 none, 1 plain, 2 residual form then plain
     int norm;
     const float* norm_w1;
@@ -546,7 +547,8 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
 
 template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, bool GREEDY = false>
 hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds, hipStream_t stream) {
-    const bool wide = block.x > 256 || DBG;  // debug variants: one register budget for every K
+    // debug variants: one register budget for every K; single-tile units: the wide variants are the RT = 1 ones
+    const bool wide = block.x > 256 || DBG || a.single_units;
     if constexpr (!DBG && !GREEDY) {
         if (a.norm) {  // decode_fits admits the fused normalization only for the 4-wave variants
             if (wide) return hipErrorInvalidValue;
@@ -639,7 +641,13 @@ hipError_t launch_decode(const LinearCall& c, hipStream_t stream) {
     // units of one workgroup iteration: pairs of row tiles, or single row tiles for the variants with the wide
     // register budget (K > 2048, i.e. more than 4 waves, and every debug variant) without gating
     const bool dbg_any = c.dump || c.dq_codes || c.dq_scales || c.dq_sums || c.dq_zeros;
-    const bool single = (W > 4 || dbg_any) && !c.gelu_gate;
+    // Single-tile units also when pairs would leave CUs idle (fewer than 256 workgroups: e.g. a fused QKV of 2560 rows
+    // makes 80 pairs) or an 8-bit pair is heavy (a wave would stream 16 KB); measured on MI355X: fused QKV 4.41 -> 3.78
+    // us, 8-bit 8192 x 2048 6.39 -> 5.94 us, while 4-bit 8192 x 2048 and the 262,144-row head stay faster in pairs.
+    const std::int64_t nt = w.geo.n_tiles;
+    const bool prefer_single = !c.norm && !c.greedy && ((nt + 1) / 2 < 256 || (w.geo.bits == 8 && nt <= 512));
+    const bool single = (W > 4 || dbg_any || prefer_single) && !c.gelu_gate;
+    a.single_units = single && W <= 4 && !dbg_any;
     a.total_pairs = static_cast<int>(c.gelu_gate ? w.geo.n_tiles / 2 : (single ? w.geo.n_tiles : (w.geo.n_tiles + 1) / 2));
     // several units per workgroup once the grid passes ~2 workgroups per CU: the activation quantization and the
     // launch of a workgroup are then shared by more weight tiles
