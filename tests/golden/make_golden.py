@@ -6,8 +6,9 @@ oracle's outputs (activation codes, block statistics, integer partials P' and fp
 The oracle (oracle/kq_ref.cpp) follows the reference's closed forms; every fixture is also checked against a
 float64 restatement of y = sum_b a_s * (w_s * P + z_w * Q) in tests/test_golden.py, which does not go through the
 oracle's own epilogue. Inputs are generated here with numpy's PCG64 from fixed seeds; the shapes sit in the domain
-of each kernel path of the HIP library (decode M <= 4, skinny M <= 16, int8 MFMA GEMM M > 16 with g = 128, row-major
-path for g the tiles cannot carry, calibrated 2/4/8-bit, GELU gate)."""
+of each kernel path of the HIP library (decode M <= 4, skinny M <= 16, int8 MFMA GEMMs M > 16 with g = 128 and with
+g = 32 / 64, row-major path for g the tiles cannot carry, calibrated 2/4/8-bit, GELU gate); the rms_* fixtures hold
+an RMS normalization (plain, or after the residual form) and the projection of its output."""
 
 from __future__ import annotations
 
@@ -38,7 +39,39 @@ CASES = {
     "asym_g96_rowmajor": (4, 96, 2, 384, 64, "zp", 0.0, 0.0, False, 0.0, False, 20),
     "gelu_gate_g128": (4, 128, 2, 512, 128, "zp", 0.0, 0.0, False, 0.0, True, 21),
     "gelu_gate_g128_prefill": (4, 128, 33, 512, 64, "zp", 0.0, 0.0, True, 0.0, True, 22),
+    "sym_g32_prefill": (4, 32, 40, 512, 256, None, 0.0, 0.0, True, 0.001, False, 23),
+    "g64_prefill_static": (4, 64, 20, 512, 128, None, 0.05, 0.0, False, 0.0, False, 24),
 }
+
+# RMS normalization before a projection (Context::rms_norm / rms_norm_residual, ops/context.cpp:1043-1049,
+# :1103-1122): name: (M, K, N, bits, group, zero points, residual form, seed)
+RMS_CASES = {
+    "rms_residual_decode": (2, 1024, 256, 4, 128, True, True, 31),
+    "rms_plain_prefill": (40, 1024, 256, 4, 128, True, False, 32),
+}
+
+
+def make_rms(case) -> dict:
+    M, K, N, bits, group, zeros, residual, seed = case
+    rng = np.random.default_rng(seed)
+    values, scales, zp, _ = weights(rng, N, K, bits, group, zero_points=zeros)
+    x = activations(rng, M, K, 0.001)
+    r = activations(rng, M, K)
+    w_in = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    w_res = rng.uniform(-1.5, 1.5, K).astype(np.float32)
+    eps, eps_res, scale = 1e-6, 1e-5, 0.78125
+    out = dict(bits=bits, group=group, x=x, values=values, scales=scales, w_in=w_in, eps=np.float32(eps))
+    if zp is not None:
+        out["zero_points"] = zp
+    src = x
+    if residual:
+        hidden, _ = kq_ref.rms_norm(x, w_res, eps_res, residual=r, scale=scale)
+        out.update(residual=r, w_res=w_res, eps_res=np.float32(eps_res), res_scale=np.float32(scale), hidden=hidden)
+        src = hidden
+    normed, inv = kq_ref.rms_norm(src, w_in, eps)
+    y, path = kq_ref.packed_linear(normed, values, scales, bits, group, zero_points=zp)
+    out.update(normed=normed, inv=inv, y=y, path=path)
+    return out
 
 
 def make(name: str, case) -> dict:
@@ -73,6 +106,9 @@ def make(name: str, case) -> dict:
 def main() -> None:
     for name, case in CASES.items():
         np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **make(name, case))
+        print(name)
+    for name, case in RMS_CASES.items():
+        np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **make_rms(case))
         print(name)
 
 

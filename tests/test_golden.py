@@ -14,7 +14,8 @@ import pytest
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 FIXTURES = sorted(glob.glob(os.path.join(HERE, "golden", "*.npz")))
-NAMES = [os.path.splitext(os.path.basename(f))[0] for f in FIXTURES]
+# projection fixtures (the rms_* ones hold a normalization before the projection: tests/test_rms_norm.py)
+NAMES = [n for n in (os.path.splitext(os.path.basename(f))[0] for f in FIXTURES) if not n.startswith("rms_")]
 
 
 def load(name):
@@ -37,7 +38,7 @@ def signed_codes(values, K, bits):
 
 
 def test_fixtures_present():
-    assert len(NAMES) >= 12
+    assert len(NAMES) >= 14
 
 
 @pytest.mark.parametrize("name", NAMES)

@@ -226,3 +226,62 @@ def test_gpu_linear_rms(ref, case, residual):
         y_ref = ref.gelu_gate(y_ref)
     err = float(np.max(np.abs(y.cpu().numpy() - y_ref)))
     assert err <= 2e-3 * float(np.max(np.abs(y_ref))), (name, err)
+
+
+# ---------------------------------------------------------------- golden fixtures -------------------------------------
+
+RMS_FIXTURES = ["rms_residual_decode", "rms_plain_prefill"]
+
+
+def _fixture(name):
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name + ".npz")
+    with np.load(path, allow_pickle=False) as f:
+        return {k: f[k] for k in f.files}
+
+
+@pytest.mark.parametrize("name", RMS_FIXTURES)
+def test_oracle_reproduces_rms_fixture(ref, name):
+    f = _fixture(name)
+    src = f["x"]
+    if "hidden" in f:
+        h, _ = ref.rms_norm(f["x"], f["w_res"], float(f["eps_res"]), residual=f["residual"], scale=float(f["res_scale"]))
+        np.testing.assert_array_equal(h, f["hidden"])
+        src = h
+    n, inv = ref.rms_norm(src, f["w_in"], float(f["eps"]))
+    np.testing.assert_array_equal(n, f["normed"])
+    np.testing.assert_array_equal(inv, f["inv"])
+    y, path = ref.packed_linear(n, f["values"], f["scales"], int(f["bits"]), int(f["group"]), zero_points=f.get("zero_points"))
+    assert path == int(f["path"])
+    np.testing.assert_array_equal(y, f["y"])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", RMS_FIXTURES)
+def test_gpu_rms_fixture(name):
+    """The fused projection reproduces the fixture: h and the normalized input bit-exact (kq_rms_norm), y within
+    2e-3 * max|y| (kq_packed_linear_rms)."""
+    from kidi_amd.ops import DeviceWeight, rms_norm
+
+    f = _fixture(name)
+    dev = _dev()
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    zp = f.get("zero_points")
+    dw = DeviceWeight(t(f["values"]), t(f["scales"]), int(f["bits"]), int(f["group"]), t(zp) if zp is not None else None)
+    x = t(f["x"]).to(torch.bfloat16)
+    if "hidden" in f:
+        r = t(f["residual"]).to(torch.bfloat16)
+        st = torch.tensor([float(f["res_scale"])], device=dev)
+        y, h = dw.linear_rms(x, t(f["w_in"]), float(f["eps"]), residual=r, residual_weight=t(f["w_res"]), residual_scale=st,
+                             residual_epsilon=float(f["eps_res"]))
+        np.testing.assert_array_equal(h.cpu().numpy(), f["hidden"])
+        h2 = rms_norm(x, t(f["w_res"]), float(f["eps_res"]), residual=r, output_scale=st)
+        n = rms_norm(h2, t(f["w_in"]), float(f["eps"]))
+    else:
+        y, _ = dw.linear_rms(x, t(f["w_in"]), float(f["eps"]))
+        n = rms_norm(x, t(f["w_in"]), float(f["eps"]))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(n.cpu().numpy(), f["normed"])
+    err = float(np.max(np.abs(y.cpu().numpy() - f["y"])))
+    assert err <= 2e-3 * float(np.max(np.abs(f["y"]))), err
