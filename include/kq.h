@@ -173,6 +173,17 @@ kq_status kq_greedy_token(const float* logits, int64_t rows, int64_t width, int3
 size_t kq_greedy_linear_workspace_size(const kq_weight* weight, int64_t m);
 kq_status kq_packed_linear_greedy(const kq_weight* weight, const kq_linear_args* args, int32_t* tokens, void* stream);
 
+/* Load-time weight quantization on the device: ops::pack_weight (src/kidi/ops/quantization.cpp:12-133), the step
+ * Context::prepare_linear_weights runs for float weights (src/kidi/ops/context.cpp:783-812) before they reach
+ * PACKED_LINEAR. weight: device [rows, cols] F32 | F16 | BF16. Outputs (device, Kidi layout, ready for
+ * kq_weight_pack with memory = KQ_DEVICE): values U8 [rows, cols / (8 / bits)], scales F32 [rows, cols / g] and, when
+ * asymmetric_clip and bits == 4, zeros F32 [rows, cols / g] (the additive zero (8 - zp) * scale; zeros may be NULL
+ * otherwise). Symmetric: scale = max|w| / (2^(bits-1) - 1), codes rounded half away from zero; asymmetric 4-bit: the
+ * 11-step MSE clip. Non-finite weights and a scale that underflows return KQ_INVALID_ARGUMENT. Synchronous. */
+kq_status kq_quantize_weight(const void* weight, kq_dtype dtype, int64_t rows, int64_t cols, int32_t bits,
+                             int32_t group_size, int32_t asymmetric_clip, uint8_t* values, float* scales, float* zeros,
+                             void* stream);
+
 /* RMS normalization over the last axis: RMS_NORM / RMS_NORM_RESIDUAL (Context::rms_norm and
  * Context::rms_norm_residual, src/kidi/ops/context.cpp:1043-1049, :1103-1122; the CPU RmsNorm operator,
  * runtime/ynn/operators.cpp:553-620):

@@ -12,7 +12,7 @@ import subprocess
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["csrc/kq_kernels.hip", "csrc/kq_skinny.hip", "csrc/kq_decode.hip", "csrc/kq_gemm.hip", "csrc/kq_gemm_g.hip", "csrc/kq_greedy.hip", "csrc/kq_norm.hip", "csrc/kq_api.cpp", "csrc/kq_layout_host.cpp"]
+SOURCES = ["csrc/kq_kernels.hip", "csrc/kq_skinny.hip", "csrc/kq_decode.hip", "csrc/kq_gemm.hip", "csrc/kq_gemm_g.hip", "csrc/kq_greedy.hip", "csrc/kq_norm.hip", "csrc/kq_pack.hip", "csrc/kq_api.cpp", "csrc/kq_layout_host.cpp"]
 LIB = os.path.join(HERE, "lib", "libkq_hip.so")
 
 FLAGS = [

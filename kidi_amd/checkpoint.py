@@ -232,3 +232,22 @@ def load_packed_linears(path: str | os.PathLike, config: dict | None = None, sig
             out[module] = PackedLinear(dw, b, group, in_s, out_s)
     load_packed_linears.last_cache = cache
     return out
+
+
+def prepare_runtime_packing(context, state: dict, weight_bits: int, group_size: int = 128,
+                            packed_prefill: bool = False, asymmetric_clip: bool = False) -> list[tuple[str, int, int]]:
+    """Runtime quantization of a float checkpoint (Gemma4Impl::set_checkpoint, src/kidi/model/gemma4.cpp:435-447):
+    every 2-D weight except the token embeddings is bound with ``context.prepare_linear_weights``, 4-bit groups of
+    ``group_size`` when ``weight_bits == 4`` and the width divides into them (the asymmetric clip only there), else
+    8-bit with one group per row. Returns the (name, bits, group) choices in ``state`` order."""
+    chosen = []
+    if not weight_bits:
+        return chosen
+    for name, weight in state.items():
+        if weight.dim() != 2 or name in ("embed_tokens.weight", "embed_tokens_per_layer.weight"):
+            continue
+        grouped = weight_bits == 4 and weight.shape[1] % group_size == 0
+        bits, group = (4, group_size) if grouped else (8, int(weight.shape[1]))
+        context.prepare_linear_weights(weight, bits, group, packed_prefill, grouped and asymmetric_clip)
+        chosen.append((name, bits, group))
+    return chosen

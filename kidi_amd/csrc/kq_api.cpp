@@ -97,6 +97,7 @@ std::map<int, Scratch> g_gelu_scratch;
 std::map<int, Scratch> g_ffn_scratch;
 std::map<int, Scratch> g_greedy_scratch;
 std::map<int, Scratch> g_norm_scratch;
+std::map<int, Scratch> g_pack_scratch;
 
 kq_status device_scratch(std::map<int, Scratch>& pool, std::size_t bytes, void** out) {
     int dev = 0;
@@ -934,6 +935,33 @@ kq_status kq_packed_linear_rms(const kq_weight* weight, const kq_linear_args* ar
     a.workspace = ws_lin ? base : nullptr;
     a.workspace_bytes = l.lin;
     return gelu_gate ? kq_packed_linear_gelu_gate(weight, &a, stream) : kq_packed_linear(weight, &a, stream);
+}
+
+kq_status kq_quantize_weight(const void* weight, kq_dtype dtype, int64_t rows, int64_t cols, int32_t bits,
+                             int32_t group_size, int32_t asymmetric_clip, uint8_t* values, float* scales, float* zeros,
+                             void* stream) {
+    // ops::pack_weight's checks (src/kidi/ops/quantization.cpp:15-20)
+    if ((dtype != KQ_F32 && dtype != KQ_F16 && dtype != KQ_BF16) || (bits != 2 && bits != 4 && bits != 8) ||
+        group_size <= 0 || group_size % (8 / bits) || rows <= 0 || cols <= 0 || cols % group_size)
+        return fail(KQ_INVALID_ARGUMENT, "invalid packed weight dimensions, precision or group size");
+    const bool asym = asymmetric_clip != 0 && bits == 4;
+    if (!weight || !values || !scales || (asym && !zeros)) return fail(KQ_INVALID_ARGUMENT, "null weight or output");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    void* flag = nullptr;
+    if (kq_status s = device_scratch(g_pack_scratch, 256, &flag); s != KQ_OK) return s;
+    int* error = static_cast<int*>(flag);
+    if (hipError_t e = hipMemsetAsync(error, 0, sizeof(int), st); e != hipSuccess) return hip_fail(e, "hipMemsetAsync");
+    const int dt = dtype == KQ_F32 ? 0 : (dtype == KQ_F16 ? 1 : 2);
+    if (hipError_t e = kq::launch_pack_weight(weight, dt, rows, cols, bits, group_size, asym, values, scales, zeros, error, st);
+        e != hipSuccess)
+        return hip_fail(e, "weight quantization launch");
+    int host_error = 0;
+    if (hipError_t e = hipMemcpyAsync(&host_error, error, sizeof(int), hipMemcpyDeviceToHost, st); e != hipSuccess)
+        return hip_fail(e, "hipMemcpyAsync");
+    if (hipError_t e = hipStreamSynchronize(st); e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    if (host_error & 1) return fail(KQ_INVALID_ARGUMENT, "non-finite weight cannot be quantized");
+    if (host_error & 2) return fail(KQ_INVALID_ARGUMENT, "quantization scale underflow");
+    return KQ_OK;
 }
 
 kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_dtype, int64_t m, float input_scale,

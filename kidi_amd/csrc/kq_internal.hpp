@@ -93,6 +93,11 @@ struct NormLaunch {
 };
 hipError_t launch_rms_norm(const NormLaunch& n, hipStream_t stream);
 
+// Load-time weight quantization (kq_pack.hip): float weights -> Kidi-layout codes, scales, zeros; error: 1 non-finite
+// weight, 2 symmetric scale underflow (OR-ed into *error).
+hipError_t launch_pack_weight(const void* w, int dtype, std::int64_t rows, std::int64_t width, int bits, std::int64_t group,
+                              bool asym, std::uint8_t* values, float* scales, float* zeros, int* error, hipStream_t stream);
+
 // Launch plan of the skinny (decode, M <= 16) projection with fused activation quantization (kq_skinny.hip).
 struct SkinnyPlan {
     int R = 1, W = 1, T = 4;

@@ -336,6 +336,28 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, epsilon: float, residual: to
     return y.reshape(x.shape)
 
 
+def pack_weight(weight: torch.Tensor, bits: int = 4, group_size: int = 128,
+                asymmetric_clip: bool = False) -> PackedWeight:
+    """ops::pack_weight (src/kidi/ops/quantization.cpp:12-133) on the device (kq_quantize_weight): float weights
+    [N, K] (F32, F16 or BF16, device) become Kidi-layout U8 codes, F32 scales and, for the asymmetric 4-bit clip,
+    F32 additive zeros. Synchronous; non-finite weights raise INVALID_ARGUMENT."""
+    dt = {torch.float32: N.KQ_F32, torch.float16: N.KQ_F16, torch.bfloat16: N.KQ_BF16}.get(weight.dtype, 99)
+    if (weight.dim() != 2 or dt == 99 or bits not in (2, 4, 8) or group_size <= 0
+            or group_size % (8 // bits) or not weight.shape[0] or not weight.shape[1]
+            or weight.shape[1] % group_size):
+        raise Failure("INVALID_ARGUMENT", "invalid packed weight dimensions, precision or group size")
+    w = weight.contiguous()
+    rows, cols = w.shape
+    values = torch.empty((rows, cols // (8 // bits)), dtype=torch.uint8, device=w.device)
+    scales = torch.empty((rows, cols // group_size), dtype=torch.float32, device=w.device)
+    asym = bool(asymmetric_clip) and bits == 4
+    zeros = torch.empty_like(scales) if asym else None
+    _raise(N.load().kq_quantize_weight(w.data_ptr(), dt, rows, cols, bits, group_size, int(asym),
+                                       values.data_ptr(), scales.data_ptr(),
+                                       zeros.data_ptr() if zeros is not None else None, _stream()))
+    return PackedWeight(values, scales, zeros, bits, group_size)
+
+
 def _identity(t: torch.Tensor | None):
     if t is None:
         return None
@@ -351,6 +373,47 @@ class Context:
         self.device = torch.device(device)
         self._prepared: collections.OrderedDict = collections.OrderedDict()
         self._zeros: dict = {}
+        self._bound: dict = {}  # weight storage -> (source, PackedWeight, packed_prefill, asymmetric_clip)
+        self.decode_projections = False  # Context's decode flag: bound weights take the packed path at any M
+
+    def prepare_linear_weights(self, weight: torch.Tensor, bits: int, group_size: int = 128,
+                               packed_prefill: bool = False, asymmetric_clip: bool = False) -> None:
+        """Context::prepare_linear_weights (ops/context.cpp:783-812): quantize a float weight once
+        (``pack_weight``), keep the packed copy on the device and bind it to the source weight, so ``linear``
+        on that weight runs the packed projection. Re-binding with another layout is INVALID_ARGUMENT."""
+        if (weight is None or weight.dim() != 2 or not weight.is_contiguous()
+                or weight.dtype not in (torch.float16, torch.bfloat16, torch.float32) or bits not in (2, 4, 8)
+                or group_size <= 0 or group_size % (8 // bits) or weight.shape[1] % group_size
+                or not weight.shape[0] or not weight.shape[1]):
+            raise Failure("INVALID_ARGUMENT", "invalid packed weight dimensions, precision or group size")
+        key = (weight.device.type, weight.untyped_storage().data_ptr() + weight.storage_offset() * weight.element_size())
+        found = self._bound.get(key)
+        if found is not None:
+            src, packed, prefill, asym = found
+            if (packed.bits != bits or packed.group_size != group_size or prefill != packed_prefill
+                    or asym != asymmetric_clip or tuple(src.shape) != tuple(weight.shape)):
+                raise Failure("INVALID_ARGUMENT", "weight already packed with a different layout")
+            return
+        packed = pack_weight(weight.to(self.device), bits, group_size, asymmetric_clip)
+        self._bound[key] = (weight, packed, bool(packed_prefill), bool(asymmetric_clip))
+
+    def linear(self, input: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+               transpose_weight: bool = True) -> torch.Tensor:
+        """Context::linear's packed redirect (ops/context.cpp:742-773): a weight bound by
+        ``prepare_linear_weights`` runs PACKED_LINEAR with dynamic activations when it was bound with
+        packed_prefill, when the context decodes, or for a single input row. The dense LINEAR it otherwise
+        falls back to is not part of this library (UNSUPPORTED)."""
+        if transpose_weight and bias is None and self._bound:
+            key = (weight.device.type,
+                   weight.untyped_storage().data_ptr() + weight.storage_offset() * weight.element_size())
+            found = self._bound.get(key)
+            single_row = input.dim() > 0 and input.numel() == input.shape[-1]
+            if (found is not None and found[0].dtype == weight.dtype
+                    and tuple(found[0].shape) == tuple(weight.shape)
+                    and (found[2] or self.decode_projections or single_row)):
+                p = found[1]
+                return self.packed_linear(input, p.values, p.scales, p.bits, p.group_size, 0.0, 0.0, p.zeros)
+        raise Failure("UNSUPPORTED", "dense LINEAR is outside the packed projection library")
 
     def bind_packed_zero(self, scales: torch.Tensor, zeros: torch.Tensor) -> None:
         """Context::bind_packed_zero (ops/context.cpp:813-815)."""
