@@ -14,6 +14,9 @@ ROOT = os.path.dirname(HERE)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 SOURCES = ["csrc/kq_kernels.hip", "csrc/kq_skinny.hip", "csrc/kq_decode.hip", "csrc/kq_gemm.hip", "csrc/kq_gemm_g.hip", "csrc/kq_greedy.hip", "csrc/kq_norm.hip", "csrc/kq_pack.hip", "csrc/kq_api.cpp", "csrc/kq_layout_host.cpp"]
 LIB = os.path.join(HERE, "lib", "libkq_hip.so")
+# Per-source flags: the decode kernels take their first nine scalar arguments preloaded into SGPRs at wave launch
+# (gfx950 kernel-argument preloading; on firmware without it the code object's preamble loads them as usual).
+EXTRA = {"csrc/kq_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"]}
 
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
@@ -28,7 +31,8 @@ def build(verbose: bool = False) -> str:
     procs = []
     for src in SOURCES:
         obj = os.path.join(HERE, "lib", os.path.basename(src) + ".o")
-        cmd = [HIPCC, *FLAGS, "-I", os.path.join(ROOT, "include"), "-c", os.path.join(HERE, src), "-o", obj]
+        cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-I", os.path.join(ROOT, "include"), "-c", os.path.join(HERE, src),
+               "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT), src))

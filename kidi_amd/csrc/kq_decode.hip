@@ -6,8 +6,9 @@
 // pairs, more for large ones (the N = 262,144 output head), so a workgroup's activation quantization serves more
 // weight tiles. Block: W = K/512 waves; wave w owns columns
 // [512 w, 512 w + 512) of both row tiles, i.e. NT = 512/KT weight tiles per row tile. A wave
-//   1. loads its activation pieces (8 columns per lane and row), the group metadata its epilogue lanes need, and
-//      its 2 x NT weight tiles (one 16-byte load per tile per lane), all up front into registers;
+//   1. loads its activation pieces (8 columns per lane and row), its 2 x NT weight tiles (one 16-byte load per tile
+//      per lane) and the group metadata its epilogue lanes need (before the tiles when g < 128), all up front into
+//      registers;
 //   2. quantizes its columns of the M rows into its LDS region (codes in the tiles' permuted order, per-group
 //      scale, code sum, zero point), with the arithmetic of kq_device.hpp;
 //   3. runs one v_mfma_i32_16x16x64_i8 per 64-column block, row tile and group of 4 rows. A row nn of the MFMA is
@@ -26,6 +27,7 @@
 #include <climits>
 #include <cstdint>
 #include <cstdlib>
+#include <type_traits>
 
 #include "kq_device.hpp"
 #include "kq_internal.hpp"
@@ -129,7 +131,12 @@ __device__ __forceinline__ float segment_sum_squares(const float (&v)[8]) {
 // MR: rows of the variant (4 or 8); WMAX: most waves per workgroup (4 for K <= 2048, 16 up to K = 8192), which
 // sets the register budget (512 / (WMAX / 4) VGPRs per lane)
 template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, int MR, int WMAX, bool GREEDY = false, bool NORM = false>
-__global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const std::uint8_t* ptiles, int pM, int pK,
+                                                           int pk_tiles, int pn_tiles, int ppairs, int ptotal, int px_f32,
+                                                           DecodeArgs a) {
+    // The leading scalar arguments duplicate fields of `a`: they are the ones the first loads need, and the build
+    // preloads them into SGPRs at wave launch (-amdgpu-kernarg-preload-count), so the activation and weight loads
+    // go out without waiting for a kernel-argument fetch.
     constexpr int H = MR / 4;            // MFMA row halves: rows 4 h .. 4 h + 3
     constexpr int RT = (WMAX > 4 && !GELU) ? 1 : 2;  // row tiles per unit: one when K > 2048 (more workgroups)
     constexpr int KT = 512 / BITS;       // columns per weight tile
@@ -145,7 +152,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int W = blockDim.x >> 6;
     const int nn = lane & 15, L = lane >> 4;
-    const int M = a.M;
+    const int M = pM, K = pK, k_tiles = pk_tiles, n_tiles = pn_tiles, x_f32 = px_f32;
     const int aslot = nn >> 2;  // A-operand row of this lane: activation row (nn & 3) + 4 h, group slot
 
     // row tiles of a unit: plain 2 p, 2 p + 1 (or the single tile p when RT = 1); GELU the gate tile p and its up
@@ -155,18 +162,18 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     auto set_pair = [&](int pair) {
         if constexpr (GELU) {
             nts[0] = pair;
-            nts[1] = pair + (a.n_tiles >> 1);
+            nts[1] = pair + (n_tiles >> 1);
         } else if constexpr (RT == 1) {
             nts[0] = pair;
-            nts[1] = a.n_tiles;
+            nts[1] = n_tiles;
         } else {
             nts[0] = 2 * pair;
             nts[1] = 2 * pair + 1;
         }
-        live1 = nts[1] < a.n_tiles;
+        live1 = nts[1] < n_tiles;
     };
-    const int pair0 = blockIdx.x * a.pairs;
-    const int pend = min(pair0 + a.pairs, a.total_pairs);
+    const int pair0 = blockIdx.x * ppairs;
+    const int pend = min(pair0 + ppairs, ptotal);
     set_pair(pair0);
 
     std::uint8_t* wl = lds + wave * WAVE_BYTES;
@@ -177,17 +184,17 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     const int zero_slot = WAVE_BYTES - 16;
     if (lane == 0) *reinterpret_cast<uint4*>(wl + zero_slot) = make_uint4(0, 0, 0, 0);
 
-    // ---- 1. loads: activations, metadata, weights (in this order) ----
-    const __amdgpu_buffer_rsrc_t xres = rsrc(a.x, static_cast<std::uint32_t>(M * a.K * (a.x_f32 ? 4 : 2)));
+    // ---- 1. loads: activations, then weights and metadata ----
+    const __amdgpu_buffer_rsrc_t xres = rsrc(px, static_cast<std::uint32_t>(M * K * (x_f32 ? 4 : 2)));
     const int kb = wave * 512;  // first column of this wave
     uint4 xr[MR][2];
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
         if (m < M) {
-            const std::uint32_t e = static_cast<std::uint32_t>(m * a.K + kb + 8 * lane);
-            const std::uint32_t off = a.x_f32 ? 4 * e : 2 * e;
+            const std::uint32_t e = static_cast<std::uint32_t>(m * K + kb + 8 * lane);
+            const std::uint32_t off = x_f32 ? 4 * e : 2 * e;
             xr[m][0] = ld16(xres, off);
-            xr[m][1] = ld16(xres, a.x_f32 ? off + 16 : off);
+            xr[m][1] = ld16(xres, x_f32 ? off + 16 : off);
         }
     }
     // fused RMS normalization (variants of up to 2048 columns): norm weights and residual rows of this lane's piece
@@ -205,14 +212,14 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
                 const float4* p2 = reinterpret_cast<const float4*>(a.norm_w2 + kb + 8 * lane);
                 nw2[0] = p2[0];
                 nw2[1] = p2[1];
-                const __amdgpu_buffer_rsrc_t rres = rsrc(a.norm_res, static_cast<std::uint32_t>(M * a.K * (a.x_f32 ? 4 : 2)));
+                const __amdgpu_buffer_rsrc_t rres = rsrc(a.norm_res, static_cast<std::uint32_t>(M * K * (x_f32 ? 4 : 2)));
 #pragma unroll
                 for (int m = 0; m < MR; ++m) {
                     if (m < M) {
-                        const std::uint32_t e = static_cast<std::uint32_t>(m * a.K + kb + 8 * lane);
-                        const std::uint32_t off = a.x_f32 ? 4 * e : 2 * e;
+                        const std::uint32_t e = static_cast<std::uint32_t>(m * K + kb + 8 * lane);
+                        const std::uint32_t off = x_f32 ? 4 * e : 2 * e;
                         nr[m][0] = ld16(rres, off);
-                        nr[m][1] = ld16(rres, a.x_f32 ? off + 16 : off);
+                        nr[m][1] = ld16(rres, x_f32 ? off + 16 : off);
                     }
                 }
                 if (a.norm_scale) nscale = a.norm_scale[0];
@@ -220,33 +227,45 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
         }
     }
     // metadata entry of quad q for this lane: group 4q + L of the wave, row nn; one 16-byte slot per weight tile
-    const std::uint32_t meta_n = static_cast<std::uint32_t>(a.n_tiles * a.groups_p * kTileRows);
-    const __amdgpu_buffer_rsrc_t sres = rsrc(a.scales, meta_n * (a.scale_half ? 2 : 4));
     std::uint32_t s_raw[RT][NQ], x_raw[RT][NQ];
     uint4 wv[RT][NT];
-    auto load_pair = [&]() {
+    auto load_meta = [&](auto later_unit) {
+        const std::uint32_t meta_n = static_cast<std::uint32_t>(n_tiles * a.groups_p * kTileRows);
+        const __amdgpu_buffer_rsrc_t sres = rsrc(a.scales, meta_n * (a.scale_half ? 2 : 4));
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
             const int nt = (r == 0 || !live1) ? nts[0] : nts[1];
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
                 const std::uint32_t mi = static_cast<std::uint32_t>((nt * a.groups_p + wave * NG + 4 * q + L) * kTileRows + nn);
-                s_raw[r][q] = a.scale_half ? __builtin_amdgcn_raw_buffer_load_b16(sres, 2 * mi, 0, 0)
-                                           : __builtin_amdgcn_raw_buffer_load_b32(sres, 4 * mi, 0, 0);
+                if constexpr (!decltype(later_unit)::value) {
+                    // one dword load whatever the element width, so no branch join (where the wait counters are
+                    // merged conservatively) waits for loads issued before; an F16 entry is the half of its
+                    // aligned dword selected by mi & 1 (meta_n is even, so in bounds)
+                    const std::uint32_t sw = __builtin_amdgcn_raw_buffer_load_b32(sres, a.scale_half ? (2 * mi) & ~3u : 4 * mi, 0, 0);
+                    s_raw[r][q] = a.scale_half ? (sw >> (16 * (mi & 1))) & 0xFFFFu : sw;
+                } else {  // units after a workgroup's first: the element-width loads (measured faster for the head)
+                    s_raw[r][q] = a.scale_half ? __builtin_amdgcn_raw_buffer_load_b16(sres, 2 * mi, 0, 0)
+                                               : __builtin_amdgcn_raw_buffer_load_b32(sres, 4 * mi, 0, 0);
+                }
                 x_raw[r][q] = 0;
                 if constexpr (BITS == 8 && QM == QUANT_DYN_ASYM)
                     x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b32(rsrc(a.aux, meta_n * 4), 4 * mi, 0, 0);
                 if constexpr (BITS != 8 && ZM == ZERO_POINT)
                     x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b8(rsrc(a.aux, meta_n / 2), (mi - nn) / 2 + nn / 2, 0, 0);
-                if constexpr (BITS != 8 && ZM == ZERO_FLOAT)
-                    x_raw[r][q] = a.aux_half ? __builtin_amdgcn_raw_buffer_load_b16(rsrc(a.aux, meta_n * 2), 2 * mi, 0, 0)
-                                             : __builtin_amdgcn_raw_buffer_load_b32(rsrc(a.aux, meta_n * 4), 4 * mi, 0, 0);
+                if constexpr (BITS != 8 && ZM == ZERO_FLOAT) {
+                    const std::uint32_t zw = __builtin_amdgcn_raw_buffer_load_b32(rsrc(a.aux, meta_n * (a.aux_half ? 2 : 4)),
+                                                                                  a.aux_half ? (2 * mi) & ~3u : 4 * mi, 0, 0);
+                    x_raw[r][q] = a.aux_half ? (zw >> (16 * (mi & 1))) & 0xFFFFu : zw;
+                }
             }
         }
-        const __amdgpu_buffer_rsrc_t w0 = rsrc(a.tiles + static_cast<std::int64_t>(nts[0]) * a.k_tiles * kTileBytes,
-                                               static_cast<std::uint32_t>(a.k_tiles * kTileBytes));
-        const __amdgpu_buffer_rsrc_t w1 = rsrc(a.tiles + static_cast<std::int64_t>(live1 ? nts[1] : nts[0]) * a.k_tiles * kTileBytes,
-                                               static_cast<std::uint32_t>(a.k_tiles * kTileBytes));
+    };
+    auto load_weights = [&]() {
+        const __amdgpu_buffer_rsrc_t w0 = rsrc(ptiles + static_cast<std::int64_t>(nts[0]) * k_tiles * kTileBytes,
+                                               static_cast<std::uint32_t>(k_tiles * kTileBytes));
+        const __amdgpu_buffer_rsrc_t w1 = rsrc(ptiles + static_cast<std::int64_t>(live1 ? nts[1] : nts[0]) * k_tiles * kTileBytes,
+                                               static_cast<std::uint32_t>(k_tiles * kTileBytes));
 #pragma unroll
         for (int u = 0; u < NT; ++u) {
             const std::uint32_t off = static_cast<std::uint32_t>((wave * NT + u) * kTileBytes + 16 * lane);
@@ -254,15 +273,30 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
             if constexpr (RT == 2) wv[RT - 1][u] = ld16(w1, off);
         }
     };
-    load_pair();
+    // Vector loads return in issue order, so the quantization (which needs only the activations) waits for the
+    // loads issued before the weights. With one quad of groups per wave (g = 128) the metadata is needed only after
+    // the last weight tile, so the weights go first: their addresses come from the preloaded arguments and need
+    // no wait for the argument struct. With several quads the first epilogue runs while later tiles are still in
+    // flight, so the metadata goes first.
+    auto load_units = [&](auto later_unit) {
+        if constexpr (NQ == 1) {
+            load_weights();
+            __builtin_amdgcn_sched_barrier(0);  // nothing that waits on the argument struct moves above the weights
+            load_meta(later_unit);
+        } else {
+            load_meta(later_unit);
+            load_weights();
+        }
+    };
+    load_units(std::false_type{});
 
     // ---- 1b. fused RMS normalization: row sums of squares over the workgroup's waves (= the whole row) ----
     float ninv1[MR], ninv2[MR];
     // h = (r + x * inv1 * w1) [* s] of this lane's piece of row m (the residual form's output)
     auto hidden_piece = [&](int m, float (&h)[8]) {
         float v[8];
-        decode_piece(xr[m], a.x_f32 != 0, v);
-        decode_piece(nr[NORM_OK ? m : 0], a.x_f32 != 0, h);
+        decode_piece(xr[m], x_f32 != 0, v);
+        decode_piece(nr[NORM_OK ? m : 0], x_f32 != 0, h);
         const float w[8] = {nw1[0].x, nw1[0].y, nw1[0].z, nw1[0].w, nw1[1].x, nw1[1].y, nw1[1].z, nw1[1].w};
 #pragma unroll
         for (int i = 0; i < 8; ++i) h[i] = (h[i] + v[i] * ninv1[m] * w[i]) * nscale;
@@ -270,12 +304,12 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     if constexpr (NORM_OK) {
         if (a.norm) {
             float* nsum = reinterpret_cast<float*>(lds + W * WAVE_BYTES + W * 2 * MR * 16 * 4 + MR * 16);  // [2][W][MR]
-            const float kf = static_cast<float>(a.K);
+            const float kf = static_cast<float>(K);
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 if (m < M) {
                     float v[8];
-                    decode_piece(xr[m], a.x_f32 != 0, v);
+                    decode_piece(xr[m], x_f32 != 0, v);
                     const float t = segment_sum_squares(v);
                     if (lane == 0) nsum[wave * MR + m] = t;
                 }
@@ -296,7 +330,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
                         float h[8];
                         hidden_piece(m, h);
                         if (blockIdx.x == 0) {
-                            float4* hp = reinterpret_cast<float4*>(a.norm_hidden + static_cast<std::int64_t>(m) * a.K + kb + 8 * lane);
+                            float4* hp = reinterpret_cast<float4*>(a.norm_hidden + static_cast<std::int64_t>(m) * K + kb + 8 * lane);
                             hp[0] = make_float4(h[0], h[1], h[2], h[3]);
                             hp[1] = make_float4(h[4], h[5], h[6], h[7]);
                         }
@@ -323,7 +357,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     for (int m = 0; m < MR; ++m) {
         if (m < M) {
             float v[8];
-            decode_piece(xr[m], a.x_f32 != 0, v);
+            decode_piece(xr[m], x_f32 != 0, v);
             if constexpr (NORM_OK) {
                 if (a.norm == 1) {
                     const float w[8] = {nw1[0].x, nw1[0].y, nw1[0].z, nw1[0].w, nw1[1].x, nw1[1].y, nw1[1].z, nw1[1].w};
@@ -368,7 +402,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
                     if (a.dq_zeros) a.dq_zeros[o] = qb.zp;
                 }
             }
-            if (dump_block && a.dq_codes) *reinterpret_cast<uint2*>(a.dq_codes + m * a.K + kb + 8 * lane) = make_uint2(lo, hi);
+            if (dump_block && a.dq_codes) *reinterpret_cast<uint2*>(a.dq_codes + m * K + kb + 8 * lane) = make_uint2(lo, hi);
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -389,7 +423,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     for (int pair = pair0; pair < pend; ++pair) {
     if (pair != pair0) {  // the first pair's loads went out before the quantization
         set_pair(pair);
-        load_pair();
+        load_units(std::true_type{});
     }
     float acc[RT][MR];
     v4i C[RT][H];
@@ -484,8 +518,11 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
         for (int i = 0; i < MR; ++i) {
             if (i < M) {
                 float v = acc[r][i];
-                v = v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));  // xor 16
-                v = v + __shfl_xor(v, 32);
+                // v(l) + v(l ^ 16), then + the same of l ^ 32: row swaps on the VALU (gfx950), no LDS round trip
+                const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+                v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+                const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+                v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
                 if (L == 0) red[((wave * RT + r) * MR + i) * 16 + nn] = v;
             }
         }
@@ -509,7 +546,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
         } else {
             const int nt = r == 0 ? cur_nt0 : cur_nt1;
             const int n = nt * kTileRows + c;
-            const bool valid = nt < a.n_tiles && n < a.N;
+            const bool valid = nt < n_tiles && n < a.N;
             if (valid && (!GREEDY || a.y)) a.y[static_cast<std::int64_t>(i) * a.N + n] = v[0];
             if constexpr (GREEDY) {
                 // this pair's best of row i over its RT x 16 lanes (larger value, then lower column), merged into
@@ -545,6 +582,8 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(DecodeArgs a) {
     }
 }
 
+#define KQ_DECODE_ARGS(a) (a).x, (a).tiles, (a).M, (a).K, (a).k_tiles, (a).n_tiles, (a).pairs, (a).total_pairs, (a).x_f32, (a)
+
 template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, bool GREEDY = false>
 hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds, hipStream_t stream) {
     // debug variants: one register budget for every K; single-tile units: the wide variants are the RT = 1 ones
@@ -552,17 +591,17 @@ hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds,
     if constexpr (!DBG && !GREEDY) {
         if (a.norm) {  // decode_fits admits the fused normalization only for the 4-wave variants
             if (wide) return hipErrorInvalidValue;
-            if (a.M <= 4) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 4, false, true>), grid, block, lds, stream, a);
-            else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 8, 4, false, true>), grid, block, lds, stream, a);
+            if (a.M <= 4) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 4, false, true>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
+            else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 8, 4, false, true>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
             return hipGetLastError();
         }
     }
     if (a.M <= 4) {
-        if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, 16, GREEDY>), grid, block, lds, stream, a);
-        else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, (DBG ? 16 : 4), GREEDY>), grid, block, lds, stream, a);
+        if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, 16, GREEDY>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
+        else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 4, (DBG ? 16 : 4), GREEDY>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
     } else {
-        if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 8, 16, GREEDY>), grid, block, lds, stream, a);
-        else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 8, (DBG ? 16 : 4), GREEDY>), grid, block, lds, stream, a);
+        if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 8, 16, GREEDY>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
+        else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, DBG, 8, (DBG ? 16 : 4), GREEDY>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
     }
     return hipGetLastError();
 }
