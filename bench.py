@@ -272,6 +272,29 @@ def main():
     mall_ms = e0.elapsed_time(e1) / (20 * 64)
     del g1
 
+    # Read floor of one launch at this size: kq_debug_read_floor only reads the same number of bytes once (launch
+    # shape and argument preloading of the decode kernel), over R rotated buffers, graph-replayed like the decode
+    # steps. It bounds what any single-launch kernel of this size can reach (launch, ramp and HBM latency
+    # included); reported beside the roofline.
+    fb = -(-bytes_step // 16) * 16
+    bufs = [torch.randint(0, 256, (fb,), dtype=torch.uint8, device=dev, generator=gen) for _ in range(R)]
+    sink = torch.zeros((1,), dtype=torch.int32, device=dev)
+    floor_calls = [lambda s, b=b: _ok(lib, lib.kq_debug_read_floor(b.data_ptr(), fb, sink.data_ptr(), s)) for b in bufs]
+    for c in floor_calls:
+        c(stream_ptr())
+    torch.cuda.synchronize()
+    gr = capture(torch, floor_calls, stream_ptr)
+    for _ in range(3):
+        gr.replay()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(20):
+        gr.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    floor_us = e0.elapsed_time(e1) * 1e3 / (20 * R)
+    del gr, bufs, floor_calls
+
     del graph_full, rem_graphs
     first_cpu = tuple(t.cpu() for t in first)
     x_cpu = x.cpu()
@@ -335,6 +358,9 @@ def main():
         "wall_s": round(wall, 4),
         "parity": parity,
         "mall_resident_gbs": round(bytes_step / (mall_ms * 1e-3) / 1e9, 1),
+        "read_floor": {"us_per_launch": round(floor_us, 3), "gbs": round(bytes_step / (floor_us * 1e-6) / 1e9, 1),
+                       "frac": round(bytes_step / (floor_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                       "how": "kq_debug_read_floor: one launch reading the same bytes once, rotated buffers, HIP graph"},
         "prefill": {"workload": "GEMM M=2048 K=2048 N=8192 asymmetric int4 g=128 (configs[2])",
                     "ms": round(pre_ms, 5), "tops": round(pre_tops, 2),
                     "mfma_frac": round(pre_tops / INT8_PEAK_TOPS, 4), "parity_ok": bool(pre_ok),
@@ -435,6 +461,26 @@ def _ok(lib, status):
 def bench_extras(torch, N_, lib, dev, gen):
     E = Extras(torch, N_, lib, dev, gen)
     out = {}
+    # configs[0] (symmetric g = 32 up projection) on the GPU, configs[1]'s other decode shapes (M = 4; the down
+    # projection K = 8192, N = 2048 at M = 1 and 4) and configs[2]'s M = 512 prefill
+    shapes = {}
+    for name, K, N, g, asym, M in (("c0_sym_g32_up_M1", 2048, 8192, 32, False, 1),
+                                   ("c1_asym_g128_up_M4", 2048, 8192, 128, True, 4),
+                                   ("c1_asym_g128_down_M1", 8192, 2048, 128, True, 1),
+                                   ("c1_asym_g128_down_M4", 8192, 2048, 128, True, 4),
+                                   ("c2_prefill_M512", 2048, 8192, 128, True, 512)):
+        dws = E.weights(N, K, 4, g, asym, rotate=2 if M > 16 else None)
+        x = E.x(M, K)
+        calls, keep = E.linear_calls(dws, x, M, N)
+        us = E.time_calls(calls, 20 if M <= 16 else 10)
+        b = layer_bytes(M, K, N, g, 4, asym)
+        ops = 2 * M * N * K
+        shapes[name] = {"us": round(us, 3), "gbs": round(b / us / 1e3, 1), "tops": round(ops / us / 1e6, 1),
+                        "rotated": len(dws)}
+        del calls, keep, dws
+    out["configs0_2_shapes"] = shapes
+    torch.cuda.empty_cache()
+
     H, I, KV = 2048, 8192, 2048 + 256 + 256
     # decoder-layer projections, M = 1 (GB/s) and M = 2048 (TOP/s)
     qkv = E.weights(KV, H, 4, 32, False)

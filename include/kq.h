@@ -251,6 +251,13 @@ kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_d
  * (ZP_U8 zero-points, u = c + 8) or c (additive float zeros), and x_code = q - zp_a for 8-bit dynamic. */
 kq_status kq_debug_partials(const kq_weight* weight, const kq_linear_args* args, int32_t* partials, void* stream);
 
+/* ---- measurement instrumentation (no counterpart in the reference) ----------------------------------------- */
+
+/* One launch that only reads `bytes` (a multiple of 16, at most 2 GiB) of device memory once, with the launch
+ * shape and argument preloading of the decode kernel; `sink` is a device int32 it writes only by chance. Its
+ * per-launch time is the floor of any single-launch kernel that streams a buffer of that size. */
+kq_status kq_debug_read_floor(const void* data, size_t bytes, int32_t* sink, void* stream);
+
 /* Host-only (no GPU): the gfx950 tile layout of a Kidi-layout weight and its inverse, for layout tests. */
 size_t kq_layout_bytes(int32_t bits, int32_t group_size, int64_t rows, int64_t cols);
 kq_status kq_layout_encode_host(int32_t bits, int64_t rows, int64_t cols, const uint8_t* values, uint8_t* tiles);

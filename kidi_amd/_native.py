@@ -27,7 +27,7 @@ EXPORTS = (
     "kq_layout_encode_host", "kq_layout_decode_host", "kq_ffn_workspace_size", "kq_gated_feed_forward",
     "kq_greedy_workspace_size", "kq_greedy_token", "kq_greedy_linear_workspace_size", "kq_packed_linear_greedy",
     "kq_weight_export_size", "kq_weight_export", "kq_weight_import", "kq_rms_norm", "kq_rms_linear_workspace_size",
-    "kq_packed_linear_rms", "kq_quantize_weight",
+    "kq_packed_linear_rms", "kq_quantize_weight", "kq_debug_read_floor",
 )
 
 
@@ -168,6 +168,8 @@ def load() -> ctypes.CDLL:
     L.kq_packed_linear_rms.restype = ctypes.c_int
     L.kq_quantize_weight.argtypes = [vp, ctypes.c_int, i64, i64, i32, i32, i32, vp, vp, vp, vp]
     L.kq_quantize_weight.restype = ctypes.c_int
+    L.kq_debug_read_floor.argtypes = [vp, ctypes.c_size_t, vp, vp]
+    L.kq_debug_read_floor.restype = ctypes.c_int
     L.kq_debug_quantize.argtypes = [vp, vp, ctypes.c_int, i64, f32, vp, vp, vp, vp, vp]
     L.kq_debug_quantize.restype = ctypes.c_int
     L.kq_debug_partials.argtypes = [vp, ctypes.POINTER(LinearArgs), vp, vp]

@@ -1023,6 +1023,15 @@ kq_status kq_debug_partials(const kq_weight* weight, const kq_linear_args* args,
     return run_call(c, args, ws, static_cast<hipStream_t>(stream));
 }
 
+kq_status kq_debug_read_floor(const void* data, size_t bytes, int32_t* sink, void* stream) {
+    if (!data || !sink || bytes == 0 || bytes > (std::size_t{1} << 31) || bytes % 16)
+        return fail(KQ_INVALID_ARGUMENT, "read floor: device buffer of 16-byte multiple size up to 2 GiB");
+    if (hipError_t e = kq::launch_read_floor(data, static_cast<std::uint32_t>(bytes), sink, static_cast<hipStream_t>(stream));
+        e != hipSuccess)
+        return hip_fail(e, "read floor launch");
+    return KQ_OK;
+}
+
 size_t kq_layout_bytes(int32_t bits, int32_t group_size, int64_t rows, int64_t cols) {
     if ((bits != 2 && bits != 4 && bits != 8) || rows <= 0 || cols <= 0) return 0;
     return static_cast<size_t>(kq::Geometry::make(bits, group_size, rows, cols).tile_bytes_total());

@@ -624,6 +624,23 @@ hipError_t launch_modes(const DecodeArgs& a, int g, bool gelu, bool dbg, bool gr
 
 int wave_bytes(int g, int mr) { return mr * 512 + 3 * 4 * mr * (512 / g) + 16; }
 
+// Measurement instrumentation: one launch that reads `bytes` once (8 x 16 bytes per lane, 256-lane workgroups,
+// arguments preloaded like the decode kernel's) and stores nothing unless the data XOR to a magic value: the floor
+// of any single-launch kernel that streams a buffer of this size.
+constexpr int kFloorLoads = 8;
+__global__ __launch_bounds__(256) void read_floor_kernel(const void* data, unsigned bytes, int* sink) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(data, bytes);
+    const unsigned total = gridDim.x * blockDim.x;
+    const unsigned t = blockIdx.x * blockDim.x + threadIdx.x;
+    uint4 v[kFloorLoads];
+#pragma unroll
+    for (int i = 0; i < kFloorLoads; ++i) v[i] = ld16(r, 16u * (t + i * total));  // past `bytes`: zeros
+    unsigned acc = 0;
+#pragma unroll
+    for (int i = 0; i < kFloorLoads; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    if (acc == 0x9e3779b9u) sink[0] = static_cast<int>(t);
+}
+
 }  // namespace
 
 bool decode_fits(const LinearCall& c) {
@@ -640,6 +657,13 @@ bool decode_fits(const LinearCall& c) {
         c.M * w.geo.cols * 4 >= (std::int64_t{1} << 31) || w.geo.n_tiles * w.geo.k_tiles * kTileBytes >= (std::int64_t{1} << 46))
         return false;
     return true;
+}
+
+hipError_t launch_read_floor(const void* data, std::uint32_t bytes, int* sink, hipStream_t stream) {
+    const std::uint32_t per_block = 16u * kFloorLoads * 256u;
+    const unsigned blocks = (bytes + per_block - 1) / per_block;
+    hipLaunchKernelGGL(read_floor_kernel, dim3(blocks), dim3(256), 0, stream, data, bytes, sink);
+    return hipGetLastError();
 }
 
 hipError_t launch_decode(const LinearCall& c, hipStream_t stream) {

@@ -93,6 +93,9 @@ struct NormLaunch {
 };
 hipError_t launch_rms_norm(const NormLaunch& n, hipStream_t stream);
 
+// Measurement instrumentation (kq_decode.hip): one launch that only reads `bytes` of `data` once.
+hipError_t launch_read_floor(const void* data, std::uint32_t bytes, int* sink, hipStream_t stream);
+
 // Load-time weight quantization (kq_pack.hip): float weights -> Kidi-layout codes, scales, zeros; error: 1 non-finite
 // weight, 2 symmetric scale underflow (OR-ed into *error).
 hipError_t launch_pack_weight(const void* w, int dtype, std::int64_t rows, std::int64_t width, int bits, std::int64_t group,
