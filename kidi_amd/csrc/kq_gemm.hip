@@ -628,6 +628,25 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
     KQ_READ_A(3, 0);
 
     float sv[4], asel[4];  // weight and activation scales of the current step
+    // Dynamic activations with F16 weight scales: the MFMAs of a group start from the bits of 1.5 * 2^23 instead of 0,
+    // so the int32 accumulator holds 0x4B400000 + P', which read as f32 is exactly 12582912 + P' (|P'| < 2^22). One
+    // FMA, (12582912 + P') * s + nb with nb = -12582912 * s, then gives round(s * P') -- the reference's t = s * P'
+    // bit for bit: s comes from an F16 value (at most 11 significant bits), so nb is exact, and the FMA rounds the
+    // exact s * P' once. acc += a_s * t is the second instruction (v_fmac with a DPP quad broadcast of a_s), two VALU
+    // per element and group instead of three (conversion, product of the scales, FMA).
+    constexpr bool kBias = SH && QM != QUANT_STATIC;
+    constexpr float kBiasF = 12582912.0F;
+    // The bias tuple comes out of inline assembly once, so the compiler keeps it in registers instead of
+    // rematerializing the constant (a VALU write) in front of an MFMA that reads it: the hazard recognizer does not
+    // see the MFMA inside the assembly and would not separate the two by the 2 wait states such a read needs.
+    v4i biasv = {0, 0, 0, 0};
+    if constexpr (kBias) {
+        int b0, b1, b2, b3;
+        KQ_ASM("v_mov_b32 %0, 0x4b400000\n\tv_mov_b32 %1, 0x4b400000\n\tv_mov_b32 %2, 0x4b400000\n\tv_mov_b32 %3, 0x4b400000"
+               : "=v"(b0), "=v"(b1), "=v"(b2), "=v"(b3));
+        biasv = v4i{b0, b1, b2, b3};
+    }
+    float nbv[4];
     // Block b: two int8 MFMAs give the exact partials P' of the step's group. The epilogue of block b, issued after
     // the MFMAs of block b + 1, forms k = a_s * s in the accumulator's lane layout (lane = column nn + 16 L,
     // register r = row 4 L + r): the lane quad 4 (lane / 4) .. + 3 holds a_s of rows 16 mi + 4 L + 0..3 (one per
@@ -642,6 +661,7 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
             for (int i = 0; i < 4; ++i) {
                 sv[i] = SH ? __half2float(__ushort_as_half(static_cast<unsigned short>(svr[i]))) : __uint_as_float(svr[i]);
                 asel[i] = __int_as_float(asr[i]);
+                if constexpr (kBias) nbv[i] = -kBiasF * sv[i];
             }
         }
         if (blk == 1) lgkm_wait<6>(B[1][0], B[1][1]);
@@ -651,7 +671,10 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
 #if defined(__HIP_DEVICE_COMPILE__)
         if constexpr (!DBG) {
             // issue order pinned (see the epilogue)
-            KQ_ASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=&v"(c) : "v"(A[mi][0]), "v"(B[ni][0]));
+            if constexpr (kBias)
+                KQ_ASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, %3" : "=&v"(c) : "v"(A[mi][0]), "v"(B[ni][0]), "v"(biasv));
+            else
+                KQ_ASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=&v"(c) : "v"(A[mi][0]), "v"(B[ni][0]));
             KQ_ASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(c) : "v"(A[mi][1]), "v"(B[ni][1]));
             return;
         }
@@ -668,6 +691,15 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
             // instructions separate every MFMA result from its first VALU read, beyond the dependency window.
             // (asel is last written at the step's first block, long before these DPP reads.)
             float kk[4], t[4];
+            if constexpr (kBias) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) KQ_ASM("v_fma_f32 %0, %1, %2, %3" : "=v"(t[r]) : "v"(c[r]), "v"(sv[ni]), "v"(nbv[ni]));
+                KQ_ASM("v_fmac_f32_dpp %0, %1, %2 quad_perm:[0,0,0,0] row_mask:0xf bank_mask:0xf" : "+v"(acc[mi][ni][0]) : "v"(asel[mi]), "v"(t[0]));
+                KQ_ASM("v_fmac_f32_dpp %0, %1, %2 quad_perm:[1,1,1,1] row_mask:0xf bank_mask:0xf" : "+v"(acc[mi][ni][1]) : "v"(asel[mi]), "v"(t[1]));
+                KQ_ASM("v_fmac_f32_dpp %0, %1, %2 quad_perm:[2,2,2,2] row_mask:0xf bank_mask:0xf" : "+v"(acc[mi][ni][2]) : "v"(asel[mi]), "v"(t[2]));
+                KQ_ASM("v_fmac_f32_dpp %0, %1, %2 quad_perm:[3,3,3,3] row_mask:0xf bank_mask:0xf" : "+v"(acc[mi][ni][3]) : "v"(asel[mi]), "v"(t[3]));
+                return;
+            }
             if constexpr (QM == QUANT_STATIC) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) kk[r] = sv[ni];
@@ -701,6 +733,11 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
                                : ctrl == 0x55 ? __builtin_amdgcn_mov_dpp(bits, 0x55, 0xF, 0xF, false)
                                : ctrl == 0xAA ? __builtin_amdgcn_mov_dpp(bits, 0xAA, 0xF, 0xF, false)
                                               : __builtin_amdgcn_mov_dpp(bits, 0xFF, 0xF, 0xF, false);
+                if constexpr (kBias) {  // the biased form's arithmetic: t = s * P' rounded once, acc += a_s * t fused
+                    const float t = sv[ni] * static_cast<float>(P);
+                    acc[mi][ni][r] = __builtin_fmaf(__int_as_float(rs), t, acc[mi][ni][r]);
+                    continue;
+                }
                 kk = __int_as_float(rs) * sv[ni];
             }
             acc[mi][ni][r] = __builtin_fmaf(kk, static_cast<float>(P), acc[mi][ni][r]);
@@ -708,11 +745,12 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
     };
     auto sched_blocks = [&]() {
         if constexpr (!DBG) {
-            // one block: 2 MFMAs, then the 12 VALU of the previous block's epilogue (8 with static activations)
+            // one block: 2 MFMAs, then the VALU of the previous block's epilogue (12; 8 with static activations or
+            // the biased accumulators)
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, QM == QUANT_STATIC ? 8 : 12, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, (QM == QUANT_STATIC || kBias) ? 8 : 12, 0);
             }
         }
         __builtin_amdgcn_sched_barrier(0);

@@ -1,10 +1,12 @@
 """Static check of the device code: an MFMA result may not be read by a VALU instruction until enough wait states have
-passed. The compiler inserts those wait states for the MFMA builtins, but its hazard recognizer does not look into
-inline assembly, and the prefill GEMMs issue their MFMAs and epilogues as inline assembly (to pin their order). The
-required distance is measured here, not assumed: a probe kernel built from the builtins is compiled and the s_nop the
-compiler puts between each MFMA and a dependent VALU read is taken as the requirement. Every inline-assembly MFMA of
-the prefill kernels must then be followed by at least that many wait states (instructions, s_nop n counting n + 1)
-before the first VALU instruction that reads one of its destination registers."""
+passed, and an MFMA may not read a register that a VALU instruction wrote until enough wait states have passed.
+The compiler inserts those wait states for the MFMA builtins, but its hazard recognizer does not look into inline
+assembly, and the prefill GEMMs issue their MFMAs and epilogues as inline assembly (to pin their order). The
+required distances are measured here, not assumed: probe kernels built from the builtins are compiled and the s_nop
+the compiler puts between each MFMA and a dependent VALU read (and between a VALU write and an MFMA reading it) is
+taken as the requirement. Every inline-assembly MFMA of the prefill kernels must then be followed by at least that
+many wait states (instructions, s_nop n counting n + 1) before the first VALU instruction that reads one of its
+destination registers, and preceded by at least that many after the last VALU write of one of its sources."""
 
 import os
 import re
@@ -31,6 +33,10 @@ __global__ void p32(const long* a, const long* b, float* o) {
 __global__ void p64(const v4i* a, const v4i* b, float* o) {
     v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[threadIdx.x], b[threadIdx.x], v4i{0, 0, 0, 0}, 0, 0, 0);
     o[threadIdx.x] = (float)c[0];
+}
+__global__ void pw(const v4i* a, const v4i* b, v4i* o) {
+    v4i A = a[threadIdx.x], B = b[threadIdx.x];
+    o[threadIdx.x] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, A ^ B, 0, 0, 0);
 }
 __global__ void p4(const float* a, const float* b, float* o) {
     v4f c = __builtin_amdgcn_mfma_f32_4x4x1f32(a[threadIdx.x], b[threadIdx.x], v4f{0, 0, 0, 0}, 0, 0, 0);
@@ -59,7 +65,10 @@ def instructions(func: str):
         if ";;#ASMEND" in line:
             in_asm = False
         ins = line.split(";")[0].strip()
-        if not ins or ins.endswith(":") or ins.startswith("."):
+        if ins.endswith(":") and not ins.startswith("_Z"):
+            out.append(("<label>", "", in_asm))
+            continue
+        if not ins or ins.startswith("."):
             continue
         op = ins.split()[0]
         out.append((op, ins[len(op):], in_asm))
@@ -81,11 +90,41 @@ def distances(asm: str, only_inline: bool):
             dest = vgprs(args.split(",")[0])
             waits = 0
             for op2, args2, _ in ins[i + 1:]:
+                if op2 == "<label>":
+                    continue
                 if op2.startswith("s_cbranch") or op2 in ("s_branch", "s_setpc_b64"):
                     waits = None
                     break
                 srcs = args2.split(",", 1)[1] if "," in args2 else ""
                 if op2.startswith("v_") and not op2.startswith("v_mfma") and vgprs(srcs) & dest:
+                    break
+                waits += int(args2.split()[0]) + 1 if op2 == "s_nop" else 1
+            else:
+                waits = None
+            if waits is not None:
+                found.append((name, op, waits))
+    return found
+
+
+def source_distances(asm: str, only_inline: bool):
+    """(kernel, mfma opcode, wait states since the last VALU write of one of its source registers) for every MFMA
+    with such a write earlier in its straight-line run (a label or branch ends the backward scan)."""
+    found = []
+    for func in re.split(r"\n(?=_Z\w+:)", asm):
+        name = func.split(":", 1)[0]
+        if not name.startswith("_Z"):
+            continue
+        ins = instructions(func)
+        for i, (op, args, in_asm) in enumerate(ins):
+            if op not in MFMAS or (only_inline and not in_asm):
+                continue
+            srcs = vgprs(args.split(",", 1)[1]) if "," in args else set()
+            waits = 0
+            for op2, args2, _ in reversed(ins[:i]):
+                if op2 == "<label>" or op2.startswith("s_cbranch") or op2 in ("s_branch", "s_setpc_b64"):
+                    waits = None
+                    break
+                if op2.startswith("v_") and not op2.startswith("v_mfma") and vgprs(args2.split(",")[0]) & srcs:
                     break
                 waits += int(args2.split()[0]) + 1 if op2 == "s_nop" else 1
             else:
@@ -104,6 +143,14 @@ def test_checker_measures_distance():
     asm = "\n".join(["_Zk:", ";;#ASMSTART", "v_mfma_i32_16x16x32_i8 v[4:7], v[0:1], v[2:3], 0", ";;#ASMEND",
                      "v_mov_b32_e32 v9, v1", "s_nop 3", "v_cvt_f32_i32_e32 v8, v5", "s_endpgm"])
     assert distances(asm, True) == [("_Zk", "v_mfma_i32_16x16x32_i8", 5)]
+    asm = "\n".join(["_Zk:", "v_mov_b32_e32 v9, 0", "v_xor_b32_e32 v2, v1, v0", "s_nop 0", ";;#ASMSTART",
+                     "v_mfma_i32_16x16x64_i8 v[4:7], v[0:3], v[8:11], v[12:15]", ";;#ASMEND", "s_endpgm"])
+    assert source_distances(asm, True) == [("_Zk", "v_mfma_i32_16x16x64_i8", 1)]
+    assert source_distances(asm.replace("v_xor_b32_e32 v2", "v_xor_b32_e32 v20"), True) == [
+        ("_Zk", "v_mfma_i32_16x16x64_i8", 2)]
+    # a label ends the backward scan
+    asm = asm.replace("v_xor_b32_e32 v2", "v_xor_b32_e32 v20").replace("v_mov_b32_e32 v9, 0", "v_mov_b32_e32 v9, 0\n.LBB0_1:")
+    assert source_distances(asm, True) == []
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
@@ -135,3 +182,10 @@ def test_inline_mfma_results_wait_as_long_as_the_compiler_requires():
                 bad.append((src, name[:70], op, waits, need[op]))
     assert seen > 0
     assert not bad, "\n".join(f"{s} {k}: {op} read after {w} wait states (needs {n})" for s, k, op, w, n in bad[:10])
+    # sources: a VALU write followed by an MFMA that reads the register
+    need_src = min(w for k, op, w in source_distances(texts["probe"], False) if k.startswith("_Z2pw"))
+    assert need_src >= 2, need_src
+    bad = [(src, name[:70], op, waits) for src in SOURCES for name, op, waits in source_distances(texts[src], True)
+           if waits < need_src]
+    assert not bad, "\n".join(f"{s} {k}: {op} reads a VALU result after {w} wait states (needs {need_src})"
+                               for s, k, op, w in bad[:10])
