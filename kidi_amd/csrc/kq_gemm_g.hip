@@ -209,6 +209,20 @@ __global__ __launch_bounds__(64 * WAVES, WAVES / 2) void gemm_i4g_kernel(GArgs a
             for (int r = 0; r < 4; ++r) acc[mi][ni][r] = 0.F;
     const v4f zerof = {0.F, 0.F, 0.F, 0.F};
     const v4i zero = {0, 0, 0, 0};
+    // Dynamic activations with F16 weight scales: each group's MFMA starts from the bits of 1.5 * 2^23, so the
+    // accumulator read as f32 is exactly 12582912 + P' (|P'| < 2^22), and fma(that, s, -12582912 * s) is round(s * P')
+    // (-12582912 * s is exact for an s of at most 11 significant bits): the conversion and the weight scale in one
+    // instruction, acc += a_s * t in a second. The bias registers come out of inline assembly once, so the compiler
+    // keeps them instead of rematerializing the constant (a VALU write) just before an MFMA that reads it.
+    constexpr bool kBias = SH && QM != QUANT_STATIC;
+    constexpr float kBiasF = 12582912.0F;
+    v4i biasv = zero;
+    if constexpr (kBias) {
+        int b0, b1, b2, b3;
+        KQ_GASM("v_mov_b32 %0, 0x4b400000\n\tv_mov_b32 %1, 0x4b400000\n\tv_mov_b32 %2, 0x4b400000\n\tv_mov_b32 %3, 0x4b400000"
+                : "=v"(b0), "=v"(b1), "=v"(b2), "=v"(b3));
+        biasv = v4i{b0, b1, b2, b3};
+    }
 
     load(0);
     store(0);
@@ -236,6 +250,8 @@ __global__ __launch_bounds__(64 * WAVES, WAVES / 2) void gemm_i4g_kernel(GArgs a
             for (int h = 0; h < HALVES; ++h) {
                 const int gi = G == 32 ? 2 * j + h : j;  // group of the step
                 const v4f sv4 = *reinterpret_cast<const v4f*>(ws + ((gi * 2 + wn) * 16 + nn) * 4);
+                v4f nb4 = zerof;
+                if constexpr (kBias) nb4 = sv4 * -kBiasF;
                 v4f as4[MI];  // activation scales of rows 16 mi + 4 L + r, r = 0..3 (the accumulator's rows)
 #pragma unroll
                 for (int mi = 0; mi < MI; ++mi) {
@@ -254,6 +270,13 @@ __global__ __launch_bounds__(64 * WAVES, WAVES / 2) void gemm_i4g_kernel(GArgs a
                     const long bv = (static_cast<long>(static_cast<std::uint32_t>(B[ni][2 * h + 1])) << 32) |
                                     static_cast<std::uint32_t>(B[ni][2 * h]);
                     if constexpr (!DBG) {
+                        if constexpr (kBias) {
+                            if constexpr (G == 32)
+                                KQ_GASM("v_mfma_i32_16x16x32_i8 %0, %1, %2, %3" : "=&v"(c) : "v"(av), "v"(bv), "v"(biasv));
+                            else
+                                KQ_GASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, %3" : "=&v"(c) : "v"(A[mi]), "v"(B[ni]), "v"(biasv));
+                            return;
+                        }
                         if constexpr (G == 32) KQ_GASM("v_mfma_i32_16x16x32_i8 %0, %1, %2, 0" : "=&v"(c) : "v"(av), "v"(bv));
                         else KQ_GASM("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=&v"(c) : "v"(A[mi]), "v"(B[ni]));
                         return;
@@ -263,6 +286,15 @@ __global__ __launch_bounds__(64 * WAVES, WAVES / 2) void gemm_i4g_kernel(GArgs a
                 };
                 auto epilogue = [&](int blk, const v4i& c) {
                     const int mi = blk >> 2, ni = blk & 3;
+                    if constexpr (!DBG && kBias) {
+                        float t[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) KQ_GASM("v_fma_f32 %0, %1, %2, %3" : "=v"(t[r]) : "v"(c[r]), "v"(sv4[ni]), "v"(nb4[ni]));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) KQ_GASM("v_fmac_f32 %0, %1, %2" : "+v"(acc[mi][ni][r]) : "v"(as4[mi][r]), "v"(t[r]));
+                        (void)t;  // (the host pass compiles the assembly out)
+                        return;
+                    }
                     if constexpr (!DBG) {
                         float kk[4], t[4];
 #pragma unroll
@@ -285,6 +317,11 @@ __global__ __launch_bounds__(64 * WAVES, WAVES / 2) void gemm_i4g_kernel(GArgs a
                         const int b = k * GPS + gi;
                         if (a.dump && row < a.M && nt < a.n_tiles && col < a.N && b < a.groups)
                             a.dump[(static_cast<std::int64_t>(row) * a.N + col) * a.groups + b] = c[r];
+                        if constexpr (kBias) {  // the biased form's arithmetic: t = s * P' rounded once, then fused
+                            const float t = sv4[ni] * static_cast<float>(c[r]);
+                            acc[mi][ni][r] = __builtin_fmaf(as4[mi][r], t, acc[mi][ni][r]);
+                            continue;
+                        }
                         const float scale = QM == QUANT_STATIC ? sv4[ni] : as4[mi][r] * sv4[ni];
                         acc[mi][ni][r] = __builtin_fmaf(scale, static_cast<float>(c[r]), acc[mi][ni][r]);
                     }
@@ -292,7 +329,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES / 2) void gemm_i4g_kernel(GArgs a
                 // Software pipeline: block blk's MFMA, then block blk - 1's epilogue. An int8 MFMA result needs 8
                 // wait states before a VALU reads it (what the compiler inserts for the builtin) and the hazard
                 // recognizer does not look into inline assembly, so the distances are kept here: from block 1 on
-                // the previous epilogue (12 VALU, 8 when calibrated, plus 2 wait states then) and the next block's
+                // the previous epilogue (12 VALU, 8 when calibrated or biased, plus 2 wait states then) and the next block's
                 // MFMA lie between an MFMA and its epilogue; block 0's epilogue and block 15's wait on s_nop.
                 v4i cp;
                 mfmas(0, cp);
@@ -301,7 +338,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES / 2) void gemm_i4g_kernel(GArgs a
                     v4i cn;
                     mfmas(blk, cn);
                     if (blk == 1) KQ_GASM("s_nop 7");
-                    else if (QM == QUANT_STATIC) KQ_GASM("s_nop 1");
+                    else if (QM == QUANT_STATIC || kBias) KQ_GASM("s_nop 1");
                     epilogue(blk - 1, cp);
                     cp = cn;
                 }
