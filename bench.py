@@ -164,9 +164,26 @@ def cpu_baseline(torch, values, scales, zp, x, g, budget_s):
             break
     per = el / n
     bytes_ = gemv_bytes(M_DEC, K_DEC, N_DEC, g)
+    # one thread as well, on a fifth of the budget (the scalar restatement's own rate)
+    n1 = 0
+    t1 = time.perf_counter()
+    while True:
+        kq_ref.packed_linear(xb, v, s, 4, g, zero_points=z, threads=1)
+        n1 += 1
+        el1 = time.perf_counter() - t1
+        if (el1 >= budget_s / 5 and n1 >= 2) or n1 >= 100000:
+            break
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
     return {"value": round(bytes_ / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{n} projections M=1 K={K_DEC} N={N_DEC} int4 g={g} asym (one weight, cache-warm), "
-                      f"{el:.1f} s, {per * 1e3:.2f} ms each, oracle/kq_ref.cpp with {threads} threads"}
+                      f"{el:.1f} s, {per * 1e3:.2f} ms each, oracle/kq_ref.cpp with {threads} threads",
+            "one_thread_value": round(bytes_ / (el1 / n1) / 1e9, 3), "cpu_model": model, "host_cores": cores,
+            "label": "build restatement of the reference CPU path (the reference's ynnpack path cannot be built)"}
 
 
 def main():
