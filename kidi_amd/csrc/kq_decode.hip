@@ -381,12 +381,26 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
             const QuantBlock qb = quant_block(QM, mx, mn, a.input_scale, true);
             std::uint32_t lo = 0, hi = 0;
             int total = 0;
+            if constexpr (QM == QUANT_DYN_SYM) {
+                // |x * inverse| <= 127 (1 + 2^-24) rounds to at most 127, so no clamp; adding 1.5 * 2^23 rounds the
+                // product to an integer (to nearest even, as rint) held in the low mantissa bits, whose low byte is
+                // the code in two's complement (inverse = 0 for an all-zero block gives code 0); v_perm gathers four
+                // codes, v_dot4 against 0x01010101 sums them
+                constexpr float kMagic = 12582912.F;
+                std::uint32_t u[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int c = quant_code(QM, v[i], qb, a.input_scale);
-                total += c;
-                if (i < 4) lo |= (static_cast<std::uint32_t>(c) & 0xFFu) << (8 * i);
-                else hi |= (static_cast<std::uint32_t>(c) & 0xFFu) << (8 * (i - 4));
+                for (int i = 0; i < 8; ++i) u[i] = __float_as_uint(v[i] * qb.inverse + kMagic);
+                lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(u[3], u[2], 0x0c0c0400u), __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u), 0x05040100u);
+                hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(u[7], u[6], 0x0c0c0400u), __builtin_amdgcn_perm(u[5], u[4], 0x0c0c0400u), 0x05040100u);
+                total = sdot4(static_cast<int>(hi), 0x01010101, sdot4(static_cast<int>(lo), 0x01010101, 0));
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int c = quant_code(QM, v[i], qb, a.input_scale);
+                    total += c;
+                    if (i < 4) lo |= (static_cast<std::uint32_t>(c) & 0xFFu) << (8 * i);
+                    else hi |= (static_cast<std::uint32_t>(c) & 0xFFu) << (8 * (i - 4));
+                }
             }
             *reinterpret_cast<uint2*>(codes + m * 512 + act_position(8 * lane)) = make_uint2(lo, hi);
             total = row_reduce<LGC>(total, [](int p, int q) { return p + q; });
