@@ -37,7 +37,6 @@ namespace {
 
 using namespace dev;
 
-constexpr std::uint32_t kOob = 0x80000000u;  // buffer offset past every resource: the load returns zeros
 constexpr int kRsrcWord3 = 0x00020000;       // raw (unformatted) buffer resource, gfx9-family word 3
 constexpr int kMaxRows = 8;  // rows of the widest variant (MR = 8: two MFMA row halves)
 

@@ -33,7 +33,7 @@ using namespace dev;
 typedef __attribute__((address_space(3))) void lds_void;
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kBN = 128, kBK = 128;  // output columns (8 row tiles), columns per step (one group)
+constexpr int kBK = 128;  // columns per step (one group); a workgroup's 128 output columns are 8 row tiles
 constexpr int kBBytes = 8 * 2 * 1024;   // unpacked weights per stage: [tile slot][64-column half][lane][16 B]
 constexpr int kQuantRows = 256;         // activation rows are padded to this for every tile shape
 
@@ -579,7 +579,6 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
     // permuted order (row 16 q + t of a 64-row block at 4 t + q)
     const std::uint32_t as_lane = lds0 + S::META_RING + S::AS_OFF + (wm * 64 + 4 * (4 * L + (lane & 3))) * 4;
     const v4i zero = {0, 0, 0, 0};
-    const v4f zerof = {0.F, 0.F, 0.F, 0.F};
 #define KQ_BSLOT(ni) (GELU ? ((ni) < 2 ? (ni) : 2 + (ni)) : (ni))
 
     // operand registers of one step, read in this order: svr[0..3], asr, A0, A1 | A2 | B0 | B1 | B2 | B3, A3
@@ -641,11 +640,12 @@ __global__ __launch_bounds__(GemmShape<WM>::THREADS) void gemm_i4_kernel(GemmArg
     // see the MFMA inside the assembly and would not separate the two by the 2 wait states such a read needs.
     v4i biasv = {0, 0, 0, 0};
     if constexpr (kBias) {
-        int b0, b1, b2, b3;
+        int b0 = 0, b1 = 0, b2 = 0, b3 = 0;  // (the host pass compiles the assembly out)
         KQ_ASM("v_mov_b32 %0, 0x4b400000\n\tv_mov_b32 %1, 0x4b400000\n\tv_mov_b32 %2, 0x4b400000\n\tv_mov_b32 %3, 0x4b400000"
                : "=v"(b0), "=v"(b1), "=v"(b2), "=v"(b3));
         biasv = v4i{b0, b1, b2, b3};
     }
+    (void)biasv;
     float nbv[4];
     // Block b: two int8 MFMAs give the exact partials P' of the step's group. The epilogue of block b, issued after
     // the MFMAs of block b + 1, forms k = a_s * s in the accumulator's lane layout (lane = column nn + 16 L,

@@ -218,11 +218,12 @@ __global__ __launch_bounds__(64 * WAVES, WAVES / 2) void gemm_i4g_kernel(GArgs a
     constexpr float kBiasF = 12582912.0F;
     v4i biasv = zero;
     if constexpr (kBias) {
-        int b0, b1, b2, b3;
+        int b0 = 0, b1 = 0, b2 = 0, b3 = 0;  // (the host pass compiles the assembly out)
         KQ_GASM("v_mov_b32 %0, 0x4b400000\n\tv_mov_b32 %1, 0x4b400000\n\tv_mov_b32 %2, 0x4b400000\n\tv_mov_b32 %3, 0x4b400000"
                 : "=v"(b0), "=v"(b1), "=v"(b2), "=v"(b3));
         biasv = v4i{b0, b1, b2, b3};
     }
+    (void)biasv;
 
     load(0);
     store(0);
@@ -252,6 +253,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES / 2) void gemm_i4g_kernel(GArgs a
                 const v4f sv4 = *reinterpret_cast<const v4f*>(ws + ((gi * 2 + wn) * 16 + nn) * 4);
                 v4f nb4 = zerof;
                 if constexpr (kBias) nb4 = sv4 * -kBiasF;
+                (void)nb4;
                 v4f as4[MI];  // activation scales of rows 16 mi + 4 L + r, r = 0..3 (the accumulator's rows)
 #pragma unroll
                 for (int mi = 0; mi < MI; ++mi) {
