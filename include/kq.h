@@ -179,7 +179,8 @@ kq_status kq_packed_linear_greedy(const kq_weight* weight, const kq_linear_args*
  * kq_weight_pack with memory = KQ_DEVICE): values U8 [rows, cols / (8 / bits)], scales F32 [rows, cols / g] and, when
  * asymmetric_clip and bits == 4, zeros F32 [rows, cols / g] (the additive zero (8 - zp) * scale; zeros may be NULL
  * otherwise). Symmetric: scale = max|w| / (2^(bits-1) - 1), codes rounded half away from zero; asymmetric 4-bit: the
- * 11-step MSE clip. Non-finite weights and a scale that underflows return KQ_INVALID_ARGUMENT. Synchronous. */
+ * 11-step MSE clip. Non-finite weights and a scale that underflows return KQ_INVALID_ARGUMENT. Synchronous; the
+ * error flag it reads back is per device, so concurrent calls on one device from several threads are not supported. */
 kq_status kq_quantize_weight(const void* weight, kq_dtype dtype, int64_t rows, int64_t cols, int32_t bits,
                              int32_t group_size, int32_t asymmetric_clip, uint8_t* values, float* scales, float* zeros,
                              void* stream);

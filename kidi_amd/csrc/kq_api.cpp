@@ -946,6 +946,12 @@ kq_status kq_quantize_weight(const void* weight, kq_dtype dtype, int64_t rows, i
         return fail(KQ_INVALID_ARGUMENT, "invalid packed weight dimensions, precision or group size");
     const bool asym = asymmetric_clip != 0 && bits == 4;
     if (!weight || !values || !scales || (asym && !zeros)) return fail(KQ_INVALID_ARGUMENT, "null weight or output");
+    const std::size_t elem = dtype == KQ_F32 ? 4 : 2;
+    if (reinterpret_cast<std::uintptr_t>(weight) % elem || reinterpret_cast<std::uintptr_t>(scales) % 4 ||
+        (asym && reinterpret_cast<std::uintptr_t>(zeros) % 4))
+        return fail(KQ_INVALID_ARGUMENT, "misaligned weight, scales or zeros");
+    if (rows * (cols / group_size) >= (std::int64_t{1} << 38))  // one thread per (row, group), 2^30 workgroups
+        return fail(KQ_UNSUPPORTED, "weight too large for one quantization launch");
     const hipStream_t st = static_cast<hipStream_t>(stream);
     void* flag = nullptr;
     if (kq_status s = device_scratch(g_pack_scratch, 256, &flag); s != KQ_OK) return s;
