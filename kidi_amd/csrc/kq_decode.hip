@@ -130,12 +130,13 @@ __device__ __forceinline__ float segment_sum_squares(const float (&v)[8]) {
 // MR: rows of the variant (4 or 8); WMAX: most waves per workgroup (4 for K <= 2048, 16 up to K = 8192), which
 // sets the register budget (512 / (WMAX / 4) VGPRs per lane)
 template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, int MR, int WMAX, bool GREEDY = false, bool NORM = false>
-__global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const std::uint8_t* ptiles, int pM, int pK,
-                                                           int pk_tiles, int pn_tiles, int ppairs, int ptotal, int px_f32,
-                                                           DecodeArgs a) {
-    // The leading scalar arguments duplicate fields of `a`: they are the ones the first loads need, and the build
-    // preloads them into SGPRs at wave launch (-amdgpu-kernarg-preload-count), so the activation and weight loads
-    // go out without waiting for a kernel-argument fetch.
+__global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const std::uint8_t* ptiles, const void* pscales,
+                                                           const void* paux, int pflags, int pK, int pn_tiles, int ppairs,
+                                                           int ptotal, DecodeArgs a) {
+    // The leading scalar arguments duplicate fields of `a`: they are the ones the first loads need (activations,
+    // weight tiles and their group metadata; pflags = M | x_f32 << 8 | scale_half << 9 | aux_half << 10), and the
+    // build preloads them into SGPRs at wave launch (-amdgpu-kernarg-preload-count), so every load of the first unit
+    // goes out without waiting for a kernel-argument fetch. The tile and group counts follow from K (K % 512 = 0).
     constexpr int H = MR / 4;            // MFMA row halves: rows 4 h .. 4 h + 3
     constexpr int RT = (WMAX > 4 && !GELU) ? 1 : 2;  // row tiles per unit: one when K > 2048 (more workgroups)
     constexpr int KT = 512 / BITS;       // columns per weight tile
@@ -151,7 +152,8 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int W = blockDim.x >> 6;
     const int nn = lane & 15, L = lane >> 4;
-    const int M = pM, K = pK, k_tiles = pk_tiles, n_tiles = pn_tiles, x_f32 = px_f32;
+    const int M = pflags & 0xFF, K = pK, k_tiles = K / (512 / BITS), n_tiles = pn_tiles, x_f32 = (pflags >> 8) & 1;
+    const int scale_half = (pflags >> 9) & 1, aux_half = (pflags >> 10) & 1, groups_p = K / G;
     const int aslot = nn >> 2;  // A-operand row of this lane: activation row (nn & 3) + 4 h, group slot
 
     // row tiles of a unit: plain 2 p, 2 p + 1 (or the single tile p when RT = 1); GELU the gate tile p and its up
@@ -229,33 +231,33 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
     std::uint32_t s_raw[RT][NQ], x_raw[RT][NQ];
     uint4 wv[RT][NT];
     auto load_meta = [&](auto later_unit) {
-        const std::uint32_t meta_n = static_cast<std::uint32_t>(n_tiles * a.groups_p * kTileRows);
-        const __amdgpu_buffer_rsrc_t sres = rsrc(a.scales, meta_n * (a.scale_half ? 2 : 4));
+        const std::uint32_t meta_n = static_cast<std::uint32_t>(n_tiles * groups_p * kTileRows);
+        const __amdgpu_buffer_rsrc_t sres = rsrc(pscales, meta_n * (scale_half ? 2 : 4));
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
             const int nt = (r == 0 || !live1) ? nts[0] : nts[1];
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
-                const std::uint32_t mi = static_cast<std::uint32_t>((nt * a.groups_p + wave * NG + 4 * q + L) * kTileRows + nn);
+                const std::uint32_t mi = static_cast<std::uint32_t>((nt * groups_p + wave * NG + 4 * q + L) * kTileRows + nn);
                 if constexpr (!decltype(later_unit)::value) {
                     // one dword load whatever the element width, so no branch join (where the wait counters are
                     // merged conservatively) waits for loads issued before; an F16 entry is the half of its
                     // aligned dword selected by mi & 1 (meta_n is even, so in bounds)
-                    const std::uint32_t sw = __builtin_amdgcn_raw_buffer_load_b32(sres, a.scale_half ? (2 * mi) & ~3u : 4 * mi, 0, 0);
-                    s_raw[r][q] = a.scale_half ? (sw >> (16 * (mi & 1))) & 0xFFFFu : sw;
+                    const std::uint32_t sw = __builtin_amdgcn_raw_buffer_load_b32(sres, scale_half ? (2 * mi) & ~3u : 4 * mi, 0, 0);
+                    s_raw[r][q] = scale_half ? (sw >> (16 * (mi & 1))) & 0xFFFFu : sw;
                 } else {  // units after a workgroup's first: the element-width loads (measured faster for the head)
-                    s_raw[r][q] = a.scale_half ? __builtin_amdgcn_raw_buffer_load_b16(sres, 2 * mi, 0, 0)
+                    s_raw[r][q] = scale_half ? __builtin_amdgcn_raw_buffer_load_b16(sres, 2 * mi, 0, 0)
                                                : __builtin_amdgcn_raw_buffer_load_b32(sres, 4 * mi, 0, 0);
                 }
                 x_raw[r][q] = 0;
                 if constexpr (BITS == 8 && QM == QUANT_DYN_ASYM)
-                    x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b32(rsrc(a.aux, meta_n * 4), 4 * mi, 0, 0);
+                    x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b32(rsrc(paux, meta_n * 4), 4 * mi, 0, 0);
                 if constexpr (BITS != 8 && ZM == ZERO_POINT)
-                    x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b8(rsrc(a.aux, meta_n / 2), (mi - nn) / 2 + nn / 2, 0, 0);
+                    x_raw[r][q] = __builtin_amdgcn_raw_buffer_load_b8(rsrc(paux, meta_n / 2), (mi - nn) / 2 + nn / 2, 0, 0);
                 if constexpr (BITS != 8 && ZM == ZERO_FLOAT) {
-                    const std::uint32_t zw = __builtin_amdgcn_raw_buffer_load_b32(rsrc(a.aux, meta_n * (a.aux_half ? 2 : 4)),
-                                                                                  a.aux_half ? (2 * mi) & ~3u : 4 * mi, 0, 0);
-                    x_raw[r][q] = a.aux_half ? (zw >> (16 * (mi & 1))) & 0xFFFFu : zw;
+                    const std::uint32_t zw = __builtin_amdgcn_raw_buffer_load_b32(rsrc(paux, meta_n * (aux_half ? 2 : 4)),
+                                                                                  aux_half ? (2 * mi) & ~3u : 4 * mi, 0, 0);
+                    x_raw[r][q] = aux_half ? (zw >> (16 * (mi & 1))) & 0xFFFFu : zw;
                 }
             }
         }
@@ -452,12 +454,12 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
         const int gi = 4 * q + L;  // this lane's group (of the wave) and the stats slot of row i
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
-            const float s = a.scale_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(s_raw[r][q]))) : __uint_as_float(s_raw[r][q]);
+            const float s = scale_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(s_raw[r][q]))) : __uint_as_float(s_raw[r][q]);
             int x2 = 0;
             if constexpr (BITS == 8 && QM == QUANT_DYN_ASYM) x2 = static_cast<int>(x_raw[r][q]);
             if constexpr (BITS != 8 && ZM == ZERO_POINT) x2 = static_cast<int>((x_raw[r][q] >> (4 * (nn & 1))) & 15u);
             if constexpr (BITS != 8 && ZM == ZERO_FLOAT)
-                x2 = __float_as_int(a.aux_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(x_raw[r][q]))) : __uint_as_float(x_raw[r][q]));
+                x2 = __float_as_int(aux_half ? __half2float(__ushort_as_half(static_cast<unsigned short>(x_raw[r][q]))) : __uint_as_float(x_raw[r][q]));
             const int n = (r == 0 ? nts[0] : nts[1]) * kTileRows + nn;
 #pragma unroll
             for (int i = 0; i < MR; ++i) {
@@ -595,7 +597,9 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
     }
 }
 
-#define KQ_DECODE_ARGS(a) (a).x, (a).tiles, (a).M, (a).K, (a).k_tiles, (a).n_tiles, (a).pairs, (a).total_pairs, (a).x_f32, (a)
+#define KQ_DECODE_ARGS(a)                                                                                             \
+    (a).x, (a).tiles, (a).scales, (a).aux, (a).M | ((a).x_f32 << 8) | ((a).scale_half << 9) | ((a).aux_half << 10), (a).K, \
+        (a).n_tiles, (a).pairs, (a).total_pairs, (a)
 
 template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, bool GREEDY = false>
 hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds, hipStream_t stream) {
