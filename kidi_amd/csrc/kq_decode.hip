@@ -722,10 +722,14 @@ hipError_t launch_decode(const LinearCall& c, hipStream_t stream) {
     // register budget (K > 2048, i.e. more than 4 waves, and every debug variant) without gating
     const bool dbg_any = c.dump || c.dq_codes || c.dq_scales || c.dq_sums || c.dq_zeros;
     // Single-tile units also when pairs would leave CUs idle (fewer than 256 workgroups: e.g. a fused QKV of 2560 rows
-    // makes 80 pairs) or an 8-bit pair is heavy (a wave would stream 16 KB); measured on MI355X: fused QKV 4.41 -> 3.78
-    // us, 8-bit 8192 x 2048 6.39 -> 5.94 us, while 4-bit 8192 x 2048 and the 262,144-row head stay faster in pairs.
+    // makes 80 pairs), an 8-bit pair is heavy (a wave would stream 16 KB) or one row meets at most 1024 row tiles: two
+    // waves per SIMD then share the work left after the last weight byte arrives. Measured on MI355X: fused QKV 4.41
+    // -> 3.78 us, 8-bit 8192 x 2048 6.39 -> 5.94 us, 4-bit 8192 x 2048 at M = 1 4.31 -> 4.11 us (symmetric g = 32 4.92
+    // -> 4.49 us); with four rows the duplicated activation quantization makes pairs faster (4.95 against 5.39 us),
+    // and the 262,144-row head stays faster in pairs.
     const std::int64_t nt = w.geo.n_tiles;
-    const bool prefer_single = !c.norm && !c.greedy && ((nt + 1) / 2 < 256 || (w.geo.bits == 8 && nt <= 512));
+    const bool prefer_single = !c.norm && !c.greedy &&
+                               ((nt + 1) / 2 < 256 || (w.geo.bits == 8 && nt <= 512) || (c.M == 1 && nt <= 1024));
     const bool single = (W > 4 || dbg_any || prefer_single) && !c.gelu_gate;
     a.single_units = single && W <= 4 && !dbg_any;
     a.total_pairs = static_cast<int>(c.gelu_gate ? w.geo.n_tiles / 2 : (single ? w.geo.n_tiles : (w.geo.n_tiles + 1) / 2));
