@@ -1,0 +1,50 @@
+"""Measurement instrumentation of the C ABI: kq_debug_read_floor (the single-launch read floor bench.py reports beside
+the decode roofline) rejects bad arguments on the host and, on the GPU, reads a buffer without writing anything
+but its sink (which it touches only when the data XOR to a magic value)."""
+
+import ctypes
+
+import pytest
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def native():
+    from kidi_amd import _native
+
+    _native.load()
+    return _native
+
+
+@pytest.mark.parametrize("bad", ["null", "zero", "ragged", "huge"])
+def test_read_floor_rejects_invalid(native, bad):
+    lib = native.load()
+    data, size, sink = ctypes.c_void_p(256), 4096, ctypes.c_void_p(512)
+    if bad == "null":
+        data = None
+    elif bad == "zero":
+        size = 0
+    elif bad == "ragged":
+        size = 4100
+    elif bad == "huge":
+        size = (1 << 31) + 16
+    assert lib.kq_debug_read_floor(data, size, sink, None) == native.KQ_INVALID_ARGUMENT
+    assert lib.kq_last_error()
+
+
+@pytest.mark.gpu
+def test_read_floor_reads_without_writing():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from kidi_amd import _native
+
+    lib = _native.load()
+    dev = torch.device("cuda:0")
+    for size in (16, 4096, 8753152 + 16 * 7, 64 << 20):
+        buf = torch.zeros((size,), dtype=torch.uint8, device=dev)
+        sink = torch.full((1,), -7, dtype=torch.int32, device=dev)
+        assert lib.kq_debug_read_floor(buf.data_ptr(), size, sink.data_ptr(), None) == _native.KQ_OK
+        torch.cuda.synchronize()
+        assert int(sink.item()) == -7
+        assert int(buf.sum().item()) == 0
