@@ -396,3 +396,32 @@ def test_fused_qkv_prefill_rows(dev, ref):
     y_ref, path = ref.packed_linear(xb, values, scales, 4, g, x_bf16=True, threads=8)
     assert path == ref.PATH_BLOCKWISE
     check_close(y[torch.from_numpy(rows).to(dev)], y_ref)
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("scale_kind", ["f32", "f16_extreme"])
+def test_prefill_scale_forms(dev, ref, group, scale_kind):
+    """Prefill GEMMs (g = 128 and g = 32 / 64 kernels) with F32 weight scales (the conversion epilogue) and with F16
+    scales spanning subnormals to large values (the biased-accumulator epilogue, exact t = s * P' for any F16 s):
+    int32 partials bit-exact, outputs within tolerance of the oracle."""
+    rng = np.random.default_rng(500 + group)
+    M, K, N = 40, 512, 256
+    if scale_kind == "f32":
+        values, scales, zp, codes = weights(rng, N, K, 4, group, zero_points=True, scale_dtype=np.float32)
+    else:
+        values, scales, zp, codes = weights(rng, N, K, 4, group, zero_points=True)
+        mags = rng.choice(np.array([6.0e-8, 3.0e-5, 0.01, 1.0, 250.0, 6.0e4], np.float32), size=scales.shape)
+        scales = (mags * rng.uniform(0.5, 1.0, scales.shape).astype(np.float32)).astype(np.float16)
+    x = activations(rng, M, K, 0.001)
+    y_ref, path = ref.packed_linear(x, values, scales, 4, group, zero_points=zp)
+    assert path == ref.PATH_BLOCKWISE
+    dw = device_weight(values, scales, 4, group, dev, zero_points=zp)
+    y_d, P_d = dw.debug_partials(to_dev(x, dev))
+    q, _, _, _ = ref.quantize_dynamic(x, group, 4)
+    np.testing.assert_array_equal(P_d.cpu().numpy().astype(np.int64),
+                                  expected_partials(ref, q, codes, None, 4, group, zero_points=zp))
+    check_close(y_d, y_ref)
+    y = dw.linear(to_dev(x, dev))
+    torch.cuda.synchronize()
+    check_close(y, y_ref)
+    np.testing.assert_array_equal(y.cpu().numpy(), y_d.cpu().numpy())  # the dump variant computes the same y
