@@ -425,3 +425,25 @@ def test_prefill_scale_forms(dev, ref, group, scale_kind):
     torch.cuda.synchronize()
     check_close(y, y_ref)
     np.testing.assert_array_equal(y.cpu().numpy(), y_d.cpu().numpy())  # the dump variant computes the same y
+
+
+@pytest.mark.parametrize("N", [16 * 511, 16 * 512, 16 * 1024, 16 * 1025 - 8])
+@pytest.mark.parametrize("bits,group,zeros", [(4, 32, None), (4, 64, "zp"), (4, 128, "zp"), (8, 32, None)])
+def test_decode_unit_plan_boundaries(dev, ref, N, bits, group, zeros):
+    """M = 1 around the launch plan's boundaries (single row-tile units up to 1024 row tiles, pairs above; ragged
+    last tile): int32 partials bit-exact, outputs within tolerance."""
+    rng = np.random.default_rng(N + bits * 7 + group)
+    M, K = 1, 512
+    values, scales, zp, codes = weights(rng, N, K, bits, group, zero_points=zeros == "zp")
+    x = activations(rng, M, K, 0.001)
+    y_ref, path = ref.packed_linear(x, values, scales, bits, group, zero_points=zp)
+    assert path == ref.PATH_BLOCKWISE
+    dw = device_weight(values, scales, bits, group, dev, zero_points=zp)
+    y_d, P_d = dw.debug_partials(to_dev(x, dev))
+    q, _, _, zpa = ref.quantize_dynamic(x, group, bits)
+    np.testing.assert_array_equal(P_d.cpu().numpy().astype(np.int64),
+                                  expected_partials(ref, q, codes, zpa, bits, group, zero_points=zp))
+    check_close(y_d, y_ref)
+    y = dw.linear(to_dev(x, dev))
+    torch.cuda.synchronize()
+    check_close(y, y_ref)
