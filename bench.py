@@ -113,6 +113,36 @@ def capture(torch, calls, stream_ptr_fn):
     return g
 
 
+class Quiet:
+    """Puts the device in a known state before a timed region: one launch that reads a 1 GiB buffer
+    (kq_debug_read_floor: reads only, so no dirty lines are left to write back) evicts every weight of the timed steps
+    from the 256 MB Infinity Cache, and its ~0.2 ms of device time lets the host enqueue the timed region behind it.
+    Host submission latency therefore falls before the start event, and the events bracket device work only."""
+
+    def __init__(self, torch, dev, lib):
+        self.torch, self.lib = torch, lib
+        self.buf = torch.ones((1 << 30,), dtype=torch.uint8, device=dev)
+        self.sink = torch.zeros((1,), dtype=torch.int32, device=dev)
+
+    def __call__(self):
+        _ok(self.lib, self.lib.kq_debug_read_floor(self.buf.data_ptr(), self.buf.numel(), self.sink.data_ptr(),
+                                                   self.torch.cuda.current_stream().cuda_stream))
+
+
+def timed(torch, quiet, enqueue):
+    """Device milliseconds of the work `enqueue()` issues on the current stream, measured with HIP events that are
+    queued behind `quiet` (a read of a buffer four times the Infinity Cache), so the interval holds device work only."""
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    quiet()
+    e0.record(stream)
+    enqueue()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
+
+
 def run_steps(torch, projs, start, count, graph_full, graph_rem_fn, stream_ptr_fn):
     """Run `count` projections starting at rotation index `start` (a multiple of len(projs)): whole rotations as
     graph replays, the remainder as one graph of the first count % R projections."""
@@ -252,17 +282,14 @@ def main():
     torch.cuda.synchronize()
     parity = check_decode_parity(torch, projs[0], *first, x, G_DEC)
 
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    quiet = Quiet(torch, dev, lib)
     t0 = time.perf_counter()
-    e0.record(stream)
-    run_steps(torch, projs, 0, args.steps, graph_full, graph_rem, stream_ptr)
-    e1.record(stream)
-    torch.cuda.synchronize()
+    dev_ms = timed(torch, quiet, lambda: run_steps(torch, projs, 0, args.steps, graph_full, graph_rem, stream_ptr))
     wall = time.perf_counter() - t0
-    dev_ms = e0.elapsed_time(e1)
     ms_per_step = dev_ms / args.steps
+    # repeatability: the same timed region four more times (median reported beside the first run)
+    reps_ms = [dev_ms] + [timed(torch, quiet, lambda: run_steps(torch, projs, 0, args.steps, graph_full, graph_rem,
+                                                                 stream_ptr)) for _ in range(4)]
     bytes_step = gemv_bytes(M_DEC, K_DEC, N_DEC, G_DEC)
     value = bytes_step / (ms_per_step * 1e-3) / 1e9
     # The decode step is one kernel launch (kq_packed_linear -> decode_kernel: activation quantization fused), so
@@ -281,12 +308,8 @@ def main():
     g1 = capture(torch, [projs[0]] * 64, stream_ptr)
     g1.replay()
     torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(20):
-        g1.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    mall_ms = e0.elapsed_time(e1) / (20 * 64)
+    g1.replay()  # the one weight back in cache after the flush that precedes the timed region
+    mall_ms = timed(torch, lambda: (quiet(), g1.replay()), lambda: [g1.replay() for _ in range(20)]) / (20 * 64)
     del g1
 
     # Read floor of one launch at this size: kq_debug_read_floor only reads the same number of bytes once (launch
@@ -304,12 +327,7 @@ def main():
     for _ in range(3):
         gr.replay()
     torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(20):
-        gr.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    floor_us = e0.elapsed_time(e1) * 1e3 / (20 * R)
+    floor_us = timed(torch, quiet, lambda: [gr.replay() for _ in range(20)]) * 1e3 / (20 * R)
     del gr, bufs, floor_calls
 
     del graph_full, rem_graphs
@@ -335,12 +353,7 @@ def main():
         gp.replay()
     torch.cuda.synchronize()
     replays = max(1, -(-args.prefill_steps // per_graph))
-    e0.record(stream)
-    for _ in range(replays):
-        gp.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    pre_ms = e0.elapsed_time(e1) / (replays * per_graph)
+    pre_ms = timed(torch, quiet, lambda: [gp.replay() for _ in range(replays)]) / (replays * per_graph)
     pre_tops = 2.0 * M_PRE * N_PRE * K_PRE / (pre_ms * 1e-3) / 1e12
     # prefill parity on a sample of rows
     import numpy as np
@@ -360,7 +373,7 @@ def main():
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(torch, *first_cpu, x_cpu, G_DEC, args.cpu_seconds)
 
-    extras = None if args.no_extras else bench_extras(torch, N_, lib, dev, gen)
+    extras = None if args.no_extras else bench_extras(torch, N_, lib, dev, gen, quiet)
 
     out = {
         "metric": "int4 GEMV GB/s (% HBM peak) at M=1; prefill GEMM TOPS (% MFMA peak)",
@@ -376,10 +389,14 @@ def main():
         "dtype": "int8",
         "data": "synthetic (seeded uniform int4 codes, fp16 scales, uint4 zero points; bf16 N(0,1) x, 0.1% x20)",
         "config": {"workload": "decode GEMV, asymmetric int4 g=128, M=1, K=2048, N=8192 (configs[1] up-proj)",
-                   "rotated_weights": R, "weight_working_set_MB": round(R * projs_bytes(N_DEC, K_DEC, G_DEC) / 1e6, 1),
-                   "launch": "HIP graph replay, one stream"},
+                   "rotated_weights": R,
+                   "distinct_weights_timed": min(R, args.steps),
+                   "weight_working_set_MB": round(min(R, args.steps) * projs_bytes(N_DEC, K_DEC, G_DEC) / 1e6, 1),
+                   "launch": "HIP graph replay, one stream, queued behind a 1 GiB read that evicts the Infinity Cache"},
         "roofline": roofline,
         "wall_s": round(wall, 4),
+        "ms_per_step_repeats": [round(v / args.steps, 6) for v in reps_ms],
+        "ms_per_step_median": round(sorted(reps_ms)[len(reps_ms) // 2] / args.steps, 6),
         "parity": parity,
         "mall_resident_gbs": round(bytes_step / (mall_ms * 1e-3) / 1e9, 1),
         "read_floor": {"us_per_launch": round(floor_us, 3), "gbs": round(bytes_step / (floor_us * 1e-6) / 1e9, 1),
@@ -407,8 +424,8 @@ def layer_bytes(M, K, N, g, bits, asym, out_cols=None):
 
 
 class Extras:
-    def __init__(self, torch, N_, lib, dev, gen):
-        self.torch, self.N_, self.lib, self.dev, self.gen = torch, N_, lib, dev, gen
+    def __init__(self, torch, N_, lib, dev, gen, quiet):
+        self.torch, self.N_, self.lib, self.dev, self.gen, self.quiet = torch, N_, lib, dev, gen, quiet
         self.stream_ptr = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
 
     def weight(self, N, K, bits, g, asym, code_bytes=None):
@@ -453,14 +470,7 @@ class Extras:
         g = capture(t, calls, self.stream_ptr)
         g.replay()
         t.cuda.synchronize()
-        stream = t.cuda.current_stream()
-        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            g.replay()
-        e1.record(stream)
-        t.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (reps * len(calls))
+        return timed(t, self.quiet, lambda: [g.replay() for _ in range(reps)]) * 1e3 / (reps * len(calls))
 
     def linear_calls(self, dws, x, M, out_cols, fn="kq_packed_linear", input_scale=0.0):
         """Calls of `fn` over `dws`, plus `keep`: every tensor and argument block the calls point into. The caller
@@ -483,8 +493,8 @@ def _ok(lib, status):
         raise RuntimeError(lib.kq_last_error().decode())
 
 
-def bench_extras(torch, N_, lib, dev, gen):
-    E = Extras(torch, N_, lib, dev, gen)
+def bench_extras(torch, N_, lib, dev, gen, quiet):
+    E = Extras(torch, N_, lib, dev, gen, quiet)
     out = {}
     # configs[0] (symmetric g = 32 up projection) on the GPU, configs[1]'s other decode shapes (M = 4; the down
     # projection K = 8192, N = 2048 at M = 1 and 4) and configs[2]'s M = 512 prefill

@@ -84,8 +84,9 @@ int32_t kq_version(void);
 const char* kq_arch(void);
 
 /* Load-time packing: validate (Context::Impl::run PACKED_LINEAR checks, ops/context.cpp:207-218), re-lay out
- * into the gfx950 tile format on the host and upload to the current device. Synchronous. The source buffers are
- * not retained. Replaces BlockwiseLinear::pack_tiles / SymmetricPackedLinear::pack_tiles
+ * into the gfx950 tile format on the host and upload to the current device. Synchronous: device sources are read in
+ * `stream` order, and a stream under graph capture is refused (KQ_RUNTIME). The source buffers are not retained.
+ * Replaces BlockwiseLinear::pack_tiles / SymmetricPackedLinear::pack_tiles
  * (runtime/ynn/operators.cpp:1061-1089, :1206-1231). */
 kq_status kq_weight_pack(const kq_pack_desc* desc, void* stream, kq_weight** out);
 
@@ -109,7 +110,8 @@ typedef struct kq_linear_args {
     float output_scale;     /* bit_cast of attributes[2]: > 0 rounds y to int8 steps of this size */
     float* y;               /* device [M, N] F32 */
     void* workspace;        /* device scratch of kq_linear_workspace_size() bytes, or NULL to use a grow-only
-                               per-device buffer owned by the library */
+                               buffer the library keeps per (device, stream); it cannot grow while the stream is
+                               being captured (KQ_RUNTIME), so captured calls pass a workspace */
     size_t workspace_bytes;
 } kq_linear_args;
 
@@ -131,6 +133,17 @@ kq_status kq_weight_pack_concat(const kq_pack_desc* descs, int32_t count, void* 
  * gate_up_proj, model/gemma4.cpp:308-316); y [M, I] = gelu_tanh(x W_gate^T) * (x W_up^T)
  * (Context::gelu_gate, ops/context.cpp:957-963; formula eager_test.cpp:444-452). */
 kq_status kq_packed_linear_gelu_gate(const kq_weight* weight, const kq_linear_args* args, void* stream);
+
+/* Kidi's LOWBIT_PARITY projection: runtime::parity::packed_linear (src/kidi/runtime/parity_math.cpp:226-291), which
+ * Context::packed_linear runs instead of PACKED_LINEAR under InferencePrecision::LOWBIT_PARITY (ops/context.cpp:917-932).
+ * Activations rounded to the calibration grid, clamp(nearbyint(x / input_scale), -128, 127) * input_scale; weights
+ * dequantized to c * s (zeros bound to the weight are not applied, as in the reference); each output one fused
+ * multiply-add per column in column order; the result rounded to the output_scale grid. Outside the reference's domain
+ * (x not F32, input_scale or output_scale not > 0, F16 scales, dimensions above INT32_MAX) it returns KQ_UNSUPPORTED
+ * with the reference's message, and KQ_INVALID_ARGUMENT when a scale is not finite and positive. The serial form is
+ * the reference's for M < 8; for M >= 8 the reference sums with Accelerate's sgemm (its order is not reproduced).
+ * Asynchronous on `stream`; no workspace. */
+kq_status kq_lowbit_parity_linear(const kq_weight* weight, const kq_linear_args* args, void* stream);
 
 /* Gated feed-forward of one decoder layer: Context::gated_feed_forward (src/kidi/ops/context.cpp:970-996) ->
  * Operation::GATED_FEED_FORWARD, run by PackedFeedForward (runtime/ynn/operators.cpp:1321-1517) for calibrated
@@ -179,8 +192,9 @@ kq_status kq_packed_linear_greedy(const kq_weight* weight, const kq_linear_args*
  * kq_weight_pack with memory = KQ_DEVICE): values U8 [rows, cols / (8 / bits)], scales F32 [rows, cols / g] and, when
  * asymmetric_clip and bits == 4, zeros F32 [rows, cols / g] (the additive zero (8 - zp) * scale; zeros may be NULL
  * otherwise). Symmetric: scale = max|w| / (2^(bits-1) - 1), codes rounded half away from zero; asymmetric 4-bit: the
- * 11-step MSE clip. Non-finite weights and a scale that underflows return KQ_INVALID_ARGUMENT. Synchronous; the
- * error flag it reads back is per device, so concurrent calls on one device from several threads are not supported. */
+ * 11-step MSE clip. Non-finite weights and a scale that underflows return KQ_INVALID_ARGUMENT. Synchronous (a stream
+ * under graph capture is refused); the error flag it reads back is per (device, stream), so concurrent calls on one
+ * stream from several threads are not supported. */
 kq_status kq_quantize_weight(const void* weight, kq_dtype dtype, int64_t rows, int64_t cols, int32_t bits,
                              int32_t group_size, int32_t asymmetric_clip, uint8_t* values, float* scales, float* zeros,
                              void* stream);
@@ -234,7 +248,9 @@ kq_status kq_packed_linear_rms(const kq_weight* weight, const kq_linear_args* ar
 /* Persisted gfx950 layout, the role of Kidi's packed-operator cache (runtime/ynn/feed_forward_cache.h:11-38,
  * feed_forward_cache.cpp): a packed weight as one host blob (header + the device image) and back, so a later load
  * skips validation and re-layout. The blob holds the layout version and the weight's geometry; kq_weight_import
- * rejects a blob of another version or a malformed one with KQ_INVALID_MANIFEST. Both calls are synchronous. */
+ * rejects with KQ_INVALID_MANIFEST, before any device call, a blob of another version, of the wrong size, or whose
+ * header (shape, modes, offsets, image size) differs from the image this library builds for that geometry and those
+ * modes. Both calls are synchronous and refuse a stream under graph capture. */
 size_t kq_weight_export_size(const kq_weight* weight);
 kq_status kq_weight_export(const kq_weight* weight, void* host, size_t bytes, void* stream);
 kq_status kq_weight_import(const void* host, size_t bytes, void* stream, kq_weight** out);
@@ -251,6 +267,16 @@ kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_d
  * per-group partials [M, N, K/g]: sum over the group of x_code * w_code, where w_code = c (symmetric), u - zp
  * (ZP_U8 zero-points, u = c + 8) or c (additive float zeros), and x_code = q - zp_a for 8-bit dynamic. */
 kq_status kq_debug_partials(const kq_weight* weight, const kq_linear_args* args, int32_t* partials, void* stream);
+
+/* The kernel sequence a projection call takes, without running it (no counterpart in the reference; for tests that
+ * assert which kernels they cover): 0 none (M = 0), 1 decode_kernel, 2 skinny_kernel, 3 quantize_rows_kernel +
+ * gemm_i4_kernel, 4 quantize_rows_g_kernel + gemm_i4g_kernel, 5 quantize_kernel + gemv_kernel, 6 quantize_kernel +
+ * gemm_kernel, 7 quantize_rowmajor_kernel + rowmajor_kernel, 8 portable_kernel; -1 for invalid arguments.
+ * kq_debug_route_shape answers for a weight described by its geometry and modes (zero_mode: 0 none, 1 ZP_U8 zero
+ * points or additive zeros equal to (8 - zp) * scale, 2 other additive zeros) and touches no device. */
+int32_t kq_debug_route(const kq_weight* weight, const kq_linear_args* args, int32_t gelu_gate);
+int32_t kq_debug_route_shape(int32_t bits, int32_t group_size, int64_t rows, int64_t cols, int32_t zero_mode,
+                             int32_t scale_f16, int64_t m, kq_dtype x_dtype, float input_scale, int32_t gelu_gate);
 
 /* ---- measurement instrumentation (no counterpart in the reference) ----------------------------------------- */
 

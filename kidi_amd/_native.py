@@ -27,8 +27,15 @@ EXPORTS = (
     "kq_layout_encode_host", "kq_layout_decode_host", "kq_ffn_workspace_size", "kq_gated_feed_forward",
     "kq_greedy_workspace_size", "kq_greedy_token", "kq_greedy_linear_workspace_size", "kq_packed_linear_greedy",
     "kq_weight_export_size", "kq_weight_export", "kq_weight_import", "kq_rms_norm", "kq_rms_linear_workspace_size",
-    "kq_packed_linear_rms", "kq_quantize_weight", "kq_debug_read_floor",
+    "kq_packed_linear_rms", "kq_quantize_weight", "kq_debug_read_floor", "kq_debug_route", "kq_debug_route_shape",
+    "kq_lowbit_parity_linear",
 )
+
+# kq_debug_route values: the kernel sequence a projection call runs
+ROUTE_NONE, ROUTE_DECODE, ROUTE_SKINNY, ROUTE_GEMM_I4, ROUTE_GEMM_I4G, ROUTE_GEMV, ROUTE_GEMM, ROUTE_ROWMAJOR, \
+    ROUTE_PORTABLE = range(9)
+ROUTE_NAMES = ("none", "decode_kernel", "skinny_kernel", "gemm_i4_kernel", "gemm_i4g_kernel", "gemv_kernel",
+               "gemm_kernel", "rowmajor_kernel", "portable_kernel")
 
 
 class PackDesc(ctypes.Structure):
@@ -170,6 +177,12 @@ def load() -> ctypes.CDLL:
     L.kq_quantize_weight.restype = ctypes.c_int
     L.kq_debug_read_floor.argtypes = [vp, ctypes.c_size_t, vp, vp]
     L.kq_debug_read_floor.restype = ctypes.c_int
+    L.kq_lowbit_parity_linear.argtypes = [vp, ctypes.POINTER(LinearArgs), vp]
+    L.kq_lowbit_parity_linear.restype = ctypes.c_int
+    L.kq_debug_route.argtypes = [vp, ctypes.POINTER(LinearArgs), i32]
+    L.kq_debug_route.restype = i32
+    L.kq_debug_route_shape.argtypes = [i32, i32, i64, i64, i32, i32, i64, ctypes.c_int, f32, i32]
+    L.kq_debug_route_shape.restype = i32
     L.kq_debug_quantize.argtypes = [vp, vp, ctypes.c_int, i64, f32, vp, vp, vp, vp, vp]
     L.kq_debug_quantize.restype = ctypes.c_int
     L.kq_debug_partials.argtypes = [vp, ctypes.POINTER(LinearArgs), vp, vp]

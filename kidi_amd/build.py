@@ -25,18 +25,28 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, incremental: bool = False) -> str:
+    """Compile every source and link lib/libkq_hip.so. With incremental=True, objects kept in lib/obj/ from an
+    earlier incremental build are reused when they are newer than their source and every header."""
     os.makedirs(os.path.dirname(LIB), exist_ok=True)
+    objdir = os.path.join(HERE, "lib", "obj") if incremental else os.path.join(HERE, "lib")
+    os.makedirs(objdir, exist_ok=True)
+    headers = [os.path.join(HERE, "csrc", f) for f in os.listdir(os.path.join(HERE, "csrc")) if f.endswith(".hpp")]
+    headers.append(os.path.join(ROOT, "include", "kq.h"))
+    newest_header = max(os.path.getmtime(h) for h in headers)
     objs = []
     procs = []
     for src in SOURCES:
-        obj = os.path.join(HERE, "lib", os.path.basename(src) + ".o")
+        obj = os.path.join(objdir, os.path.basename(src) + ".o")
+        objs.append(obj)
+        if incremental and os.path.exists(obj) and os.path.getmtime(obj) > max(
+                newest_header, os.path.getmtime(os.path.join(HERE, src))):
+            continue
         cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-I", os.path.join(ROOT, "include"), "-c", os.path.join(HERE, src),
                "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT), src))
-        objs.append(obj)
     for p, src in procs:
         out, _ = p.communicate()
         text = "\n".join(l for l in out.decode(errors="replace").splitlines() if "packed-fp32-ops" not in l)
@@ -46,10 +56,13 @@ def build(verbose: bool = False) -> str:
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
-    for o in objs:
-        os.remove(o)
+    if not incremental:
+        for o in objs:
+            os.remove(o)
     return LIB
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    import sys
+
+    print(build(verbose=True, incremental="--incremental" in sys.argv))

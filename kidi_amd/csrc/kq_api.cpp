@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -86,36 +87,42 @@ std::int64_t act_rows(const kq::Weight& w, std::int64_t M) {
 constexpr std::size_t kAlign = 256;
 std::size_t align_up(std::size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-// Grow-only per-device scratch used when the caller passes no workspace.
+// Grow-only scratch used when the caller passes no workspace, one per (device, stream): calls on one stream are
+// ordered, so reusing that stream's buffer needs no synchronization, and calls on different streams never share
+// one. Growing allocates a larger buffer and keeps the old one until the process ends (queued work may still read
+// it), so no call waits for the device; growth is refused while the stream is being captured into a graph.
 struct Scratch {
     void* ptr = nullptr;
     std::size_t bytes = 0;
 };
 std::mutex g_scratch_mutex;
-std::map<int, Scratch> g_scratch;
-std::map<int, Scratch> g_gelu_scratch;
-std::map<int, Scratch> g_ffn_scratch;
-std::map<int, Scratch> g_greedy_scratch;
-std::map<int, Scratch> g_norm_scratch;
-std::map<int, Scratch> g_pack_scratch;
+using ScratchPool = std::map<std::pair<int, hipStream_t>, Scratch>;
+ScratchPool g_scratch;
+ScratchPool g_ffn_scratch;
+ScratchPool g_greedy_scratch;
+ScratchPool g_norm_scratch;
+ScratchPool g_pack_scratch;
+ScratchPool g_debug_scratch;  // parity instrumentation's own buffers
+std::vector<void*> g_retired;  // outgrown scratch buffers, never freed while work may still be queued on them
 
-kq_status device_scratch(std::map<int, Scratch>& pool, std::size_t bytes, void** out) {
+kq_status device_scratch(ScratchPool& pool, std::size_t bytes, hipStream_t stream, void** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
-    Scratch& s = pool[dev];
+    Scratch& s = pool[{dev, stream}];
     if (s.bytes < bytes) {
-        if (s.ptr) {
-            e = hipDeviceSynchronize();
-            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
-            (void)hipFree(s.ptr);
-            s.ptr = nullptr;
-            s.bytes = 0;
-        }
-        e = hipMalloc(&s.ptr, bytes);
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &capture);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+        if (capture != hipStreamCaptureStatusNone)
+            return fail(KQ_RUNTIME, "the library's workspace cannot grow during stream capture: pass a workspace");
+        void* p = nullptr;
+        e = hipMalloc(&p, std::max(bytes, s.bytes * 2));
         if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
-        s.bytes = bytes;
+        if (s.ptr) g_retired.push_back(s.ptr);
+        s.ptr = p;
+        s.bytes = std::max(bytes, s.bytes * 2);
     }
     *out = s.ptr;
     return KQ_OK;
@@ -138,16 +145,62 @@ kq_status validate_desc(const kq_pack_desc* d) {
     return KQ_OK;
 }
 
-// Copy a descriptor's buffer to host memory (it may live on the device).
-kq_status fetch(const void* src, std::size_t bytes, kq_memory memory, std::vector<std::uint8_t>& out) {
+// Load-time calls (packing, import, export, weight quantization) synchronize their stream and allocate, so they
+// refuse a stream that is being captured into a graph.
+kq_status refuse_capture(hipStream_t stream, const char* what) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipError_t e = hipStreamIsCapturing(stream, &capture); e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    if (capture != hipStreamCaptureStatusNone) return fail(KQ_RUNTIME, std::string(what) + " cannot run under stream capture");
+    return KQ_OK;
+}
+
+// Copy a descriptor's buffer to host memory. Device sources are read in `stream` order, after the work that
+// produced them on that stream.
+kq_status fetch(const void* src, std::size_t bytes, kq_memory memory, hipStream_t stream, std::vector<std::uint8_t>& out) {
     out.resize(bytes);
     if (memory == KQ_HOST) {
         std::memcpy(out.data(), src, bytes);
         return KQ_OK;
     }
-    const hipError_t e = hipMemcpy(out.data(), src, bytes, hipMemcpyDeviceToHost);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpy(weight source)");
+    hipError_t e = hipMemcpyAsync(out.data(), src, bytes, hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return hip_fail(e, "copy of a weight source");
     return KQ_OK;
+}
+
+// Offsets of the sub-buffers in a packed weight's one device allocation (-1 when absent) and its size. Both packing
+// and kq_weight_import derive the image from the weight's geometry and modes with this function, so an imported
+// blob is accepted only when its header describes exactly the image this library would have built.
+struct ImageLayout {
+    std::int64_t tiles = 0, scales = 0, zero_points = -1, zeros = -1, code_sums = -1;
+    std::size_t bytes = 0;
+};
+ImageLayout image_layout(const kq::Weight& w) {
+    const kq::Geometry& g = w.geo;
+    const std::int64_t N = g.rows, B = g.cols / g.group, row_bytes = g.cols / (8 / g.bits);
+    const std::size_t ssz = w.scale_type == kq::META_F16 ? 2 : 4;
+    const std::size_t zsz = w.zero_type == kq::META_F16 ? 2 : 4;
+    ImageLayout l;
+    std::size_t off = 0;
+    l.tiles = 0;
+    off = align_up(off + static_cast<std::size_t>(w.tiled ? g.tile_bytes_total() : N * row_bytes));
+    const std::int64_t meta_n = w.tiled ? g.meta_count() : N * B;
+    l.scales = static_cast<std::int64_t>(off);
+    off = align_up(off + static_cast<std::size_t>(meta_n) * ssz);
+    if (w.zero_mode == kq::ZERO_POINT) {
+        l.zero_points = static_cast<std::int64_t>(off);
+        off = align_up(off + static_cast<std::size_t>(w.tiled ? meta_n / 2 : meta_n));
+    }
+    if (w.zero_mode == kq::ZERO_FLOAT) {
+        l.zeros = static_cast<std::int64_t>(off);
+        off = align_up(off + static_cast<std::size_t>(meta_n) * zsz);
+    }
+    if (w.tiled && g.bits == 8) {
+        l.code_sums = static_cast<std::int64_t>(off);
+        off = align_up(off + static_cast<std::size_t>(meta_n) * 4);
+    }
+    l.bytes = off;
+    return l;
 }
 
 struct HostWeight {
@@ -162,6 +215,10 @@ kq_status pack_impl(const kq_pack_desc* descs, int count, void* stream, kq_weigh
     if (!descs || count <= 0) return fail(KQ_INVALID_ARGUMENT, "no weights to pack");
     for (int i = 0; i < count; ++i)
         if (kq_status s = validate_desc(&descs[i]); s != KQ_OK) return s;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < count; ++i)  // device sources are read on `stream`: it must not be capturing
+        if (descs[i].memory == KQ_DEVICE)
+            if (kq_status s = refuse_capture(st, "packing a weight"); s != KQ_OK) return s;
     const kq_pack_desc& d0 = descs[0];
     std::int64_t N = 0;
     for (int i = 0; i < count; ++i) {
@@ -188,12 +245,12 @@ kq_status pack_impl(const kq_pack_desc* descs, int count, void* stream, kq_weigh
     for (int i = 0; i < count; ++i) {
         const kq_pack_desc& d = descs[i];
         std::vector<std::uint8_t> tmp;
-        if (kq_status s = fetch(d.values, static_cast<std::size_t>(d.rows * row_bytes), d.memory, tmp); s != KQ_OK) return s;
+        if (kq_status s = fetch(d.values, static_cast<std::size_t>(d.rows * row_bytes), d.memory, st, tmp); s != KQ_OK) return s;
         std::memcpy(hw.values.data() + r0 * row_bytes, tmp.data(), tmp.size());
-        if (kq_status s = fetch(d.scales, static_cast<std::size_t>(d.rows * B) * ssz, d.memory, tmp); s != KQ_OK) return s;
+        if (kq_status s = fetch(d.scales, static_cast<std::size_t>(d.rows * B) * ssz, d.memory, st, tmp); s != KQ_OK) return s;
         std::memcpy(hw.scales.data() + static_cast<std::size_t>(r0 * B) * ssz, tmp.data(), tmp.size());
         if (has_zero) {
-            if (kq_status s = fetch(d.zeros, static_cast<std::size_t>(d.rows * B) * zsz, d.memory, tmp); s != KQ_OK) return s;
+            if (kq_status s = fetch(d.zeros, static_cast<std::size_t>(d.rows * B) * zsz, d.memory, st, tmp); s != KQ_OK) return s;
             std::memcpy(hw.zeros.data() + static_cast<std::size_t>(r0 * B) * zsz, tmp.data(), tmp.size());
         }
         r0 += d.rows;
@@ -222,6 +279,11 @@ kq_status pack_impl(const kq_pack_desc* descs, int count, void* stream, kq_weigh
 
     auto* w = new (std::nothrow) kq::Weight();
     if (!w) return fail(KQ_RUNTIME, "out of host memory");
+    w->scales_positive = true;
+    for (std::int64_t i = 0; i < N * B && w->scales_positive; ++i) {
+        const float sv = scale_at(i);
+        w->scales_positive = std::isfinite(sv) && sv > 0.F;
+    }
     w->geo = kq::Geometry::make(bits, group, N, K);
     w->tiled = kq::tiled_group_ok(bits, group);
     w->scale_type = d0.scales_dtype == KQ_F16 ? kq::META_F16 : kq::META_F32;
@@ -264,27 +326,13 @@ kq_status pack_impl(const kq_pack_desc* descs, int count, void* stream, kq_weigh
         }
     }
 
-    // sizes
     const kq::Geometry& g = w->geo;
-    std::size_t off = 0;
-    const std::size_t tiles_off = off;
-    off = align_up(off + static_cast<std::size_t>(w->tiled ? g.tile_bytes_total() : N * row_bytes));
-    const std::int64_t meta_n = w->tiled ? g.meta_count() : N * B;
-    const std::size_t scales_off = off;
-    off = align_up(off + static_cast<std::size_t>(meta_n) * ssz);
-    std::size_t zp_off = 0, zeros_off = 0, cs_off = 0;
-    if (w->zero_mode == kq::ZERO_POINT) {
-        zp_off = off;
-        off = align_up(off + static_cast<std::size_t>(w->tiled ? meta_n / 2 : meta_n));
-    }
-    if (w->zero_mode == kq::ZERO_FLOAT) {
-        zeros_off = off;
-        off = align_up(off + static_cast<std::size_t>(meta_n) * zsz);
-    }
-    if (w->tiled && bits == 8) {
-        cs_off = off;
-        off = align_up(off + static_cast<std::size_t>(meta_n) * 4);
-    }
+    const ImageLayout lay = image_layout(*w);
+    const std::size_t tiles_off = static_cast<std::size_t>(lay.tiles), scales_off = static_cast<std::size_t>(lay.scales);
+    const std::size_t zp_off = static_cast<std::size_t>(std::max<std::int64_t>(lay.zero_points, 0));
+    const std::size_t zeros_off = static_cast<std::size_t>(std::max<std::int64_t>(lay.zeros, 0));
+    const std::size_t cs_off = static_cast<std::size_t>(std::max<std::int64_t>(lay.code_sums, 0));
+    const std::size_t off = lay.bytes;
     std::vector<std::uint8_t> image(off, 0);
     if (w->tiled) {
         kq::encode_tiles(bits, N, K, hw.values.data(), image.data() + tiles_off);
@@ -314,6 +362,10 @@ kq_status pack_impl(const kq_pack_desc* descs, int count, void* stream, kq_weigh
         if (w->zero_mode == kq::ZERO_FLOAT) std::memcpy(image.data() + zeros_off, hw.zeros.data(), hw.zeros.size());
     }
 
+    if (kq_status s = refuse_capture(st, "packing a weight"); s != KQ_OK) {
+        delete w;
+        return s;
+    }
     hipError_t e = hipGetDevice(&w->device);
     if (e != hipSuccess) {
         delete w;
@@ -370,54 +422,64 @@ kq_status prepare_call(const kq_weight* weight, const kq_linear_args* args, bool
     return KQ_OK;
 }
 
+// The kernel sequence of a prepared call. Workspace-independent: the predicates read shapes, modes and (for the g = 32
+// / 64 GEMM's 16-byte loads) the input's alignment only.
+kq::Route route_of(const kq::LinearCall& c, kq::SkinnyPlan* plan) {
+    if (c.M == 0) return kq::ROUTE_NONE;
+    if (kq::decode_fits(c)) return kq::ROUTE_DECODE;
+    kq::SkinnyPlan p;
+    if (kq::skinny_plan(c, p)) {
+        if (plan) *plan = p;
+        return kq::ROUTE_SKINNY;
+    }
+    if (kq::gemm_i4_fits(c)) return kq::ROUTE_GEMM_I4;
+    if (kq::gemm_i4g_fits(c)) return kq::ROUTE_GEMM_I4G;
+    if (c.path == kq::PATH_PORTABLE) return kq::ROUTE_PORTABLE;
+    if (!c.w->tiled) return kq::ROUTE_ROWMAJOR;
+    return c.M <= 8 ? kq::ROUTE_GEMV : kq::ROUTE_GEMM;
+}
+
 kq_status run_call(kq::LinearCall& c, const kq_linear_args* args, std::size_t ws_needed, hipStream_t stream) {
     if (c.M == 0) return KQ_OK;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     if (dev != c.w->device) return fail(KQ_INVALID_ARGUMENT, "weight was packed on another device");
-    // Decode (M <= 16): one fused launch, no workspace.
-    if (kq::decode_fits(c)) {
-        e = kq::launch_decode(c, stream);
-        if (e != hipSuccess) return hip_fail(e, "decode projection launch");
-        return KQ_OK;
-    }
     kq::SkinnyPlan plan;
-    if (kq::skinny_plan(c, plan)) {
+    const kq::Route route = route_of(c, &plan);
+    // Decode shapes: one fused launch, no workspace.
+    if (route == kq::ROUTE_DECODE) {
+        e = kq::launch_decode(c, stream);
+        return e == hipSuccess ? KQ_OK : hip_fail(e, "decode projection launch");
+    }
+    if (route == kq::ROUTE_SKINNY) {
         e = kq::launch_skinny(c, plan, stream);
-        if (e != hipSuccess) return hip_fail(e, "skinny projection launch");
-        return KQ_OK;
+        return e == hipSuccess ? KQ_OK : hip_fail(e, "skinny projection launch");
     }
     void* ws = args->workspace;
     if (ws_needed) {
         if (ws) {
             if (args->workspace_bytes < ws_needed) return fail(KQ_INVALID_ARGUMENT, "workspace too small");
-        } else if (kq_status s = device_scratch(g_scratch, ws_needed, &ws); s != KQ_OK) {
+        } else if (kq_status s = device_scratch(g_scratch, ws_needed, stream, &ws); s != KQ_OK) {
             return s;
         }
         c.act = kq::carve_workspace(*c.w, c.M, ws);
     }
     // Prefill, 4-bit g = 128: quantizer + int8 MFMA GEMM (GELU gate fused).
-    if (kq::gemm_i4_fits(c)) {
+    if (route == kq::ROUTE_GEMM_I4) {
         e = kq::launch_gemm_i4(c, c.act, stream);
-        if (e != hipSuccess) return hip_fail(e, "prefill projection launch");
-        return KQ_OK;
+        return e == hipSuccess ? KQ_OK : hip_fail(e, "prefill projection launch");
     }
     // Prefill, 4-bit g = 32 / 64 (fused QKV): quantizer + two-stage int8 MFMA GEMM.
-    if (kq::gemm_i4g_fits(c)) {
+    if (route == kq::ROUTE_GEMM_I4G) {
         e = kq::launch_gemm_i4g(c, stream);
-        if (e != hipSuccess) return hip_fail(e, "prefill projection launch");
-        return KQ_OK;
+        return e == hipSuccess ? KQ_OK : hip_fail(e, "prefill projection launch");
     }
-    // GELU gating is fused into the tiled GEMV/GEMM when the gate and up halves are whole tiles; otherwise the
-    // full projection goes to a scratch buffer and a gating kernel follows.
-    const bool fused_gelu = c.gelu_gate && c.path != kq::PATH_PORTABLE && c.w->tiled && (c.w->geo.rows / 2) % kq::kTileRows == 0;
+    // GELU gating is fused everywhere except in the tiled GEMV/GEMM when the gate/up split falls inside a 16-row
+    // tile: the full projection then goes to the workspace's temp and a gating kernel follows.
     float* final_y = c.y;
-    if (c.gelu_gate && !fused_gelu) {
-        void* tmp = nullptr;
-        if (kq_status s = device_scratch(g_gelu_scratch, static_cast<std::size_t>(c.M * c.w->geo.rows) * 4, &tmp); s != KQ_OK)
-            return s;
-        c.y = static_cast<float*>(tmp);
+    if (c.gelu_gate && (route == kq::ROUTE_GEMV || route == kq::ROUTE_GEMM) && kq::gelu_needs_temp(*c.w)) {
+        c.y = c.act.gelu_tmp;
         c.gelu_gate = false;
     }
     e = kq::launch_quantize(c, stream);
@@ -536,12 +598,14 @@ std::size_t split_bytes(const Weight& w, std::int64_t M) {
 }
 }  // namespace
 
+bool gelu_needs_temp(const Weight& w) { return w.tiled && w.geo.rows % 2 == 0 && (w.geo.rows / 2) % kTileRows != 0; }
+
 std::size_t workspace_bytes(const Weight& w, std::int64_t M) {
     const std::int64_t rows = act_rows(w, M);
     const std::int64_t cols = w.tiled ? w.geo.cols_p : w.geo.cols;
     const std::int64_t groups = w.tiled ? w.geo.groups_p : w.geo.cols / w.geo.group;
     return align_up(static_cast<std::size_t>(rows * cols)) + 3 * align_up(static_cast<std::size_t>(rows * groups) * 4) +
-           split_bytes(w, M);
+           split_bytes(w, M) + (gelu_needs_temp(w) ? align_up(static_cast<std::size_t>(M * w.geo.rows) * 4) : 0);
 }
 
 ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base) {
@@ -558,7 +622,11 @@ ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base) {
     p += align_up(static_cast<std::size_t>(a.rows_p * groups) * 4);
     a.zero = reinterpret_cast<std::int32_t*>(p);
     p += align_up(static_cast<std::size_t>(a.rows_p * groups) * 4);
-    if (split_bytes(w, M)) a.partial = reinterpret_cast<float*>(p);
+    if (const std::size_t sb = split_bytes(w, M)) {
+        a.partial = reinterpret_cast<float*>(p);
+        p += sb;
+    }
+    if (gelu_needs_temp(w)) a.gelu_tmp = reinterpret_cast<float*>(p);
     return a;
 }
 
@@ -587,6 +655,7 @@ kq_status kq_weight_export(const kq_weight* weight, void* host, size_t bytes, vo
     if (!weight || !host) return fail(KQ_INVALID_ARGUMENT, "null weight or buffer");
     const kq::Weight& w = *as_weight(weight);
     if (bytes < sizeof(BlobHeader) + w.bytes) return fail(KQ_INVALID_ARGUMENT, "export buffer too small");
+    if (kq_status s = refuse_capture(static_cast<hipStream_t>(stream), "exporting a weight"); s != KQ_OK) return s;
     BlobHeader h{};
     std::memcpy(h.magic, kBlobMagic, sizeof(h.magic));
     h.version = kBlobVersion;
@@ -622,9 +691,17 @@ kq_status kq_weight_import(const void* host, size_t bytes, void* stream, kq_weig
     std::memcpy(&h, host, sizeof(h));
     if (std::memcmp(h.magic, kBlobMagic, sizeof(h.magic)) != 0 || h.version != kBlobVersion)
         return fail(KQ_INVALID_MANIFEST, "not a packed weight blob of this layout version");
+    // The header must describe exactly the image pack_impl builds for its geometry and modes: the same PACKED_LINEAR
+    // shape rules (context.cpp:207-218), modes in range, the tiled flag the geometry implies, and every offset and the
+    // size equal to what image_layout() derives. Anything else could send a kernel past the allocation.
     const bool ok_bits = h.bits == 2 || h.bits == 4 || h.bits == 8;
-    if (!ok_bits || h.group <= 0 || h.rows <= 0 || h.cols <= 0 || h.cols % h.group || bytes != sizeof(h) + h.bytes ||
+    if (!ok_bits || h.group <= 0 || h.rows <= 0 || h.cols <= 0 || h.cols % h.group || h.group % (8 / h.bits) ||
+        h.rows >= (std::int64_t{1} << 40) || h.cols >= (std::int64_t{1} << 32) || bytes != sizeof(h) + h.bytes ||
         h.bytes == 0)
+        return fail(KQ_INVALID_MANIFEST, "malformed packed weight blob");
+    if ((h.scale_type != kq::META_F32 && h.scale_type != kq::META_F16) ||
+        (h.zero_mode != kq::ZERO_NONE && h.zero_mode != kq::ZERO_POINT && h.zero_mode != kq::ZERO_FLOAT) ||
+        (h.zero_type != kq::META_F32 && h.zero_type != kq::META_F16) || (h.tiled != 0) != kq::tiled_group_ok(h.bits, h.group))
         return fail(KQ_INVALID_MANIFEST, "malformed packed weight blob");
     auto* w = new kq::Weight{};
     w->geo = kq::Geometry::make(h.bits, h.group, h.rows, h.cols);
@@ -632,15 +709,33 @@ kq_status kq_weight_import(const void* host, size_t bytes, void* stream, kq_weig
     w->scale_type = h.scale_type;
     w->zero_mode = h.zero_mode;
     w->zero_type = h.zero_type;
-    for (std::int64_t o : {h.tiles, h.scales, h.zero_points, h.zeros, h.code_sums}) {
-        if (o < -1 || o >= static_cast<std::int64_t>(h.bytes)) {
-            delete w;
-            return fail(KQ_INVALID_MANIFEST, "malformed packed weight blob");
-        }
-    }
-    if (h.tiles < 0 || h.scales < 0) {
+    const ImageLayout lay = image_layout(*w);
+    if (h.tiles != lay.tiles || h.scales != lay.scales || h.zero_points != lay.zero_points || h.zeros != lay.zeros ||
+        h.code_sums != lay.code_sums || h.bytes != lay.bytes) {
         delete w;
         return fail(KQ_INVALID_MANIFEST, "malformed packed weight blob");
+    }
+    if (kq_status s = refuse_capture(static_cast<hipStream_t>(stream), "importing a weight"); s != KQ_OK) {
+        delete w;
+        return s;
+    }
+    {
+        const auto* img = static_cast<const std::uint8_t*>(host) + sizeof(h);
+        const std::int64_t B = h.cols / h.group;
+        w->scales_positive = true;
+        for (std::int64_t n = 0; n < h.rows && w->scales_positive; ++n)
+            for (std::int64_t b = 0; b < B && w->scales_positive; ++b) {
+                const std::int64_t i = w->tiled ? w->geo.meta_index(n, b) : n * B + b;
+                float sv;
+                if (h.scale_type == kq::META_F16) {
+                    std::uint16_t hb;
+                    std::memcpy(&hb, img + h.scales + 2 * i, 2);
+                    sv = half_bits_to_float(hb);
+                } else {
+                    std::memcpy(&sv, img + h.scales + 4 * i, 4);
+                }
+                w->scales_positive = std::isfinite(sv) && sv > 0.F;
+            }
     }
     hipError_t e = hipGetDevice(&w->device);
     if (e == hipSuccess) e = hipMalloc(&w->allocation, h.bytes);
@@ -723,17 +818,17 @@ kq_status kq_gated_feed_forward(const kq_weight* gate_up, const kq_weight* down,
     const kq::Weight& gu = *as_weight(gate_up);
     const kq::Weight& dn = *as_weight(down);
     const FfnLayout l = ffn_layout(gu, dn, args->m);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
     void* ws = args->workspace;
     if (ws) {
         if (args->workspace_bytes < l.total()) return fail(KQ_INVALID_ARGUMENT, "workspace too small");
-    } else if (kq_status s = device_scratch(g_ffn_scratch, l.total(), &ws); s != KQ_OK) {
+    } else if (kq_status s = device_scratch(g_ffn_scratch, l.total(), st, &ws); s != KQ_OK) {
         return s;
     }
     auto* base = static_cast<std::uint8_t*>(ws);
     float* h = reinterpret_cast<float*>(base);
     float* full = reinterpret_cast<float*>(base + l.h);
     void* proj = base + l.h + l.full;
-    const hipStream_t st = static_cast<hipStream_t>(stream);
     kq_linear_args a{};
     a.x = args->x;
     a.x_dtype = args->x_dtype;
@@ -770,13 +865,13 @@ kq_status kq_greedy_token(const float* logits, int64_t rows, int64_t width, int3
     if (rows == 0) return KQ_OK;
     if (!logits || !tokens) return fail(KQ_INVALID_ARGUMENT, "null logits or tokens");
     const std::size_t need = kq_greedy_workspace_size(rows, width);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
     void* ws = workspace;
     if (ws) {
         if (workspace_bytes < need) return fail(KQ_INVALID_ARGUMENT, "workspace too small");
-    } else if (kq_status s = device_scratch(g_greedy_scratch, need, &ws); s != KQ_OK) {
+    } else if (kq_status s = device_scratch(g_greedy_scratch, need, st, &ws); s != KQ_OK) {
         return s;
     }
-    const hipStream_t st = static_cast<hipStream_t>(stream);
     auto* parts = static_cast<int4*>(ws);
     if (hipError_t e = kq::launch_greedy_chunks(logits, rows, width, parts, st); e != hipSuccess) return hip_fail(e, "greedy launch");
     if (hipError_t e = kq::launch_greedy_reduce(parts, rows, kq::greedy_chunk_count(width), tokens, st); e != hipSuccess)
@@ -798,7 +893,7 @@ kq_status kq_packed_linear_greedy(const kq_weight* weight, const kq_linear_args*
     if (args->m > 0) {
         if (ws) {
             if (args->workspace_bytes < l.total()) return fail(KQ_INVALID_ARGUMENT, "workspace too small");
-        } else if (kq_status s = device_scratch(g_greedy_scratch, l.total(), &ws); s != KQ_OK) {
+        } else if (kq_status s = device_scratch(g_greedy_scratch, l.total(), static_cast<hipStream_t>(stream), &ws); s != KQ_OK) {
             return s;
         }
     }
@@ -894,7 +989,7 @@ kq_status kq_packed_linear_rms(const kq_weight* weight, const kq_linear_args* ar
     void* ws = args->workspace;
     if (ws) {
         if (args->workspace_bytes < l.total()) return fail(KQ_INVALID_ARGUMENT, "workspace too small");
-    } else if (kq_status s = device_scratch(g_norm_scratch, l.total(), &ws); s != KQ_OK) {
+    } else if (kq_status s = device_scratch(g_norm_scratch, l.total(), st, &ws); s != KQ_OK) {
         return s;
     }
     auto* base = static_cast<std::uint8_t*>(ws);
@@ -912,7 +1007,9 @@ kq_status kq_packed_linear_rms(const kq_weight* weight, const kq_linear_args* ar
     n.eps2 = norm->epsilon;
     // Prefill 4-bit g = 128: per-row statistics (and h), then the row quantizer normalizes while it quantizes.
     if (ws_lin) c.act = kq::carve_workspace(*c.w, c.M, base);
-    if (kq::gemm_i4_fits(c) && aligned16(norm->weight)) {
+    kq::LinearCall fused = c;  // the row quantizer reads h (F32) in the residual form
+    if (res) fused.x_type = kq::ACT_F32;
+    if (kq::gemm_i4_fits(fused) && aligned16(norm->weight)) {
         n.out1 = res ? norm->hidden : nullptr;
         n.w2 = res ? norm->weight : nullptr;
         n.inv_out = inv;
@@ -953,8 +1050,9 @@ kq_status kq_quantize_weight(const void* weight, kq_dtype dtype, int64_t rows, i
     if (rows * (cols / group_size) >= (std::int64_t{1} << 38))  // one thread per (row, group), 2^30 workgroups
         return fail(KQ_UNSUPPORTED, "weight too large for one quantization launch");
     const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (kq_status s = refuse_capture(st, "weight quantization"); s != KQ_OK) return s;
     void* flag = nullptr;
-    if (kq_status s = device_scratch(g_pack_scratch, 256, &flag); s != KQ_OK) return s;
+    if (kq_status s = device_scratch(g_pack_scratch, 256, st, &flag); s != KQ_OK) return s;
     int* error = static_cast<int*>(flag);
     if (hipError_t e = hipMemsetAsync(error, 0, sizeof(int), st); e != hipSuccess) return hip_fail(e, "hipMemsetAsync");
     const int dt = dtype == KQ_F32 ? 0 : (dtype == KQ_F16 ? 1 : 2);
@@ -989,7 +1087,7 @@ kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_d
     if (fused || kq::skinny_plan(c, plan)) {
         // the fused quantizer of the decode projection reports what it computed
         void* ybuf = nullptr;
-        if (kq_status s = device_scratch(g_gelu_scratch, static_cast<std::size_t>(m * c.w->geo.rows) * 4, &ybuf); s != KQ_OK)
+        if (kq_status s = device_scratch(g_debug_scratch, static_cast<std::size_t>(m * c.w->geo.rows) * 4, st, &ybuf); s != KQ_OK)
             return s;
         c.y = static_cast<float*>(ybuf);
         c.dq_codes = codes;
@@ -1001,7 +1099,7 @@ kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_d
         return KQ_OK;
     }
     void* ws = nullptr;
-    if (kq_status s = device_scratch(g_scratch, ws_bytes, &ws); s != KQ_OK) return s;
+    if (kq_status s = device_scratch(g_debug_scratch, align_up(ws_bytes) + 256, st, &ws); s != KQ_OK) return s;
     c.act = kq::carve_workspace(*c.w, m, ws);
     if (kq::gemm_i4_fits(c)) {
         const hipError_t e = kq::launch_gemm_i4_quantize_dump(c, c.act, codes, scales, sums, zero_points, st);
@@ -1027,6 +1125,69 @@ kq_status kq_debug_partials(const kq_weight* weight, const kq_linear_args* args,
     if (c.path == kq::PATH_PORTABLE) return fail(KQ_UNSUPPORTED, "the portable path has no integer partials");
     c.dump = partials;
     return run_call(c, args, ws, static_cast<hipStream_t>(stream));
+}
+
+kq_status kq_lowbit_parity_linear(const kq_weight* weight, const kq_linear_args* args, void* stream) {
+    if (!weight || !args) return fail(KQ_INVALID_ARGUMENT, "null weight or arguments");
+    const kq::Weight& w = *as_weight(weight);
+    // Context::packed_linear's scale check (ops/context.cpp:824-825), then its LOWBIT_PARITY domain (:919-929)
+    if (!std::isfinite(args->input_scale) || args->input_scale < 0 || !std::isfinite(args->output_scale) ||
+        args->output_scale < 0)
+        return fail(KQ_INVALID_ARGUMENT, "invalid calibrated projection scales");
+    if (args->m < 0) return fail(KQ_INVALID_ARGUMENT, "negative row count");
+    if (args->x_dtype != KQ_F32 || !(args->input_scale > 0) || !(args->output_scale > 0) ||
+        w.scale_type != kq::META_F32 || args->m > INT32_MAX || w.geo.cols > INT32_MAX || w.geo.rows > INT32_MAX)
+        return fail(KQ_UNSUPPORTED, "lowbit-parity requires calibrated CPU packed weights with compatible group scales");
+    // runtime::parity::packed_linear's scale check (parity_math.cpp:239-240)
+    if (!w.scales_positive) return fail(KQ_INVALID_ARGUMENT, "packed weight scales must be finite and positive");
+    if (args->m == 0) return KQ_OK;
+    if (!args->x || !args->y) return fail(KQ_INVALID_ARGUMENT, "null input or output");
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev != w.device) return fail(KQ_INVALID_ARGUMENT, "weight was packed on another device");
+    kq::LinearCall c{};
+    c.w = &w;
+    c.x = args->x;
+    c.x_type = kq::ACT_F32;
+    c.M = args->m;
+    c.input_scale = args->input_scale;
+    c.output_scale = args->output_scale;
+    c.y = args->y;
+    c.path = kq::PATH_PORTABLE;
+    c.parity = true;
+    if (hipError_t e = kq::launch_linear(c, static_cast<hipStream_t>(stream)); e != hipSuccess)
+        return hip_fail(e, "lowbit-parity projection launch");
+    return KQ_OK;
+}
+
+int32_t kq_debug_route(const kq_weight* weight, const kq_linear_args* args, int32_t gelu_gate) {
+    kq::LinearCall c;
+    std::size_t ws = 0;
+    if (prepare_call(weight, args, gelu_gate != 0, c, &ws) != KQ_OK) return -1;
+    return route_of(c, nullptr);
+}
+
+int32_t kq_debug_route_shape(int32_t bits, int32_t group_size, int64_t rows, int64_t cols, int32_t zero_mode,
+                             int32_t scale_f16, int64_t m, kq_dtype x_dtype, float input_scale, int32_t gelu_gate) {
+    if ((bits != 2 && bits != 4 && bits != 8) || group_size <= 0 || rows <= 0 || cols <= 0 || cols % group_size ||
+        group_size % (8 / bits) || zero_mode < kq::ZERO_NONE || zero_mode > kq::ZERO_FLOAT || m < 0 ||
+        (x_dtype != KQ_F32 && x_dtype != KQ_BF16) || !std::isfinite(input_scale) || input_scale < 0 ||
+        (gelu_gate && rows % 2))
+        return -1;
+    kq::Weight w;  // geometry and modes only: no device memory is touched
+    w.geo = kq::Geometry::make(bits, group_size, rows, cols);
+    w.tiled = kq::tiled_group_ok(bits, group_size);
+    w.scale_type = scale_f16 ? kq::META_F16 : kq::META_F32;
+    w.zero_mode = zero_mode;
+    kq::LinearCall c{};
+    c.w = &w;
+    c.x = nullptr;
+    c.x_type = x_dtype == KQ_BF16 ? kq::ACT_BF16 : kq::ACT_F32;
+    c.M = m;
+    c.input_scale = input_scale;
+    c.path = select_path(bits, group_size, cols, rows, zero_mode != kq::ZERO_NONE, input_scale);
+    c.gelu_gate = gelu_gate != 0;
+    return route_of(c, nullptr);
 }
 
 kq_status kq_debug_read_floor(const void* data, size_t bytes, int32_t* sink, void* stream) {

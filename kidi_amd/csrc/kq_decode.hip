@@ -735,11 +735,7 @@ hipError_t launch_decode(const LinearCall& c, hipStream_t stream) {
     a.total_pairs = static_cast<int>(c.gelu_gate ? w.geo.n_tiles / 2 : (single ? w.geo.n_tiles : (w.geo.n_tiles + 1) / 2));
     // several units per workgroup once the grid passes ~2 workgroups per CU: the activation quantization and the
     // launch of a workgroup are then shared by more weight tiles
-    static const int forced_pairs = [] {
-        const char* e = std::getenv("KQ_DECODE_PAIRS");  // tuning override
-        return e ? std::atoi(e) : 0;
-    }();
-    a.pairs = forced_pairs > 0 ? forced_pairs : std::max(1, a.total_pairs / 512);
+    a.pairs = std::max(1, a.total_pairs / 512);
     const int blocks = (a.total_pairs + a.pairs - 1) / a.pairs;
     const dim3 grid(static_cast<unsigned>(blocks)), block(64 * W);
     const int mr = c.M <= 4 ? 4 : 8;

@@ -202,6 +202,7 @@ struct LinearArgs {
     std::int64_t M, N, K, cols_p, k_tiles, n_tiles;
     int group, groups_p, groups;  // groups = K / g (real)
     int zero_mode, zero_half, is_static, gelu;
+    int parity;                   // portable kernel: LOWBIT_PARITY form (serial FMA, zeros not applied)
     float input_scale, output_scale;
     int units, tiles_per_unit;    // GEMV split of the K range across waves
     // skinny (fused quantization) projection

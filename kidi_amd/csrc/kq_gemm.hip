@@ -908,18 +908,10 @@ __global__ __launch_bounds__(256) void transpose_stats_kernel(const float* s_t, 
 
 }  // namespace
 
-namespace {
-int env_int(const char* name) {
-    const char* e = std::getenv(name);  // tuning overrides
-    return e ? std::atoi(e) : 0;
-}
-}  // namespace
-
 // Launch plan: 256-row tiles (WM = 4), the K range split in 2, 4 or 8 when that fills the chip (at least 256
 // workgroups) and every range keeps >= 16 groups; otherwise 128-row tiles (WM = 2), split the same way. A split adds
 // one small reduction launch and the partial tiles' traffic, so short K ranges do not pay for it.
 GemmPlan gemm_i4_plan(const Weight& w, std::int64_t M, bool gelu) {
-    static const int forced_wm = env_int("KQ_GEMM_WM"), forced_split = env_int("KQ_GEMM_KSPLIT");
     const int kt = static_cast<int>(w.geo.k_tiles);
     GemmPlan p;
     p.n_blocks = gelu ? static_cast<int>((w.geo.n_tiles / 2 + 3) / 4) : static_cast<int>((w.geo.n_tiles + 7) / 8);
@@ -933,22 +925,15 @@ GemmPlan gemm_i4_plan(const Weight& w, std::int64_t M, bool gelu) {
         }
         return need_full ? 0 : best;
     };
-    if (forced_wm == 2 || forced_wm == 4) {
-        p.wm = forced_wm;
-        p.m_blocks = blocks_m(p.wm);
+    p.wm = 4;
+    p.m_blocks = blocks_m(4);
+    p.ksplit = best_split(p.m_blocks * p.n_blocks, true);
+    if (p.ksplit == 0) {
+        p.wm = 2;
+        p.m_blocks = blocks_m(2);
         p.ksplit = best_split(p.m_blocks * p.n_blocks, false);
-    } else {
-        p.wm = 4;
-        p.m_blocks = blocks_m(4);
-        p.ksplit = best_split(p.m_blocks * p.n_blocks, true);
-        if (p.ksplit == 0) {
-            p.wm = 2;
-            p.m_blocks = blocks_m(2);
-            p.ksplit = best_split(p.m_blocks * p.n_blocks, false);
-        }
     }
     if (p.ksplit < 1) p.ksplit = 1;
-    if (forced_split > 0 && kt % forced_split == 0 && kt / forced_split >= 4) p.ksplit = forced_split;
     return p;
 }
 
@@ -960,6 +945,8 @@ bool gemm_i4_fits(const LinearCall& c) {
     if (w.geo.cols % 512 || w.geo.cols_p != w.geo.cols) return false;
     if (c.gelu_gate && ((w.geo.rows / 2) % kTileRows || w.geo.n_tiles % 2)) return false;
     const std::int64_t M_p = round_up(c.M, kQuantRows);
+    // the row quantizer addresses x with 32-bit byte offsets (buffer resource of M * K * element bytes)
+    if (c.M * w.geo.cols * (c.x_type == ACT_F32 ? 4 : 2) >= (std::int64_t{1} << 32)) return false;
     if (M_p * w.geo.cols >= (std::int64_t{1} << 31) || w.geo.k_tiles * kTileBytes >= (std::int64_t{1} << 31) ||
         w.geo.meta_count() * 4 >= (std::int64_t{1} << 31) || M_p * w.geo.groups_p * 4 >= (std::int64_t{1} << 31))
         return false;

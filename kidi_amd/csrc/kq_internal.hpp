@@ -31,6 +31,20 @@ struct Weight {
     void* allocation = nullptr;     // one hipMalloc holding all of the above
     std::size_t bytes = 0;
     int device = 0;
+    bool scales_positive = false;   // every scale finite and > 0 (LOWBIT_PARITY's precondition)
+};
+
+// The kernel sequence a projection call runs (kq_debug_route reports it; run_call dispatches on it).
+enum Route : int {
+    ROUTE_NONE = 0,      // M = 0: nothing runs
+    ROUTE_DECODE = 1,    // decode_kernel (kq_decode.hip), activation quantization fused
+    ROUTE_SKINNY = 2,    // skinny_kernel (kq_skinny.hip), activation quantization fused
+    ROUTE_GEMM_I4 = 3,   // quantize_rows_kernel + gemm_i4_kernel (kq_gemm.hip)
+    ROUTE_GEMM_I4G = 4,  // quantize_rows_g_kernel + gemm_i4g_kernel (kq_gemm_g.hip)
+    ROUTE_GEMV = 5,      // quantize_kernel + gemv_kernel (kq_kernels.hip)
+    ROUTE_GEMM = 6,      // quantize_kernel + gemm_kernel (kq_kernels.hip)
+    ROUTE_ROWMAJOR = 7,  // quantize_rowmajor_kernel + rowmajor_kernel (kq_kernels.hip)
+    ROUTE_PORTABLE = 8   // portable_kernel (kq_kernels.hip)
 };
 
 // Activation workspace carved out of one device buffer.
@@ -40,6 +54,7 @@ struct ActBuffers {
     std::int32_t* sum = nullptr;    // [rows_p][groups_p]
     std::int32_t* zero = nullptr;   // [rows_p][groups_p]
     float* partial = nullptr;       // prefill GEMM with split K: fp32 partial tiles of every K range
+    float* gelu_tmp = nullptr;      // [M][N] projection before GELU gating, for gate/up splits inside a row tile
     std::int64_t rows_p = 0;
 };
 
@@ -52,6 +67,7 @@ struct LinearCall {
     float* y;
     int path;
     bool gelu_gate;                 // y [M, N/2] = gelu_tanh(first half) * second half
+    bool parity = false;            // LOWBIT_PARITY projection (portable kernel, serial FMA)
     std::int32_t* dump;             // optional int32 partials [M][N][K/g]
     ActBuffers act;
     // optional dumps of the fused (skinny) quantizer: codes [M][K] natural order, block stats [M][K/g]
@@ -137,6 +153,9 @@ hipError_t launch_gemm_i4g_quantize_dump(const LinearCall& c, std::int8_t* codes
                                          std::int32_t* zero_points, hipStream_t stream);
 
 std::size_t workspace_bytes(const Weight& w, std::int64_t M);
+// GELU gating runs after the projection (through ActBuffers::gelu_tmp) only for tiled weights whose gate/up split
+// falls inside a 16-row tile; every other path fuses it.
+bool gelu_needs_temp(const Weight& w);
 ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base);
 
 // Kernel launchers (kq_kernels.hip). Return hipSuccess or the launch error.

@@ -683,10 +683,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(LinearArgs a) {
 // Row-major (Kidi layout) integer path for group sizes the tiles cannot carry: one thread per output, exact int32
 // per group, epilogue in the oracle's order.
 template <int BITS, typename ST>
-__global__ __launch_bounds__(256) void rowmajor_kernel(LinearArgs a) {
-    const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (id >= a.M * a.N) return;
-    const std::int64_t m = id / a.N, n = id % a.N;
+__device__ float rowmajor_output(const LinearArgs& a, std::int64_t m, std::int64_t n) {
     const std::int64_t row_bytes = a.K / (8 / BITS);
     const std::uint8_t* row = a.tiles + n * row_bytes;
     float acc = 0.F;
@@ -712,16 +709,22 @@ __global__ __launch_bounds__(256) void rowmajor_kernel(LinearArgs a) {
         acc = a.is_static ? acc + t : acc + a.a_scale[ab] * t;
     }
     if (a.is_static) acc = acc * a.input_scale;
-    a.y[m * a.N + n] = calibrate_output(acc, a.output_scale);
+    return calibrate_output(acc, a.output_scale);
 }
 
-// Kidi's portable float path (PortablePackedLinearOp, operators.cpp:2639-2713): w = c*s (+ z), activations
-// statically rounded when input_scale > 0, fp32 sum over k in order, output rounding. One thread per output.
+// One thread per output; with a.gelu one thread per gated output (gate row i and up row i + N/2).
 template <int BITS, typename ST>
-__global__ __launch_bounds__(256) void portable_kernel(LinearArgs a, int tiled) {
+__global__ __launch_bounds__(256) void rowmajor_kernel(LinearArgs a) {
     const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (id >= a.M * a.N) return;
-    const std::int64_t m = id / a.N, n = id % a.N;
+    const std::int64_t cols = a.gelu ? a.N / 2 : a.N;
+    if (id >= a.M * cols) return;
+    const std::int64_t m = id / cols, n = id % cols;
+    if (a.gelu) a.y[id] = gelu_tanh(rowmajor_output<BITS, ST>(a, m, n)) * rowmajor_output<BITS, ST>(a, m, n + cols);
+    else a.y[id] = rowmajor_output<BITS, ST>(a, m, n);
+}
+
+template <int BITS, typename ST>
+__device__ float portable_output(const LinearArgs& a, int tiled, std::int64_t m, std::int64_t n) {
     const std::int64_t row_bytes = a.K / (8 / BITS);
     float acc = 0.F;
     for (std::int64_t k = 0; k < a.K; ++k) {
@@ -739,6 +742,14 @@ __global__ __launch_bounds__(256) void portable_kernel(LinearArgs a, int tiled) 
         }
         const float s = meta_load(static_cast<const ST*>(a.scales), meta);
         float w = static_cast<float>(c) * s;
+        if (a.parity) {
+            // runtime::parity::packed_linear (parity_math.cpp:247-277): x on the calibration grid, w = c * s, one
+            // fused multiply-add per column in order
+            const float xv = clampf(__builtin_rintf(load_act(a.x, a.x_type, m * a.K + k) / a.input_scale), -128.F, 127.F) *
+                             a.input_scale;
+            acc = __builtin_fmaf(xv, w, acc);
+            continue;
+        }
         if (a.zero_mode == ZERO_POINT) {
             int zp;
             if (tiled) zp = (a.zero_points[(meta - n % kTileRows) / 2 + (n % kTileRows) / 2] >> (4 * (n & 1))) & 15;
@@ -751,7 +762,20 @@ __global__ __launch_bounds__(256) void portable_kernel(LinearArgs a, int tiled) 
         if (a.input_scale > 0.F) xv = clampf(__builtin_rintf(xv / a.input_scale), -128.F, 127.F) * a.input_scale;
         acc = acc + xv * w;
     }
-    a.y[m * a.N + n] = calibrate_output(acc, a.output_scale);
+    return calibrate_output(acc, a.output_scale);
+}
+
+// Kidi's portable float path (PortablePackedLinearOp, operators.cpp:2639-2713): w = c*s (+ z), activations
+// statically rounded when input_scale > 0, fp32 sum over k in order, output rounding. One thread per output; with
+// a.gelu one thread per gated output (gate row i and up row i + N/2).
+template <int BITS, typename ST>
+__global__ __launch_bounds__(256) void portable_kernel(LinearArgs a, int tiled) {
+    const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const std::int64_t cols = a.gelu ? a.N / 2 : a.N;
+    if (id >= a.M * cols) return;
+    const std::int64_t m = id / cols, n = id % cols;
+    if (a.gelu) a.y[id] = gelu_tanh(portable_output<BITS, ST>(a, tiled, m, n)) * portable_output<BITS, ST>(a, tiled, m, n + cols);
+    else a.y[id] = portable_output<BITS, ST>(a, tiled, m, n);
 }
 
 // GELU-tanh gating over a [M, 2I] buffer (used after the GEMM / row-major / portable kernels).
@@ -838,7 +862,7 @@ hipError_t launch_tiled(const LinearCall& c, hipStream_t stream) {
 template <int BITS, typename ST>
 hipError_t launch_rowmajor(const LinearCall& c, hipStream_t stream) {
     LinearArgs a = make_linear_args(c);
-    const std::int64_t total = c.M * c.w->geo.rows;
+    const std::int64_t total = c.M * (c.gelu_gate ? c.w->geo.rows / 2 : c.w->geo.rows);
     hipLaunchKernelGGL((rowmajor_kernel<BITS, ST>), dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
@@ -846,7 +870,7 @@ hipError_t launch_rowmajor(const LinearCall& c, hipStream_t stream) {
 template <int BITS, typename ST>
 hipError_t launch_portable(const LinearCall& c, hipStream_t stream) {
     LinearArgs a = make_linear_args(c);
-    const std::int64_t total = c.M * c.w->geo.rows;
+    const std::int64_t total = c.M * (c.gelu_gate ? c.w->geo.rows / 2 : c.w->geo.rows);
     hipLaunchKernelGGL((portable_kernel<BITS, ST>), dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, a,
                        c.w->tiled ? 1 : 0);
     return hipGetLastError();
@@ -974,6 +998,7 @@ LinearArgs make_linear_args(const LinearCall& c) {
     a.zero_half = w.zero_type == META_F16;
     a.is_static = c.path == PATH_SYMMETRIC;
     a.gelu = c.gelu_gate;
+    a.parity = c.parity ? 1 : 0;
     a.input_scale = c.input_scale;
     a.output_scale = c.output_scale;
     a.dq_codes = c.dq_codes;

@@ -582,21 +582,6 @@ int lds_limit() {
     return g_lds_limit;
 }
 
-// Launch-shape overrides for tuning sweeps: KQ_SKINNY_WAVES (waves per workgroup, a power of two <= 16) and
-// KQ_SKINNY_ROWS (row tiles per workgroup, 1 or 2). Read once; unset means the heuristic.
-int env_int(const char* name) {
-    const char* v = std::getenv(name);
-    return v ? std::atoi(v) : 0;
-}
-int tune_waves() {
-    static const int v = env_int("KQ_SKINNY_WAVES");
-    return v;
-}
-int tune_rows() {
-    static const int v = env_int("KQ_SKINNY_ROWS");
-    return v;
-}
-
 int align16(int v) { return (v + 15) / 16 * 16; }
 bool pow2(std::int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 int log2i(std::int64_t v) {
@@ -625,13 +610,11 @@ bool skinny_plan(const LinearCall& c, SkinnyPlan& p) {
         return false;
     // two row tiles per workgroup when there are enough of them (halves the redundant activation quantization)
     p.R = c.gelu_gate ? 2 : 1;
-    if (!c.gelu_gate && tune_rows() > 0) p.R = tune_rows() == 2 ? 2 : 1;
     if (c.gelu_gate && (w.geo.rows / 2) % kTileRows) return false;
     p.blocks = c.gelu_gate ? w.geo.n_tiles / 2 : (w.geo.n_tiles + p.R - 1) / p.R;
     // waves: about 4096 over the chip (four per SIMD), whole units per wave, a power of two
     int W = static_cast<int>(std::max<std::int64_t>(1, 4096 / std::max<std::int64_t>(1, p.blocks)));
     W = std::min({W, kMaxWaves, units});
-    if (tune_waves() > 0) W = std::min({tune_waves(), kMaxWaves, units});
     W = 1 << log2i(W);
     const int per_wave_tiles = (units + W - 1) / W * tpu;
     p.T = 4;

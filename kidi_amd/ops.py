@@ -247,6 +247,21 @@ class DeviceWeight:
         y = y.reshape(*x.shape[:-1], width)
         return y, (hidden.reshape(x.shape) if hidden is not None else None)
 
+    def route(self, x: torch.Tensor, input_scale: float = 0.0, gelu_gate: bool = False) -> str:
+        """Name of the projection kernel ``linear`` runs for x (kq_debug_route), without running it."""
+        x2 = x.reshape(-1, self.cols)
+        m = x2.shape[0]
+        a = N.LinearArgs()
+        a.x = x2.data_ptr()
+        a.x_dtype = N.KQ_BF16 if x2.dtype == torch.bfloat16 else N.KQ_F32
+        a.m = m
+        a.input_scale = input_scale
+        a.y = 1  # any non-null pointer: nothing is written
+        r = N.load().kq_debug_route(self.handle, ctypes.byref(a), int(bool(gelu_gate)))
+        if r < 0:
+            raise Failure("INVALID_ARGUMENT", N.load().kq_last_error().decode())
+        return N.ROUTE_NAMES[r]
+
     def debug_partials(self, x: torch.Tensor, input_scale: float = 0.0, output_scale: float = 0.0):
         """(y, int32 partials [M, N, K/g]) from the same kernel as ``linear``."""
         x2 = x.reshape(-1, self.cols).contiguous()
@@ -364,6 +379,13 @@ def _identity(t: torch.Tensor | None):
     return (t.device.type, t.untyped_storage().data_ptr(), t.storage_offset(), tuple(t.shape), t.dtype)
 
 
+# core::InferencePrecision values this library serves (src/kidi/core/precision.h:8-22, names :66-80). CHECKPOINT
+# runs PACKED_LINEAR (the operator); LOWBIT_PARITY runs runtime::parity::packed_linear. Kidi's other precisions
+# dequantize the weight and run a dense LINEAR on a host device (ops/context.cpp:832-916), outside this library.
+CHECKPOINT, LOWBIT_PARITY = "checkpoint", "lowbit-parity"
+_PRECISION_NAMES = {"checkpoint": CHECKPOINT, "lowbit-parity": LOWBIT_PARITY, "checkpoint-parity": LOWBIT_PARITY}
+
+
 class Context:
     """The packed-linear slice of ops::Context on one HIP device."""
 
@@ -371,6 +393,7 @@ class Context:
 
     def __init__(self, device: str | torch.device = "cuda"):
         self.device = torch.device(device)
+        self.precision = CHECKPOINT
         self._prepared: collections.OrderedDict = collections.OrderedDict()
         self._zeros: dict = {}
         self._bound: dict = {}  # weight storage -> (source, PackedWeight, packed_prefill, asymmetric_clip)
@@ -415,6 +438,14 @@ class Context:
                 return self.packed_linear(input, p.values, p.scales, p.bits, p.group_size, 0.0, 0.0, p.zeros)
         raise Failure("UNSUPPORTED", "dense LINEAR is outside the packed projection library")
 
+    def set_precision(self, precision: str) -> None:
+        """Context::set_precision (ops/context.h): "checkpoint" or "lowbit-parity" (also "checkpoint-parity",
+        core::parse_precision, precision.h:74). The dense-dequantized precisions are UNSUPPORTED here."""
+        found = _PRECISION_NAMES.get(precision)
+        if found is None:
+            raise Failure("UNSUPPORTED", "selected precision requires CPU packed weights with compatible group scales")
+        self.precision = found
+
     def bind_packed_zero(self, scales: torch.Tensor, zeros: torch.Tensor) -> None:
         """Context::bind_packed_zero (ops/context.cpp:813-815)."""
         if scales is not None and zeros is not None:
@@ -450,7 +481,10 @@ class Context:
     def packed_linear(self, input: torch.Tensor, weight: torch.Tensor, scales: torch.Tensor, bits: int,
                       group_size: int, input_scale: float = 0.0, output_scale: float = 0.0,
                       zeros: torch.Tensor | None = None) -> torch.Tensor:
-        """Context::packed_linear (ops/context.cpp:821-939) for CHECKPOINT precision: F32 [..., N] output."""
+        """Context::packed_linear (ops/context.cpp:821-939): PACKED_LINEAR under CHECKPOINT precision, Kidi's
+        LOWBIT_PARITY projection under that precision (:917-932). F32 [..., N] output."""
+        if self.precision == LOWBIT_PARITY:
+            return self._lowbit_parity(input, weight, scales, bits, group_size, input_scale, output_scale)
         self._validate(input, weight, scales, bits, group_size, input_scale, output_scale)
         bound = zeros if zeros is not None else self._zeros.get(_identity(scales))
         dw = self._prepare(weight, scales, bits, group_size, bound)
@@ -460,6 +494,31 @@ class Context:
         if host:  # a HIP op behind a CPU tensor returns host-visible results (synchronous)
             y = y.cpu()
         return y
+
+    def _lowbit_parity(self, input, weight, scales, bits, group_size, input_scale, output_scale):
+        # Context::packed_linear's scale check (ops/context.cpp:824-825), its LOWBIT_PARITY domain (:919-929), then
+        # runtime::parity::packed_linear (kq_lowbit_parity_linear). Bound zeros are not passed in this mode.
+        if not math.isfinite(input_scale) or input_scale < 0 or not math.isfinite(output_scale) or output_scale < 0:
+            raise Failure("INVALID_ARGUMENT", "invalid calibrated projection scales")
+        per = 8 // bits if bits in (2, 4, 8) else 0
+        width = weight.shape[1] * per if weight.dim() == 2 else 0
+        groups = width // group_size if group_size > 0 else 0
+        if (not per or input.dtype != torch.float32 or input.dim() == 0 or input_scale <= 0 or output_scale <= 0
+                or group_size <= 0 or width != input.shape[-1] or width % group_size or weight.dim() != 2
+                or weight.dtype != torch.uint8 or scales.dtype != torch.float32
+                or scales.numel() != weight.shape[0] * groups or input.numel() // max(width, 1) > 2**31 - 1
+                or width > 2**31 - 1 or weight.shape[0] > 2**31 - 1):
+            raise Failure("UNSUPPORTED", "lowbit-parity requires calibrated CPU packed weights with compatible group scales")
+        dw = self._prepare(weight, scales.reshape(weight.shape[0], groups), bits, group_size, None)
+        host = not input.is_cuda
+        x = (input.to(self.device) if host else input).reshape(-1, width).contiguous()
+        y = torch.empty((x.shape[0], weight.shape[0]), dtype=torch.float32, device=x.device)
+        a = N.LinearArgs()
+        a.x, a.x_dtype, a.m = x.data_ptr(), N.KQ_F32, x.shape[0]
+        a.input_scale, a.output_scale, a.y = input_scale, output_scale, y.data_ptr()
+        _raise(N.load().kq_lowbit_parity_linear(dw.handle, ctypes.byref(a), _stream()))
+        y = y.reshape(*input.shape[:-1], weight.shape[0])
+        return y.cpu() if host else y
 
     def packed_linear_gelu_gate(self, input: torch.Tensor, weight: torch.Tensor, scales: torch.Tensor, bits: int,
                                 group_size: int, input_scale: float = 0.0, output_scale: float = 0.0,

@@ -24,6 +24,10 @@
 //                           expected value); portable float path pinned to 1e-3 / 0.05 by eager_test.cpp:300-378.
 //   kqr_gelu_tanh           pinned by eager_test.cpp:431-452 (formula to 1e-5 and exact saturation values).
 //   kqr_silu_gate           pinned by eager_test.cpp:167-186 (g / (1 + exp(-g)) * up to 1e-5).
+//   kqr_parity_linear       pinned: precision_test.cpp:87-92 LOWBIT_PARITY KAT (exact outputs 0.4, 0) and the
+//                           reference's own cross-check graph_test.cpp:158-177 (LOWBIT_PARITY within 1e-5 of the
+//                           calibrated SymmetricPackedLinear path); bit-exact to parity_math.cpp for M < 8 (serial
+//                           FMA), while for M >= 8 the reference sums with Accelerate's sgemm, whose order is unknown.
 //   kqr_rms_norm            pinned: eager_test.cpp:388-412 KAT (plain, 2x weight, residual, scaled; zero row
 //                           exactly 0), cuda/operators_test.cpp:346-350 identity (residual form == (norm + r) * s
 //                           exactly), float64 closed form to a few ulp, power-of-two weight scaling exact. The
@@ -538,6 +542,36 @@ float rms_sum_squares(const float* x, std::int64_t width) {
         total = seg == 0 ? piece[0] : total + piece[0];
     }
     return total;
+}
+
+// Kidi's LOWBIT_PARITY projection, runtime::parity::packed_linear (src/kidi/runtime/parity_math.cpp:226-291), reached
+// from Context::packed_linear under InferencePrecision::LOWBIT_PARITY (ops/context.cpp:917-932): activations rounded
+// to the calibration grid (nearbyint(x / input_scale) clamped to [-128, 127], times input_scale, :247-250), weights
+// dequantized to c * s (:259-260; bound zeros are not applied in this mode), each output a serial FMA over the columns
+// in order (:269-277), then the output rounded to the output_scale grid (:279-282). x F32 [M, K], values U8 Kidi
+// layout, scales F32 [N, K/g], y F32 [M, N]. Returns 0; 1 (INVALID_ARGUMENT) for a non-finite or non-positive scale
+// (:239-240); 2 (UNSUPPORTED) outside the domain Context::packed_linear checks (:919-929).
+int kqr_parity_linear(const float* x, std::int64_t M, std::int64_t K, const std::uint8_t* values, std::int64_t N, int bits,
+                      std::int64_t group, const float* scales, float input_scale, float output_scale, float* y) {
+    if ((bits != 2 && bits != 4 && bits != 8) || group <= 0 || K <= 0 || K % group || group % (8 / bits) || N <= 0 ||
+        M < 0 || !(input_scale > 0.F) || !(output_scale > 0.F) || !std::isfinite(input_scale) ||
+        !std::isfinite(output_scale) || M > INT32_MAX || K > INT32_MAX || N > INT32_MAX)
+        return 2;
+    const std::int64_t B = K / group, row_bytes = K / (8 / bits);
+    for (std::int64_t i = 0; i < N * B; ++i)
+        if (!std::isfinite(scales[i]) || !(scales[i] > 0.F)) return 1;
+    std::vector<float> xr(static_cast<std::size_t>(M * K)), w(static_cast<std::size_t>(K));
+    for (std::int64_t i = 0; i < M * K; ++i) xr[static_cast<std::size_t>(i)] = clampf(std::nearbyint(x[i] / input_scale), -128.F, 127.F) * input_scale;
+    for (std::int64_t n = 0; n < N; ++n) {
+        for (std::int64_t k = 0; k < K; ++k)
+            w[static_cast<std::size_t>(k)] = static_cast<float>(code_at(values + n * row_bytes, bits, k)) * scales[n * B + k / group];
+        for (std::int64_t m = 0; m < M; ++m) {
+            float v = 0.F;
+            for (std::int64_t k = 0; k < K; ++k) v = std::fma(xr[static_cast<std::size_t>(m * K + k)], w[static_cast<std::size_t>(k)], v);
+            y[m * N + n] = clampf(std::nearbyint(v / output_scale), -128.F, 127.F) * output_scale;
+        }
+    }
+    return 0;
 }
 
 // x and residual are F32 or BF16 [rows, width] (residual may be NULL: RMS_NORM); weight F32 [width]; scale NULL or

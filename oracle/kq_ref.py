@@ -59,6 +59,8 @@ def lib() -> ctypes.CDLL:
         L.kqr_silu_gate.restype = None
         L.kqr_rms_norm.argtypes = [vp, i32, i64, i64, vp, vp, vp, f32, vp, vp]
         L.kqr_rms_norm.restype = i32
+        L.kqr_parity_linear.argtypes = [vp, i64, i64, vp, i64, i32, i64, vp, f32, f32, vp]
+        L.kqr_parity_linear.restype = i32
         _lib = L
     return _lib
 
@@ -192,6 +194,24 @@ def packed_linear(x: np.ndarray, values: np.ndarray, scales: np.ndarray, bits: i
     if path < 0:
         raise ValueError("packed linear shape or dtype mismatch")
     return y, path
+
+
+def parity_linear(x: np.ndarray, values: np.ndarray, scales: np.ndarray, bits: int, group_size: int,
+                  input_scale: float, output_scale: float) -> np.ndarray:
+    """Kidi's LOWBIT_PARITY projection (runtime/parity_math.cpp:226-291): calibrated input grid, c * s weights, serial
+    FMA per output, output grid. Raises ValueError("INVALID_ARGUMENT" / "UNSUPPORTED") as the reference fails."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    v = np.ascontiguousarray(values, dtype=np.uint8)
+    N = v.shape[0]
+    s = np.ascontiguousarray(scales, dtype=np.float32)
+    y = np.zeros((M, N), np.float32)
+    st = lib().kqr_parity_linear(_p(x), M, K, _p(v), N, bits, group_size, _p(s), input_scale, output_scale, _p(y))
+    if st == 1:
+        raise ValueError("INVALID_ARGUMENT")
+    if st == 2:
+        raise ValueError("UNSUPPORTED")
+    return y
 
 
 def gelu_gate(gate_up: np.ndarray) -> np.ndarray:

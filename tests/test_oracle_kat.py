@@ -331,3 +331,64 @@ def test_dynamic_linear_closed_form(ref):
     xd = (q.astype(np.float64) - np.repeat(zpa, g, axis=1)) * np.repeat(a_s, g, axis=1)
     want = xd @ (c8.astype(np.float64) * np.repeat(s8, g, axis=1)).T
     assert np.max(np.abs(y - want)) <= 1e-5 * np.max(np.abs(want))
+
+
+def _graph_test_operands(bits, m_rows):
+    """tests/kidi/runtime/ynn/graph_test.cpp:120-135: INPUT_SIZE 128, INTERMEDIATE 2056, gate_up bytes
+    (i * 11 + 7) & 0xFF, x = ((i * 5) % 19 - 9) / 16, per-channel scales (1 + i % 5) / 256."""
+    K, I = 128, 2056
+    per = 8 // bits
+    x = ((np.arange(m_rows * K) * 5) % 19 - 9).astype(np.float32).reshape(m_rows, K) * np.float32(0.0625)
+    gu = ((np.arange(2 * I * (K // per)) * 11 + 7) & 0xFF).astype(np.uint8).reshape(2 * I, K // per)
+    s = (np.float32(0.00390625) * (1 + np.arange(2 * I) % 5).astype(np.float32)).reshape(2 * I, 1)
+    return x, gu, s
+
+
+def test_lowbit_parity_kat(ref):
+    """tests/kidi/layers/precision_test.cpp:59-64, :87-92: LOWBIT_PARITY on x [0.15, -0.2], 8-bit weights
+    [[2, -2], [1, 1]], scales [0.5, 0.25], g = 2, input and output scales 0.1 -> [0.4, 0]."""
+    x = np.array([[0.15, -0.2]], np.float32)
+    w = np.array([[2, 254], [1, 1]], np.uint8)
+    s = np.array([[0.5], [0.25]], np.float32)
+    y = ref.parity_linear(x, w, s, 8, 2, 0.1, 0.1)
+    assert abs(y[0, 0] - 0.4) < 1e-5 and abs(y[0, 1]) < 1e-5
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("m_rows", [1, 17])
+def test_lowbit_parity_matches_calibrated_path(ref, bits, m_rows):
+    """graph_test.cpp:158-177: the calibrated SymmetricPackedLinear output equals LOWBIT_PARITY within 1e-5 (input
+    scale 0.125, output scale 0.0625, g = K = 128)."""
+    x, gu, s = _graph_test_operands(bits, m_rows)
+    fast, path = ref.packed_linear(x, gu, s, bits, 128, 0.125, 0.0625)
+    assert path == ref.PATH_SYMMETRIC
+    parity = ref.parity_linear(x, gu, s, bits, 128, 0.125, 0.0625)
+    assert np.max(np.abs(fast - parity)) <= 1e-5
+
+
+def test_lowbit_parity_serial_fma_and_domain(ref):
+    """The serial form: a float64 dot of grid-rounded x and c * s matches to the float32 rounding of the running FMA
+    chain; non-positive scales are INVALID_ARGUMENT, a zero input or output scale UNSUPPORTED (parity_math.cpp:239-240,
+    ops/context.cpp:919-929)."""
+    rng = np.random.default_rng(3)
+    K, N, g = 256, 64, 32
+    codes = rng.integers(-8, 8, size=(N, K)).astype(np.int8)
+    from tests.cases import pack_codes
+
+    v = pack_codes(codes, 4)
+    s = rng.uniform(0.01, 0.02, size=(N, K // g)).astype(np.float32)
+    x = rng.standard_normal((3, K)).astype(np.float32)
+    in_s, out_s = 0.05, 1e-4
+    y = ref.parity_linear(x, v, s, 4, g, in_s, out_s)
+    xr = np.clip(np.rint(x / np.float32(in_s)), -128, 127).astype(np.float64) * np.float32(in_s)
+    w = codes.astype(np.float64) * np.repeat(s.astype(np.float64), g, axis=1)
+    exact = np.clip(np.rint((xr @ w.T) / out_s), -128, 127) * out_s
+    assert np.max(np.abs(y - exact)) <= out_s * 1.0001  # at most one output step where the chain rounds across
+    bad = s.copy()
+    bad[3, 1] = 0.0
+    with pytest.raises(ValueError, match="INVALID_ARGUMENT"):
+        ref.parity_linear(x, v, bad, 4, g, in_s, out_s)
+    with pytest.raises(ValueError, match="UNSUPPORTED"):
+        ref.parity_linear(x, v, s, 4, g, 0.0, out_s)
+    with pytest.raises(ValueError, match="UNSUPPORTED"):
+        ref.parity_linear(x, v, s, 4, g, in_s, 0.0)
