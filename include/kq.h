@@ -123,6 +123,14 @@ size_t kq_linear_workspace_size(const kq_weight* weight, int64_t m);
  * Asynchronous on `stream`. */
 kq_status kq_packed_linear(const kq_weight* weight, const kq_linear_args* args, void* stream);
 
+/* kq_packed_linear without any allocation, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. args->workspace is
+ * ignored: the workspace is a static device array of the library (64 MiB per device, held until the process ends),
+ * and a call whose kq_linear_workspace_size() exceeds it returns KQ_INVALID_ARGUMENT without running. Calls on one
+ * stream are ordered; calls that overlap on one device (several streams) share the array and race. Results equal
+ * kq_packed_linear's. */
+kq_status kq_packed_linear_noalloc(const kq_weight* weight, const kq_linear_args* args, void* stream);
+
 /* Fused projections that share one activation read (Kidi fuses gate+up and k+v by concatenating rows,
  * model/gemma4.cpp:308-322; its CUDA backend groups projections with one input, runtime/cuda/operators.cpp:366-437):
  * kq_weight_pack_concat packs `count` weights with equal bits, group and K into one weight whose rows are the

@@ -28,7 +28,7 @@ EXPORTS = (
     "kq_greedy_workspace_size", "kq_greedy_token", "kq_greedy_linear_workspace_size", "kq_packed_linear_greedy",
     "kq_weight_export_size", "kq_weight_export", "kq_weight_import", "kq_rms_norm", "kq_rms_linear_workspace_size",
     "kq_packed_linear_rms", "kq_quantize_weight", "kq_debug_read_floor", "kq_debug_route", "kq_debug_route_shape",
-    "kq_lowbit_parity_linear",
+    "kq_lowbit_parity_linear", "kq_packed_linear_noalloc",
 )
 
 # kq_debug_route values: the kernel sequence a projection call runs
@@ -177,6 +177,8 @@ def load() -> ctypes.CDLL:
     L.kq_quantize_weight.restype = ctypes.c_int
     L.kq_debug_read_floor.argtypes = [vp, ctypes.c_size_t, vp, vp]
     L.kq_debug_read_floor.restype = ctypes.c_int
+    L.kq_packed_linear_noalloc.argtypes = [vp, ctypes.POINTER(LinearArgs), vp]
+    L.kq_packed_linear_noalloc.restype = ctypes.c_int
     L.kq_lowbit_parity_linear.argtypes = [vp, ctypes.POINTER(LinearArgs), vp]
     L.kq_lowbit_parity_linear.restype = ctypes.c_int
     L.kq_debug_route.argtypes = [vp, ctypes.POINTER(LinearArgs), i32]

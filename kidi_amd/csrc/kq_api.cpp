@@ -598,6 +598,8 @@ std::size_t split_bytes(const Weight& w, std::int64_t M) {
 }
 }  // namespace
 
+int set_error(int code, const char* message) { return fail(static_cast<kq_status>(code), message); }
+
 bool gelu_needs_temp(const Weight& w) { return w.tiled && w.geo.rows % 2 == 0 && (w.geo.rows / 2) % kTileRows != 0; }
 
 std::size_t workspace_bytes(const Weight& w, std::int64_t M) {

@@ -152,6 +152,9 @@ hipError_t launch_gemm_i4g(const LinearCall& c, hipStream_t stream);
 hipError_t launch_gemm_i4g_quantize_dump(const LinearCall& c, std::int8_t* codes, float* scales, std::int32_t* sums,
                                          std::int32_t* zero_points, hipStream_t stream);
 
+// Records `message` as this thread's kq_last_error() and returns `code` (a kq_status value).
+int set_error(int code, const char* message);
+
 std::size_t workspace_bytes(const Weight& w, std::int64_t M);
 // GELU gating runs after the projection (through ActBuffers::gelu_tmp) only for tiled weights whose gate/up split
 // falls inside a 16-row tile; every other path fuses it.
