@@ -12,7 +12,7 @@ import subprocess
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["csrc/kq_kernels.hip", "csrc/kq_skinny.hip", "csrc/kq_decode.hip", "csrc/kq_gemm.hip", "csrc/kq_gemm_g.hip", "csrc/kq_greedy.hip", "csrc/kq_norm.hip", "csrc/kq_pack.hip", "csrc/kq_noalloc.hip", "csrc/kq_api.cpp", "csrc/kq_layout_host.cpp"]
+SOURCES = ["csrc/kq_kernels.hip", "csrc/kq_skinny.hip", "csrc/kq_decode.hip", "csrc/kq_gemm.hip", "csrc/kq_gemm_g.hip", "csrc/kq_gemm8.hip", "csrc/kq_greedy.hip", "csrc/kq_norm.hip", "csrc/kq_pack.hip", "csrc/kq_noalloc.hip", "csrc/kq_api.cpp", "csrc/kq_layout_host.cpp"]
 LIB = os.path.join(HERE, "lib", "libkq_hip.so")
 # Per-source flags: the decode kernels take their first nine scalar arguments preloaded into SGPRs at wave launch
 # (gfx950 kernel-argument preloading; on firmware without it the code object's preamble loads them as usual).

@@ -203,6 +203,49 @@ ImageLayout image_layout(const kq::Weight& w) {
     return l;
 }
 
+// Prefill copy of a 4-bit g = 128 weight for kq_gemm8.hip (layout in kq_internal.hpp): codes[N][K] signed, zp[N][K/g]
+// uint4 zero points (ZERO_POINT) or null, zeros[N][K/g] additive zeros (ZERO_FLOAT) or null. Column k of a 32-column
+// chunk sits at lane half (k >> 3) & 1, byte (k & 7) + 8 (k >> 4) of the column's 16-byte lane slot.
+std::vector<std::uint8_t> build_prefill(const kq::Weight& w, const std::int8_t* codes, const float* scales,
+                                        const std::uint8_t* zp, const float* zeros, std::size_t* codes_bytes) {
+    const std::int64_t N = w.geo.rows, K = w.geo.cols, B = K / w.geo.group, NB = (N + 31) / 32, KC = K / 32;
+    *codes_bytes = align_up(static_cast<std::size_t>(NB * KC) * 1024);
+    std::vector<std::uint8_t> out(*codes_bytes + static_cast<std::size_t>(B * NB * 32) * 16, 0);
+    for (std::int64_t n = 0; n < N; ++n) {
+        const std::int64_t nb = n / 32, c = n % 32;
+        for (std::int64_t k = 0; k < K; ++k) {
+            const int kk = static_cast<int>(k % 32);
+            const std::int64_t lane = c + 32 * ((kk >> 3) & 1), p = (kk & 7) + 8 * (kk >> 4);
+            int v = codes[n * K + k];
+            if (zp) v += 8 - zp[n * B + k / w.geo.group];
+            out[static_cast<std::size_t>(((nb * KC + k / 32) * 64 + lane) * 16 + p)] = static_cast<std::uint8_t>(static_cast<std::int8_t>(v));
+        }
+        for (std::int64_t b = 0; b < B; ++b) {
+            const float rec[4] = {scales[n * B + b], -12582912.F * scales[n * B + b], zeros ? zeros[n * B + b] : 0.F, 0.F};
+            std::memcpy(out.data() + *codes_bytes + static_cast<std::size_t>(((b * NB + nb) * 32 + c) * 16), rec, 16);
+        }
+    }
+    return out;
+}
+
+// Uploads a prefill copy into its own allocation (synchronous on `stream`).
+kq_status upload_prefill(kq::Weight& w, const std::vector<std::uint8_t>& img, std::size_t codes_bytes, hipStream_t stream) {
+    hipError_t e = hipMalloc(&w.prefill_alloc, img.size());
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(prefill copy)");
+    e = hipMemcpyAsync(w.prefill_alloc, img.data(), img.size(), hipMemcpyHostToDevice, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) {
+        (void)hipFree(w.prefill_alloc);
+        w.prefill_alloc = nullptr;
+        return hip_fail(e, "upload prefill copy");
+    }
+    w.prefill_bytes = img.size();
+    w.has_prefill = true;
+    w.prefill_codes = static_cast<std::int8_t*>(w.prefill_alloc);
+    w.prefill_meta = reinterpret_cast<float*>(static_cast<std::uint8_t*>(w.prefill_alloc) + codes_bytes);
+    return KQ_OK;
+}
+
 struct HostWeight {
     std::vector<std::uint8_t> values;  // Kidi layout, all descriptors concatenated by rows
     std::vector<std::uint8_t> scales;  // [N][B] of the scale dtype
@@ -390,6 +433,26 @@ kq_status pack_impl(const kq_pack_desc* descs, int count, void* stream, kq_weigh
     if (w->zero_mode == kq::ZERO_POINT) w->zero_points = base + zp_off;
     if (w->zero_mode == kq::ZERO_FLOAT) w->zeros = base + zeros_off;
     if (w->tiled && bits == 8) w->code_sums = reinterpret_cast<std::int32_t*>(base + cs_off);
+    if (kq::gemm8_eligible(*w)) {
+        std::vector<std::int8_t> codes(static_cast<std::size_t>(N * K));
+        std::vector<float> sc(static_cast<std::size_t>(N * B)), zf;
+        for (std::int64_t n = 0; n < N; ++n)
+            for (std::int64_t k = 0; k < K; ++k)
+                codes[static_cast<std::size_t>(n * K + k)] = static_cast<std::int8_t>(kq::kidi_code(hw.values.data() + n * row_bytes, bits, k));
+        for (std::int64_t i = 0; i < N * B; ++i) sc[static_cast<std::size_t>(i)] = scale_at(i);
+        if (w->zero_mode == kq::ZERO_FLOAT) {
+            zf.resize(static_cast<std::size_t>(N * B));
+            for (std::int64_t i = 0; i < N * B; ++i) zf[static_cast<std::size_t>(i)] = zero_at(i);
+        }
+        std::size_t cb = 0;
+        const auto img = build_prefill(*w, codes.data(), sc.data(), w->zero_mode == kq::ZERO_POINT ? zp.data() : nullptr,
+                                       zf.empty() ? nullptr : zf.data(), &cb);
+        if (kq_status s = upload_prefill(*w, img, cb, st); s != KQ_OK) {
+            (void)hipFree(w->allocation);
+            delete w;
+            return s;
+        }
+    }
     *out = reinterpret_cast<kq_weight*>(w);
     return KQ_OK;
 }
@@ -432,6 +495,7 @@ kq::Route route_of(const kq::LinearCall& c, kq::SkinnyPlan* plan) {
         if (plan) *plan = p;
         return kq::ROUTE_SKINNY;
     }
+    if (kq::gemm8_fits(c)) return kq::ROUTE_GEMM8;
     if (kq::gemm_i4_fits(c)) return kq::ROUTE_GEMM_I4;
     if (kq::gemm_i4g_fits(c)) return kq::ROUTE_GEMM_I4G;
     if (c.path == kq::PATH_PORTABLE) return kq::ROUTE_PORTABLE;
@@ -464,6 +528,11 @@ kq_status run_call(kq::LinearCall& c, const kq_linear_args* args, std::size_t ws
             return s;
         }
         c.act = kq::carve_workspace(*c.w, c.M, ws);
+    }
+    // Prefill, 4-bit g = 128 from the weight's prefill copy: quantizer + int8 GEMM (GELU gate fused).
+    if (route == kq::ROUTE_GEMM8) {
+        e = kq::launch_gemm8(c, c.act, stream);
+        return e == hipSuccess ? KQ_OK : hip_fail(e, "prefill projection launch");
     }
     // Prefill, 4-bit g = 128: quantizer + int8 MFMA GEMM (GELU gate fused).
     if (route == kq::ROUTE_GEMM_I4) {
@@ -585,8 +654,13 @@ namespace {
 // where that GEMM does not run or does not split.
 std::size_t split_bytes(const Weight& w, std::int64_t M) {
     std::size_t partial = 0;
+    if (gemm8_eligible(w) && M > 16) {
+        partial = gemm8_partial_bytes(w, M, false);
+        if (w.geo.rows % 64 == 0) partial = std::max(partial, gemm8_partial_bytes(w, M, true));
+        partial = align_up(partial);
+    }
     if (!w.tiled || w.geo.bits != 4 || w.geo.group != 128 || M <= 16 || w.geo.cols % 512 || w.geo.cols_p != w.geo.cols)
-        return 0;
+        return partial;
     for (int gelu = 0; gelu < 2; ++gelu) {
         if (gelu && ((w.geo.rows / 2) % kTileRows || w.geo.n_tiles % 2)) continue;
         const GemmPlan p = gemm_i4_plan(w, M, gelu != 0);
@@ -761,6 +835,44 @@ kq_status kq_weight_import(const void* host, size_t bytes, void* stream, kq_weig
     w->zero_points = at(h.zero_points);
     w->zeros = at(h.zeros);
     w->code_sums = reinterpret_cast<std::int32_t*>(at(h.code_sums));
+    if (kq::gemm8_eligible(*w)) {  // the prefill copy is derived from the image, not stored in the blob
+        const auto* img = static_cast<const std::uint8_t*>(host) + sizeof(h);
+        const std::int64_t N = h.rows, K = h.cols, B = K / h.group;
+        std::vector<std::int8_t> codes(static_cast<std::size_t>(N * K));
+        kq::decode_tiles(h.bits, N, K, img + h.tiles, codes.data());
+        std::vector<float> sc(static_cast<std::size_t>(N * B)), zf;
+        std::vector<std::uint8_t> zpv;
+        auto meta_float = [&](std::int64_t off, int type, std::int64_t i) {
+            float f;
+            if (type == kq::META_F16) {
+                std::uint16_t hb;
+                std::memcpy(&hb, img + off + 2 * i, 2);
+                f = half_bits_to_float(hb);
+            } else {
+                std::memcpy(&f, img + off + 4 * i, 4);
+            }
+            return f;
+        };
+        if (h.zero_mode == kq::ZERO_POINT) zpv.resize(static_cast<std::size_t>(N * B));
+        if (h.zero_mode == kq::ZERO_FLOAT) zf.resize(static_cast<std::size_t>(N * B));
+        for (std::int64_t n = 0; n < N; ++n)
+            for (std::int64_t b = 0; b < B; ++b) {
+                const std::int64_t mi = w->geo.meta_index(n, b), i = n * B + b;
+                sc[static_cast<std::size_t>(i)] = meta_float(h.scales, h.scale_type, mi);
+                if (h.zero_mode == kq::ZERO_POINT)
+                    zpv[static_cast<std::size_t>(i)] = static_cast<std::uint8_t>(
+                        (img[h.zero_points + (mi - n % kq::kTileRows) / 2 + (n % kq::kTileRows) / 2] >> (4 * (n & 1))) & 15);
+                if (h.zero_mode == kq::ZERO_FLOAT) zf[static_cast<std::size_t>(i)] = meta_float(h.zeros, h.zero_type, mi);
+            }
+        std::size_t cb = 0;
+        const auto pimg = build_prefill(*w, codes.data(), sc.data(), zpv.empty() ? nullptr : zpv.data(),
+                                        zf.empty() ? nullptr : zf.data(), &cb);
+        if (kq_status s = upload_prefill(*w, pimg, cb, static_cast<hipStream_t>(stream)); s != KQ_OK) {
+            (void)hipFree(w->allocation);
+            delete w;
+            return s;
+        }
+    }
     *out = reinterpret_cast<kq_weight*>(w);
     return KQ_OK;
 }
@@ -769,6 +881,7 @@ void kq_weight_free(kq_weight* weight) {
     if (!weight) return;
     auto* w = reinterpret_cast<kq::Weight*>(weight);
     if (w->allocation) (void)hipFree(w->allocation);
+    if (w->prefill_alloc) (void)hipFree(w->prefill_alloc);
     delete w;
 }
 
@@ -781,7 +894,7 @@ kq_status kq_weight_info(const kq_weight* weight, int32_t* bits, int32_t* group_
     if (rows) *rows = w.geo.rows;
     if (cols) *cols = w.geo.cols;
     if (has_zeros) *has_zeros = w.zero_mode != kq::ZERO_NONE;
-    if (device_bytes) *device_bytes = w.bytes;
+    if (device_bytes) *device_bytes = w.bytes + w.prefill_bytes;
     return KQ_OK;
 }
 
@@ -1010,7 +1123,20 @@ kq_status kq_packed_linear_rms(const kq_weight* weight, const kq_linear_args* ar
     // Prefill 4-bit g = 128: per-row statistics (and h), then the row quantizer normalizes while it quantizes.
     if (ws_lin) c.act = kq::carve_workspace(*c.w, c.M, base);
     kq::LinearCall fused = c;  // the row quantizer reads h (F32) in the residual form
-    if (res) fused.x_type = kq::ACT_F32;
+    if (res) {
+        fused.x_type = kq::ACT_F32;
+        fused.x = norm->hidden;
+    }
+    if (kq::gemm8_fits(fused) && aligned16(norm->weight)) {
+        n.out1 = res ? norm->hidden : nullptr;
+        n.w2 = res ? norm->weight : nullptr;
+        n.inv_out = inv;
+        if (hipError_t e = kq::launch_rms_norm(n, st); e != hipSuccess) return hip_fail(e, "RMS normalization launch");
+        fused.norm_inv = inv;
+        fused.norm_w1 = norm->weight;
+        if (hipError_t e = kq::launch_gemm8(fused, c.act, st); e != hipSuccess) return hip_fail(e, "prefill projection launch");
+        return KQ_OK;
+    }
     if (kq::gemm_i4_fits(fused) && aligned16(norm->weight)) {
         n.out1 = res ? norm->hidden : nullptr;
         n.w2 = res ? norm->weight : nullptr;
@@ -1103,6 +1229,12 @@ kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_d
     void* ws = nullptr;
     if (kq_status s = device_scratch(g_debug_scratch, align_up(ws_bytes) + 256, st, &ws); s != KQ_OK) return s;
     c.act = kq::carve_workspace(*c.w, m, ws);
+    if (kq::gemm8_fits(c)) {
+        hipError_t e = kq::launch_gemm8(c, c.act, st, true, codes, scales, sums);
+        if (e == hipSuccess && zero_points) e = hipMemsetAsync(zero_points, 0, static_cast<std::size_t>(m * (c.w->geo.cols / c.w->geo.group)) * 4, st);
+        if (e != hipSuccess) return hip_fail(e, "debug quantize");
+        return KQ_OK;
+    }
     if (kq::gemm_i4_fits(c)) {
         const hipError_t e = kq::launch_gemm_i4_quantize_dump(c, c.act, codes, scales, sums, zero_points, st);
         if (e != hipSuccess) return hip_fail(e, "debug quantize");
@@ -1181,6 +1313,7 @@ int32_t kq_debug_route_shape(int32_t bits, int32_t group_size, int64_t rows, int
     w.tiled = kq::tiled_group_ok(bits, group_size);
     w.scale_type = scale_f16 ? kq::META_F16 : kq::META_F32;
     w.zero_mode = zero_mode;
+    w.has_prefill = kq::gemm8_eligible(w);
     kq::LinearCall c{};
     c.w = &w;
     c.x = nullptr;

@@ -1,0 +1,815 @@
+// Prefill projection (M > 16) of the MI355X quantized linear layer for 4-bit weights with g = 128 on
+// v_mfma_i32_32x32x32_i8, from a prefill copy of the weight.
+//
+// Prefill copy (built once when the weight is packed, kq_api.cpp build_prefill): the codes as int8 with the zero point
+// folded in (u - zp for uint4 zero points, c otherwise), in the operand order of v_mfma_i32_32x32x32_i8: for each 32
+// output columns and 32 input columns one 1 KiB fragment [64 lanes][16 B], lane l = column l % 32 and k-half
+// h = l / 32, byte p holding k = 8 h + p (p < 8) or 16 + 8 h + p - 8; fragments of one column block are contiguous
+// along K. Per (column, group) a record {s, -1.5 * 2^23 * s, z, 0}.
+//
+// quantize_rows8_kernel: one lane per 32 columns of a row, a lane quad per group (max |x| reduced with DPP), the
+//   codes of (row, 32 columns) written as the two 16-byte halves of the same fragment order (A operand: lane l =
+//   row l % 32), block scales transposed [groups][M_p] in natural row order (and a_s * Q for additive zeros).
+// gemm8_kernel: workgroup tile 256 rows x 128 columns, 8 waves of 64 x 64 (two 32-row blocks x two 32-column
+//   blocks, two waves per SIMD), one 128-column k step (one group) per iteration. Operands and per-step metadata
+//   (weight records, activation scales) reach LDS through direct copies only (buffer_load ... lds, 16 B per lane,
+//   exactly 7 per wave and step) into a 3-stage ring of 52 KiB stages; each wave reads its fragments with
+//   ds_read_b128 one block ahead of use. Per 32 x 32 block and group: four MFMAs whose first one
+//   starts from the bits of 1.5 * 2^23, so the int32 result read as f32 is 12582912 + P' exactly (|P'| < 2^22); then
+//   per element t = fma(bits, s, -12582912 s) = fl(s * P') (exact for F16-derived s) and acc += a_s * t, with a_s
+//   broadcast from one register by DPP row_newbcast (the 16 rows a lane holds are lane-index-addressable in every
+//   16-lane row). The epilogue of a block runs after MFMAs 2-4 of the next block (12 wait states after its last
+//   MFMA), so its VALU issues in the shadow of the 8-pass MFMAs.
+// Numerics: BlockwiseLinear / SymmetricPackedLinear closed forms (runtime/ynn/operators.cpp:1118-1169, :1250-1308),
+// zero point folded into the integer operand, additive float zeros as acc += (a_s * Q) * z.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "kq_device.hpp"
+#include "kq_internal.hpp"
+
+namespace kq {
+namespace {
+
+using namespace dev;
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kBM = 256, kStepK = 128;  // tile rows (columns: 4 blocks of 32), k step
+constexpr int kWaves = 8, kThreads = 64 * kWaves;
+// One LDS stage (one k step): activation fragments [8 row blocks][4 k-chunks][1 KiB], weight fragments
+// [4 column blocks][4 k-chunks][1 KiB], the 256 rows' activation scales, a_s * Q (additive zeros), and the weight
+// records [4 column blocks][32 columns][16 B]. After the 3 stages, 1 KiB that dummy copies write into.
+constexpr int kAOff = 0, kBOff = 32768, kSOff = 49152, kZOff = 50176, kWOff = 51200;
+constexpr int kStageBytes = 53248;
+constexpr int kStages = 3;
+constexpr int kDummyOff = kStages * kStageBytes;
+constexpr int kLds = kDummyOff + 1024;               // 157 KiB
+[[maybe_unused]] constexpr int kCopies = 7;                           // direct copies per wave and step (4 A + 2 B + 1 metadata/dummy)
+constexpr float kBias = 12582912.F;                  // 1.5 * 2^23
+constexpr int kBiasBits = 0x4B400000;
+static_assert(kLds <= 160 * 1024, "LDS budget");
+
+#if defined(__HIP_DEVICE_COMPILE__)
+#define KQ_ASM(...) asm volatile(__VA_ARGS__)
+#else
+#define KQ_ASM(...) (void)0
+#endif
+
+__device__ __forceinline__ std::uint32_t lds_addr(void* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return static_cast<std::uint32_t>(reinterpret_cast<std::uintptr_t>((lds_void*)p));
+#else
+    return static_cast<std::uint32_t>(reinterpret_cast<std::uintptr_t>(p));
+#endif
+}
+template <int OFF>
+__device__ __forceinline__ void ds_read16(v4i& v, std::uint32_t addr) {
+    KQ_ASM("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+}
+template <typename T>
+__device__ __forceinline__ void tie(T& x) {
+    KQ_ASM("" : "+v"(x));
+}
+template <typename T, int N>
+__device__ __forceinline__ void tie(T (&x)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) tie(x[i]);
+}
+// s_waitcnt lgkmcnt(N) that every guarded register depends on (no use can move above it)
+template <int N, typename... T>
+__device__ __forceinline__ void lgkm_wait(T&... x) {
+    KQ_ASM("s_waitcnt lgkmcnt(%0)" : : "n"(N));
+    (tie(x), ...);
+}
+
+constexpr int kRsrcWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, std::uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kRsrcWord3);
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Row quantizer
+
+// Byte position (lane half h, byte p) of column kk (0..31) of a 32-column chunk in the fragment order.
+// kk 0..7 -> (0, kk), 8..15 -> (1, kk - 8), 16..23 -> (0, 8 + kk - 16), 24..31 -> (1, 8 + kk - 24)
+
+struct QRow8Args {
+    const void* x;
+    int M, M_p, K;
+    float input_scale;
+    std::int8_t* q;         // [M_p/32][K/32][64][16]
+    float* scale_t;         // [K/128][M_p] (dynamic)
+    float* az_t;            // [K/128][M_p] a_s * Q (additive float zeros), or null
+    const float* ninv;      // NORM: per-row inverse RMS [M]
+    const float* nw;        // NORM: norm weight [K]
+    // parity dumps (natural order), or null
+    std::int8_t* d_codes;   // [M][K]
+    float* d_scales;        // [M][K/128]
+    std::int32_t* d_sums;   // [M][K/128]
+};
+
+// One lane per 32 columns [32 j, 32 j + 32) of row m; four lanes (a quad) per group of 128 columns.
+template <int QM, bool F32, bool NORM>
+__global__ __launch_bounds__(256) void quantize_rows8_kernel(QRow8Args a) {
+    const int units = a.K / 32;
+    const int t = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    const int m = t / units, j = t - m * units;
+    if (m >= a.M_p) return;  // whole waves (M_p * units is a multiple of 64)
+    const bool live = m < a.M;
+    float v[32];
+    if (live) {
+        if constexpr (F32) {
+            const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + static_cast<std::int64_t>(m) * a.K + 32 * j);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 r = src[i];
+                v[4 * i] = r.x;
+                v[4 * i + 1] = r.y;
+                v[4 * i + 2] = r.z;
+                v[4 * i + 3] = r.w;
+            }
+        } else {
+            const uint4* src = reinterpret_cast<const uint4*>(static_cast<const std::uint16_t*>(a.x) + static_cast<std::int64_t>(m) * a.K + 32 * j);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint4 r = src[i];
+                const std::uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    v[8 * i + 2 * d] = __uint_as_float(w4[d] << 16);
+                    v[8 * i + 2 * d + 1] = __uint_as_float(w4[d] & 0xFFFF0000u);
+                }
+            }
+        }
+        if constexpr (NORM) {
+            const float inv = a.ninv[m];
+            const float4* wp = reinterpret_cast<const float4*>(a.nw + 32 * j);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 w = wp[i];
+                v[4 * i] = v[4 * i] * inv * w.x;
+                v[4 * i + 1] = v[4 * i + 1] * inv * w.y;
+                v[4 * i + 2] = v[4 * i + 2] * inv * w.z;
+                v[4 * i + 3] = v[4 * i + 3] * inv * w.w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i] = 0.F;
+    }
+    float mx = 0.F, mn = 0.F;
+    if constexpr (QM != QUANT_STATIC) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) quant_stat(QM, v[i], mx, mn);
+        mx = fmaxf(mx, __int_as_float(dpp<0xB1>(__float_as_int(mx))));
+        mx = fmaxf(mx, __int_as_float(dpp<0x4E>(__float_as_int(mx))));
+    }
+    const QuantBlock qb = quant_block(QM, mx, mn, a.input_scale, live);
+    // codes as bytes, columns in order: w[i] holds columns 4 i .. 4 i + 3
+    std::uint32_t w[8];
+    if constexpr (QM == QUANT_STATIC) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            std::uint32_t d = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float c = fminf(fmaxf(__builtin_rintf(v[4 * i + e] / a.input_scale), -128.F), 127.F);
+                d = __builtin_amdgcn_cvt_pk_u8_f32(c + 128.F, e, d);
+            }
+            w[i] = d ^ 0x80808080u;
+        }
+    } else {
+        // dynamic: |x * inverse| <= 127 (1 + 2^-24) rounds to at most 127 (no clamp); adding 1.5 * 2^23 rounds
+        // x * inverse to the nearest integer (ties to even, as rint), held in the low mantissa byte
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            std::uint32_t u[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) u[e] = __float_as_uint(v[4 * i + e] * qb.inverse + kBias);
+            const std::uint32_t lo = __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(u[3], u[2], 0x0c0c0400u);
+            w[i] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        }
+    }
+    // fragment halves: h = 0 gets columns 0-7 and 16-23, h = 1 columns 8-15 and 24-31
+    const int mb = m >> 5, r = m & 31;
+    std::int8_t* frag = a.q + (static_cast<std::int64_t>(mb) * units + j) * 1024;
+    *reinterpret_cast<uint4*>(frag + r * 16) = make_uint4(w[0], w[1], w[4], w[5]);
+    *reinterpret_cast<uint4*>(frag + (r + 32) * 16) = make_uint4(w[2], w[3], w[6], w[7]);
+    // code sums of the group (additive float zeros and the parity dump)
+    int qsum = 0;
+    if (a.az_t || a.d_sums) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qsum += static_cast<std::int8_t>((w[i] >> (8 * e)) & 0xFFu);
+        qsum += dpp<0xB1>(qsum);
+        qsum += dpp<0x4E>(qsum);
+    }
+    const int b = j >> 2;
+    if ((j & 3) == 0) {
+        const std::int64_t o = static_cast<std::int64_t>(b) * a.M_p + m;
+        if (a.scale_t) a.scale_t[o] = qb.s;
+        if (a.az_t) a.az_t[o] = qb.s * static_cast<float>(qsum);
+        if (live && a.d_scales) a.d_scales[static_cast<std::int64_t>(m) * (a.K / 128) + b] = QM == QUANT_STATIC ? a.input_scale : qb.s;
+        if (live && a.d_sums) a.d_sums[static_cast<std::int64_t>(m) * (a.K / 128) + b] = qsum;
+    }
+    if (live && a.d_codes) {
+        uint4* dst = reinterpret_cast<uint4*>(a.d_codes + static_cast<std::int64_t>(m) * a.K + 32 * j);
+        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    }
+}
+
+
+// ------------------------------------------------------------------------------------------------------------------
+// GEMM
+
+struct Gemm8Args {
+    const std::int8_t* q;       // activation fragments [M_p/32][K/32][64][16]
+    const float* scale_t;       // [groups][M_p] activation block scales (dynamic)
+    const float* az_t;          // [groups][M_p] a_s * Q (additive float zeros)
+    const std::int8_t* w;       // weight fragments [NB][K/32][64][16]
+    const float4* wmeta;        // [groups][NB][32] {s, -1.5 * 2^23 * s, z, 0}
+    float* y;
+    std::int32_t* dump;         // [M][N][groups] P' (parity instrumentation), or null
+    float* partial;             // split K: [ksplit][tiles][512 threads][64] raw accumulators
+    int M, M_p, N, K, NB, groups, m_blocks, n_blocks, ksplit;
+    float input_scale, output_scale;
+};
+
+// Global 32-column block of workgroup column block nb, local block cb (0..3); >= NB when out of range. GELU: cb 0, 1
+// are gate blocks 2 nb + cb, cb 2, 3 the matching up blocks (gate rows [0, I), up rows [I, 2I), I a multiple of 32).
+template <bool GELU>
+__device__ __forceinline__ int col_block(const Gemm8Args& a, int nb, int cb) {
+    if constexpr (GELU) {
+        const int half = a.NB >> 1;
+        const int g = 2 * nb + (cb & 1);
+        return g < half ? (cb < 2 ? g : half + g) : a.NB;
+    }
+    return 4 * nb + cb;
+}
+
+// Row (within its 32-row block) of element k (0..15) of a 32 x 32 result held by lane l: 8 (k / 4) + 4 (l / 32) + k % 4.
+// The DPP broadcast register of a row block holds, at lane 16 r + k, the value of that row for lanes of row r.
+__device__ __forceinline__ int bcast_row(int lane) { return 8 * ((lane & 15) >> 2) + 4 * (lane >> 5) + (lane & 3); }
+
+struct Meta {  // one k step's epilogue operands of a wave: weight records of its two column blocks, scales of its rows
+    v4i rec[2];      // {s, -1.5 * 2^23 * s, z, 0} of the lane's column in column blocks 0, 1
+    float as[2];     // a_s of DPP row bcast_row(lane) in row blocks 0, 1
+    float az[2];     // a_s * Q likewise (additive zeros)
+};
+
+// Epilogue of elements [K0, K1) of one block; P holds the biased int32 partials (as f32: 12582912 + P'). Each slice
+// issues its conversions first and its accumulations after, so no accumulation reads a register written by the
+// instruction right before it.
+//   F16 scales, dynamic:    P = fma(P, s, nb) = fl(s * P');   acc += a_s[row] * P   (a_s broadcast by DPP)
+//   F16 scales, calibrated: P = fma(P, s, nb);                 acc += P (input_scale applied at the end)
+//   F32 scales, dynamic:    P = P - 12582912 (exact);  P = P * s;  acc += a_s[row] * P
+//   F32 scales, calibrated: P = P - 12582912;          acc += P * s
+//   additive zeros:         acc += (a_s * Q)[row] * z
+template <int K, bool SF16, bool STAT>
+__device__ __forceinline__ void epi_convert(int& P, const v4i& rec) {
+    if constexpr (SF16) {
+        KQ_ASM("v_fma_f32 %0, %0, %1, %2" : "+v"(P) : "v"(rec[0]), "v"(rec[1]));
+    } else {
+        KQ_ASM("v_add_f32 %0, 0xcb400000, %0" : "+v"(P));
+        if constexpr (!STAT) KQ_ASM("v_mul_f32 %0, %0, %1" : "+v"(P) : "v"(rec[0]));
+    }
+}
+template <int K, bool SF16, bool STAT, bool ZF>
+__device__ __forceinline__ void epi_accumulate(float& acc, int P, const v4i& rec, float as, float az) {
+    if constexpr (STAT) {
+        if constexpr (SF16) KQ_ASM("v_add_f32 %0, %0, %1" : "+v"(acc) : "v"(P));
+        else KQ_ASM("v_fmac_f32 %0, %1, %2" : "+v"(acc) : "v"(P), "v"(rec[0]));
+    } else {
+        KQ_ASM("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(as), "v"(P), "n"(K));
+    }
+    if constexpr (ZF)
+        KQ_ASM("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(az), "v"(rec[2]), "n"(K));
+}
+template <int K0, int K1, bool SF16, bool STAT>
+__device__ __forceinline__ void epi_converts(v16i& P, const v4i& rec) {
+    if constexpr (K0 < K1) {
+        int p = P[K0];
+        epi_convert<K0, SF16, STAT>(p, rec);
+        P[K0] = p;
+        epi_converts<K0 + 1, K1, SF16, STAT>(P, rec);
+    }
+}
+template <int K0, int K1, bool SF16, bool STAT, bool ZF>
+__device__ __forceinline__ void epi_accumulates(float (&acc)[16], const v16i& P, const v4i& rec, float as, float az) {
+    if constexpr (K0 < K1) {
+        epi_accumulate<K0, SF16, STAT, ZF>(acc[K0], P[K0], rec, as, az);
+        epi_accumulates<K0 + 1, K1, SF16, STAT, ZF>(acc, P, rec, as, az);
+    }
+}
+// DBG first stores P' = P - 0x4B400000 to the dump through a buffer resource: element k of the block is at byte
+// voff + (8 (k / 4) + k % 4) N G 4 + g 4; lanes of columns past N carry an offset beyond the buffer, and rows past M
+// land beyond it too, so the hardware drops those stores.
+template <int K0, int K1, bool DBG>
+__device__ __forceinline__ void epi_dump(const v16i& P, __amdgpu_buffer_rsrc_t dres, std::uint32_t voff, std::uint32_t row_bytes,
+                                         std::uint32_t g_bytes) {
+    if constexpr (DBG && K0 < K1) {
+        int v;  // (inline assembly keeps this read of the MFMA result in the epilogue's place)
+        KQ_ASM("v_subrev_u32 %0, %1, %2" : "=v"(v) : "v"(kBiasBits), "v"(P[K0]));
+        __builtin_amdgcn_raw_buffer_store_b32(v, dres, voff, (8 * (K0 >> 2) + (K0 & 3)) * row_bytes + g_bytes, 0);
+        epi_dump<K0 + 1, K1, DBG>(P, dres, voff, row_bytes, g_bytes);
+    }
+}
+struct Dump {
+    __amdgpu_buffer_rsrc_t res;
+    std::uint32_t row_bytes;  // N * groups * 4
+};
+template <int K0, int K1, bool SF16, bool STAT, bool ZF, bool DBG>
+__device__ __forceinline__ void epi_range(float (&acc)[16], v16i& P, const v4i& rec, float as, float az, const Dump& d,
+                                          std::uint32_t voff, int g) {
+    epi_dump<K0, K1, DBG>(P, d.res, voff, d.row_bytes, static_cast<std::uint32_t>(g) * 4);
+    epi_converts<K0, K1, SF16, STAT>(P, rec);
+    epi_accumulates<K0, K1, SF16, STAT, ZF>(acc, P, rec, as, az);
+}
+
+__device__ __forceinline__ void mfma_first(v16i& P, const v4i& A, const v4i& B, const v16i& bias) {
+    KQ_ASM("v_mfma_i32_32x32x32_i8 %0, %1, %2, %3" : "=&v"(P) : "v"(A), "v"(B), "v"(bias));
+}
+__device__ __forceinline__ void mfma_acc(v16i& P, const v4i& A, const v4i& B) {
+    KQ_ASM("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(P) : "v"(A), "v"(B));
+}
+
+// Final values of a wave's 2 x 2 blocks: calibrated inputs scale by input_scale, calibrated outputs round to
+// output_scale steps, GELU pairs column block 0 (gate) with 1 (up).
+template <bool STAT, bool GELU>
+__device__ __forceinline__ void store8(const Gemm8Args& a, const float (&acc)[2][2][16], int m0, int wm, const int (&gc)[2],
+                                       int lane) {
+    const int col = lane & 31;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int row = m0 + 64 * wm + 32 * i + 8 * (k >> 2) + 4 * (lane >> 5) + (k & 3);
+            if (row >= a.M) continue;
+            if constexpr (GELU) {
+                const int half_n = a.N >> 1;
+                const int n = 32 * gc[0] + col;
+                if (gc[0] >= (a.NB >> 1) || n >= half_n) continue;
+                float g = acc[i][0][k], up = acc[i][1][k];
+                if (STAT) {
+                    g = g * a.input_scale;
+                    up = up * a.input_scale;
+                }
+                g = calibrate_output(g, a.output_scale);
+                up = calibrate_output(up, a.output_scale);
+                a.y[static_cast<std::int64_t>(row) * half_n + n] = gelu_tanh(g) * up;
+            } else {
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const int n = 32 * gc[c] + col;
+                    if (n >= a.N) continue;
+                    float v = acc[i][c][k];
+                    if (STAT) v = v * a.input_scale;
+                    a.y[static_cast<std::int64_t>(row) * a.N + n] = calibrate_output(v, a.output_scale);
+                }
+            }
+        }
+    }
+}
+
+template <bool SF16, bool STAT, bool ZF, bool GELU, bool SPLIT, bool DBG>
+__global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
+    extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 3, wn = wave >> 2;  // rows [64 wm, +64) of the tile; column blocks below
+    const std::uint32_t lds0 = lds_addr(lds);
+
+    // workgroup -> (K range, row block, column block); consecutive workgroups run on different XCDs, so each XCD takes
+    // a contiguous range of tiles, row blocks fastest (the XCD's few column blocks of weights stay in its L2)
+    const int tiles = a.m_blocks * a.n_blocks;
+    const int total = tiles * a.ksplit;
+    int bid = blockIdx.x;
+    if (total % 8 == 0) bid = (bid % 8) * (total / 8) + bid / 8;
+    const int ks = bid / tiles, tile = bid % tiles;
+    const int mb = tile % a.m_blocks, nbk = tile / a.m_blocks;
+    const int m0 = mb * kBM;
+    const int KC = a.K / 32;
+    const int steps = a.K / kStepK / a.ksplit, s0 = ks * steps;
+
+    // ---- copies of one step: wave w brings activation row block w (4 fragments), half of weight column block w / 2
+    // (2 fragments) and one metadata block: w = 0, 1 the weight records of column blocks 0-1 / 2-3, w = 2 the tile's
+    // activation scales, w = 3 its a_s * Q (additive zeros); the other copies write zeros into the dummy area
+    const __amdgpu_buffer_rsrc_t ares = rsrc(a.q + static_cast<std::int64_t>(m0 / 32) * KC * 1024,
+                                             static_cast<std::uint32_t>(kBM / 32) * KC * 1024);
+    const int cbc = wave >> 1, ckc = 2 * (wave & 1);
+    const int gcb = col_block<GELU>(a, nbk, cbc);
+    const bool clive = gcb < a.NB;
+    const __amdgpu_buffer_rsrc_t bres = rsrc(a.w + static_cast<std::int64_t>(clive ? gcb : 0) * KC * 1024,
+                                             clive ? static_cast<std::uint32_t>(KC) * 1024 : 0u);
+    __amdgpu_buffer_rsrc_t mres = rsrc(a.wmeta, 0u);
+    std::uint32_t meta_base = 0x80000000u, meta_step = 0;
+    int meta_dst = kDummyOff;
+    if (wave < 2) {
+        const int blk = col_block<GELU>(a, nbk, 2 * wave);  // first of two adjacent global column blocks
+        mres = rsrc(a.wmeta, static_cast<std::uint32_t>(a.groups) * a.NB * 512);
+        meta_base = static_cast<std::uint32_t>(blk) * 512 + lane * 16;
+        meta_step = static_cast<std::uint32_t>(a.NB) * 512;
+        meta_dst = kWOff + wave * 1024;
+    } else if ((wave == 2 && !STAT) || (wave == 3 && ZF)) {
+        mres = rsrc(wave == 2 ? a.scale_t : a.az_t, static_cast<std::uint32_t>(a.groups) * a.M_p * 4);
+        meta_base = static_cast<std::uint32_t>(m0) * 4 + lane * 16;
+        meta_step = static_cast<std::uint32_t>(a.M_p) * 4;
+        meta_dst = wave == 2 ? kSOff : kZOff;
+    }
+    auto issue = [&](int step) {
+        const int st = step < steps ? step : steps - 1;  // past the range: the last step again, into an unread stage
+        std::uint8_t* base = lds + (step % kStages) * kStageBytes;
+        const std::uint32_t kc0 = static_cast<std::uint32_t>((s0 + st) * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(base + kAOff + (wave * 4 + i) * 1024), 16, lane * 16,
+                                                     (static_cast<std::uint32_t>(wave) * KC + kc0 + i) * 1024, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(base + kBOff + (cbc * 4 + ckc + i) * 1024), 16,
+                                                     lane * 16, (kc0 + ckc + i) * 1024, 0, 0);
+        const __amdgpu_buffer_rsrc_t mr = mres;
+        std::uint8_t* mdst = meta_dst == kDummyOff ? lds + kDummyOff : base + meta_dst;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(mr, (lds_void*)mdst, 16, meta_base,
+                                                 meta_step * static_cast<std::uint32_t>(s0 + st), 0, 0);
+    };
+
+    // ---- the wave's fragments: row blocks 2 wm + i; column blocks (plain) 2 wn + i, (GELU) wn + 2 i
+    const int cb_l0 = GELU ? wn : 2 * wn, cb_l1 = GELU ? wn + 2 : 2 * wn + 1;
+    const int gc[2] = {col_block<GELU>(a, nbk, cb_l0), col_block<GELU>(a, nbk, cb_l1)};
+    const std::uint32_t a_lane = lds0 + kAOff + (2 * wm * 4) * 1024 + lane * 16;
+    const std::uint32_t b_lane0 = lds0 + kBOff + (cb_l0 * 4) * 1024 + lane * 16;
+    const std::uint32_t b_lane1 = lds0 + kBOff + (cb_l1 * 4) * 1024 + lane * 16;
+    const int col = lane & 31;
+    [[maybe_unused]] const std::uint32_t w_lane0 = lds0 + kWOff + (cb_l0 * 32 + col) * 16;
+    [[maybe_unused]] const std::uint32_t w_lane1 = lds0 + kWOff + (cb_l1 * 32 + col) * 16;
+    [[maybe_unused]] const std::uint32_t s_lane = lds0 + kSOff + (64 * wm + bcast_row(lane)) * 4;
+    [[maybe_unused]] const std::uint32_t z_lane = lds0 + kZOff + (64 * wm + bcast_row(lane)) * 4;
+    auto read_meta = [&](Meta& mt, std::uint32_t stage) {
+        KQ_ASM("ds_read_b128 %0, %1" : "=v"(mt.rec[0]) : "v"(w_lane0 + stage));
+        KQ_ASM("ds_read_b128 %0, %1" : "=v"(mt.rec[1]) : "v"(w_lane1 + stage));
+        if constexpr (!STAT) {
+            KQ_ASM("ds_read_b32 %0, %1" : "=v"(mt.as[0]) : "v"(s_lane + stage));
+            KQ_ASM("ds_read_b32 %0, %1 offset:128" : "=v"(mt.as[1]) : "v"(s_lane + stage));
+        }
+        if constexpr (ZF) {
+            KQ_ASM("ds_read_b32 %0, %1" : "=v"(mt.az[0]) : "v"(z_lane + stage));
+            KQ_ASM("ds_read_b32 %0, %1 offset:128" : "=v"(mt.az[1]) : "v"(z_lane + stage));
+        }
+    };
+    auto read4 = [&](v4i (&f)[4], std::uint32_t addr) {
+        ds_read16<0>(f[0], addr);
+        ds_read16<1024>(f[1], addr);
+        ds_read16<2048>(f[2], addr);
+        ds_read16<3072>(f[3], addr);
+    };
+
+    // parity dump (DBG): P' of element (row, column n, group g) at dump[(row N + n) G + g]; dvo[i][c] is the byte
+    // offset of the lane's element 0 in block (i, c), beyond the buffer for columns past N
+    Dump dmp{};
+    std::uint32_t dvo[2][2] = {{0u, 0u}, {0u, 0u}};
+    if constexpr (DBG) {
+        // the resource starts at this tile's first row, so every offset stays far below 2^31
+        const std::uint64_t row_elems = static_cast<std::uint64_t>(a.N) * a.groups;
+        const std::uint64_t rest = static_cast<std::uint64_t>(a.M - m0) * row_elems * 4;
+        dmp.res = rsrc(a.dump + static_cast<std::uint64_t>(m0) * row_elems,
+                       static_cast<std::uint32_t>(rest < 0x7FFFFFFFull ? rest : 0x7FFFFFFFull));
+        dmp.row_bytes = static_cast<std::uint32_t>(row_elems * 4);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int n = 32 * gc[c] + col, r0 = 64 * wm + 32 * i + 4 * (lane >> 5);
+                dvo[i][c] = (gc[c] < a.NB && n < a.N && m0 + r0 < a.M)
+                                ? static_cast<std::uint32_t>((static_cast<std::uint64_t>(r0) * a.N + n) * a.groups * 4)
+                                : 0x80000000u;
+            }
+    }
+
+    float acc[2][2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int k = 0; k < 16; ++k) acc[i][c][k] = 0.F;
+    v16i bias;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) bias[k] = kBiasBits;
+    KQ_ASM("" : "+v"(bias));  // opaque: never rematerialized next to an MFMA
+    // P[1] starts as the bias and the metadata of "step -1" as zeros: the epilogue step 0 runs for the block before its
+    // first one adds exactly 0
+    v16i P[2];
+    P[0] = bias;
+    P[1] = bias;
+    v4i A[2][4], B0[4], B1[2][4];
+    Meta mt[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        mt[1].rec[i] = v4i{0, 0, 0, 0};
+        mt[1].as[i] = 0.F;
+        mt[1].az[i] = 0.F;
+        mt[0].as[i] = 0.F;
+        mt[0].az[i] = 0.F;
+    }
+
+    // prologue: three stages in flight; step 0's operands (but A row block 1) and metadata in registers
+    issue(0);
+    issue(1);
+    issue(2);
+    KQ_ASM("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    read4(A[0], a_lane);
+    read4(B0, b_lane0);
+    read4(B1[0], b_lane1);
+    read_meta(mt[0], 0);
+
+    // Step t (parity p) in four blocks (row block, column block) of four MFMAs each; the epilogue of a block runs in
+    // the VALU slots after MFMAs 2-4 of the next block. Reads (ds_read_b128) go into the gap after a block's MFMA 1:
+    //   b0 (0, 0) -> P0: gap: A row block 1 of step t;         epilogue of b3 of step t - 1
+    //   b1 (0, 1) -> P1:                                        epilogue of b0
+    //   [lgkmcnt(0), vmcnt(7), barrier: stage t + 1 complete, stage t free; copies of step t + 3 into stage t]
+    //   b2 (1, 0) -> P0: gap: B column block 1 and metadata of step t + 1;  epilogue of b1
+    //   b3 (1, 1) -> P1: gap: A row block 0 and B column block 0 of step t + 1;  epilogue of b2
+    // Stage t % 3 is read from b2 of step t - 1 to b0 of step t; the mid-step barrier of step t comes after every
+    // wave waited for those reads, and after every wave's copies of step t + 1 (issued at mid-step t - 2) landed.
+    auto step_body = [&](int t, auto parity) {
+        constexpr int p = decltype(parity)::value;
+        Meta& cur = mt[p];
+        Meta& prv = mt[p ^ 1];
+        v4i (&Bc)[4] = B1[p];
+        v4i (&Bn)[4] = B1[p ^ 1];
+        const std::uint32_t st_now = static_cast<std::uint32_t>((t % kStages) * kStageBytes);
+        const std::uint32_t st_next = static_cast<std::uint32_t>(((t + 1) % kStages) * kStageBytes);
+        const int g = s0 + t;
+        // ---- b0
+        lgkm_wait<0>(A[0], B0, Bc, cur.rec, cur.as, cur.az);  // step t's operands and metadata (read during step t - 1)
+        mfma_first(P[0], A[0][0], B0[0], bias);
+        ds_read16<4096>(A[1][0], a_lane + st_now);
+        ds_read16<5120>(A[1][1], a_lane + st_now);
+        ds_read16<6144>(A[1][2], a_lane + st_now);
+        ds_read16<7168>(A[1][3], a_lane + st_now);
+        mfma_acc(P[0], A[0][1], B0[1]);
+        epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1], prv.as[1], prv.az[1], dmp, t > 0 ? dvo[1][1] : 0x80000000u, g - 1);
+        mfma_acc(P[0], A[0][2], B0[2]);
+        epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1], prv.as[1], prv.az[1], dmp, t > 0 ? dvo[1][1] : 0x80000000u, g - 1);
+        mfma_acc(P[0], A[0][3], B0[3]);
+        epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1], prv.as[1], prv.az[1], dmp, t > 0 ? dvo[1][1] : 0x80000000u, g - 1);
+        // ---- b1
+        mfma_first(P[1], A[0][0], Bc[0], bias);
+        mfma_acc(P[1], A[0][1], Bc[1]);
+        epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0], cur.as[0], cur.az[0], dmp, dvo[0][0], g);
+        mfma_acc(P[1], A[0][2], Bc[2]);
+        epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0], cur.as[0], cur.az[0], dmp, dvo[0][0], g);
+        mfma_acc(P[1], A[0][3], Bc[3]);
+        epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0], cur.as[0], cur.az[0], dmp, dvo[0][0], g);
+        // ---- mid-step
+        lgkm_wait<0>(A[1]);
+        KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(kCopies) : "memory");
+        issue(t + 3);
+        // ---- b2
+        mfma_first(P[0], A[1][0], B0[0], bias);
+        read4(Bn, b_lane1 + st_next);
+        read_meta(prv, st_next);
+        mfma_acc(P[0], A[1][1], B0[1]);
+        epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1], cur.as[0], cur.az[0], dmp, dvo[0][1], g);
+        mfma_acc(P[0], A[1][2], B0[2]);
+        epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1], cur.as[0], cur.az[0], dmp, dvo[0][1], g);
+        mfma_acc(P[0], A[1][3], B0[3]);
+        epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1], cur.as[0], cur.az[0], dmp, dvo[0][1], g);
+        // ---- b3
+        mfma_first(P[1], A[1][0], Bc[0], bias);
+        read4(A[0], a_lane + st_next);
+        read4(B0, b_lane0 + st_next);
+        mfma_acc(P[1], A[1][1], Bc[1]);
+        epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0], cur.as[1], cur.az[1], dmp, dvo[1][0], g);
+        mfma_acc(P[1], A[1][2], Bc[2]);
+        epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0], cur.as[1], cur.az[1], dmp, dvo[1][0], g);
+        mfma_acc(P[1], A[1][3], Bc[3]);
+        epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0], cur.as[1], cur.az[1], dmp, dvo[1][0], g);
+    };
+    for (int t = 0; t < steps; t += 2) {
+        step_body(t, std::integral_constant<int, 0>{});
+        step_body(t + 1, std::integral_constant<int, 1>{});
+    }
+    // drain: the epilogue of the last step's b3 (step steps - 1, parity 1)
+    KQ_ASM("s_nop 11");
+    epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], mt[1].rec[1], mt[1].as[1], mt[1].az[1], dmp, dvo[1][1], s0 + steps - 1);
+    KQ_ASM("s_waitcnt vmcnt(0)" ::: "memory");  // the copies past the range land before the workgroup ends
+
+    if constexpr (SPLIT) {
+        v4f* dst = reinterpret_cast<v4f*>(a.partial + ((static_cast<std::int64_t>(ks) * tiles + tile) * kThreads + tid) * 64);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4)
+                    __builtin_nontemporal_store(v4f{acc[i][c][4 * q4], acc[i][c][4 * q4 + 1], acc[i][c][4 * q4 + 2], acc[i][c][4 * q4 + 3]},
+                                                dst + (i * 2 + c) * 4 + q4);
+    } else {
+        store8<STAT, GELU>(a, acc, m0, wm, gc, lane);
+    }
+}
+
+// Split K: the ranges' partial accumulators of one tile added in range order, then the same final stores.
+template <bool STAT, bool GELU>
+__global__ __launch_bounds__(kThreads) void gemm8_reduce_kernel(Gemm8Args a) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = tid >> 6, wm = wave & 3, wn = wave >> 2;
+    const int tile = blockIdx.x;
+    const int tiles = a.m_blocks * a.n_blocks;
+    const int mb = tile % a.m_blocks, nbk = tile / a.m_blocks;
+    float acc[2][2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int k = 0; k < 16; ++k) acc[i][c][k] = 0.F;
+    for (int ks = 0; ks < a.ksplit; ++ks) {
+        const v4f* src = reinterpret_cast<const v4f*>(a.partial + ((static_cast<std::int64_t>(ks) * tiles + tile) * kThreads + tid) * 64);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const v4f v = __builtin_nontemporal_load(src + (i * 2 + c) * 4 + q4);
+                    acc[i][c][4 * q4] += v[0];
+                    acc[i][c][4 * q4 + 1] += v[1];
+                    acc[i][c][4 * q4 + 2] += v[2];
+                    acc[i][c][4 * q4 + 3] += v[3];
+                }
+    }
+    const int gc[2] = {col_block<GELU>(a, nbk, GELU ? wn : 2 * wn), col_block<GELU>(a, nbk, GELU ? wn + 2 : 2 * wn + 1)};
+    store8<STAT, GELU>(a, acc, mb * kBM, wm, gc, lane);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------------------------
+// Host side
+
+bool gemm8_eligible(const Weight& w) {
+    return w.tiled && w.geo.bits == 4 && w.geo.group == 128 && w.geo.cols % 256 == 0 && w.geo.cols_p == w.geo.cols;
+}
+
+Gemm8Plan gemm8_plan(const Weight& w, std::int64_t M, bool gelu) {
+    Gemm8Plan p;
+    const int NB = static_cast<int>((w.geo.rows + 31) / 32);
+    p.m_blocks = static_cast<int>((M + kBM - 1) / kBM);
+    p.n_blocks = gelu ? (NB / 2 + 1) / 2 : (NB + 3) / 4;
+    const int k_steps = static_cast<int>(w.geo.cols / kStepK);
+    const int tiles = p.m_blocks * p.n_blocks;
+    p.ksplit = 1;
+    for (int sp = 2; sp <= 8 && tiles * p.ksplit < 256; sp *= 2) {
+        if (k_steps % (2 * sp) || k_steps / sp < 4) break;
+        p.ksplit = sp;
+    }
+    return p;
+}
+
+bool gemm8_fits(const LinearCall& c) {
+    const Weight& w = *c.w;
+    if (!w.has_prefill || !gemm8_eligible(w) || c.M <= 16) return false;
+    if (c.path != PATH_BLOCKWISE && c.path != PATH_SYMMETRIC) return false;
+    if (c.path == PATH_SYMMETRIC && w.zero_mode != ZERO_NONE) return false;
+    if (c.gelu_gate && ((w.geo.rows / 2) % 32)) return false;
+    if ((reinterpret_cast<std::uintptr_t>(c.x) & 15u) || (c.norm_inv && (reinterpret_cast<std::uintptr_t>(c.norm_w1) & 15u)))
+        return false;
+    const std::int64_t M_p = round_up(c.M, kBM);
+    const std::int64_t NB = (w.geo.rows + 31) / 32, groups = w.geo.cols / 128;
+    if (M_p * w.geo.cols >= (std::int64_t{1} << 31) || groups * NB * 512 >= (std::int64_t{1} << 31) ||
+        groups * M_p * 4 >= (std::int64_t{1} << 31) || M_p >= (std::int64_t{1} << 24))
+        return false;
+    return true;
+}
+
+std::size_t gemm8_partial_bytes(const Weight& w, std::int64_t M, bool gelu) {
+    const Gemm8Plan p = gemm8_plan(w, M, gelu);
+    if (p.ksplit == 1) return 0;
+    return static_cast<std::size_t>(p.ksplit) * p.m_blocks * p.n_blocks * kThreads * 64 * 4;
+}
+
+namespace {
+template <bool SF16, bool STAT, bool ZF, bool GELU, bool SPLIT, bool DBG>
+hipError_t launch8(const Gemm8Args& g, unsigned blocks, hipStream_t stream) {
+    auto kern = gemm8_kernel<SF16, STAT, ZF, GELU, SPLIT, DBG>;
+    static bool configured = false;  // per instance: the dynamic LDS limit is raised once
+    if (!configured) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), kLds, stream, g);
+    return hipGetLastError();
+}
+template <bool SF16, bool STAT, bool ZF, bool GELU>
+hipError_t launch8_split(const Gemm8Args& g, unsigned blocks, bool split, bool dbg, hipStream_t stream) {
+    if constexpr (!GELU) {  // the parity dump covers plain projections
+        if (dbg) return split ? launch8<SF16, STAT, ZF, false, true, true>(g, blocks, stream)
+                              : launch8<SF16, STAT, ZF, false, false, true>(g, blocks, stream);
+    }
+    return split ? launch8<SF16, STAT, ZF, GELU, true, false>(g, blocks, stream)
+                 : launch8<SF16, STAT, ZF, GELU, false, false>(g, blocks, stream);
+}
+}  // namespace
+
+hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t stream, bool quantize_only, std::int8_t* d_codes,
+                        float* d_scales, std::int32_t* d_sums) {
+    const Weight& w = *c.w;
+    const bool stat = c.path == PATH_SYMMETRIC;
+    const bool zf = w.zero_mode == ZERO_FLOAT;
+    const int M = static_cast<int>(c.M), K = static_cast<int>(w.geo.cols);
+    const int M_p = static_cast<int>(round_up(c.M, kBM));
+    // activation quantization into the workspace
+    QRow8Args q{};
+    q.x = c.x;
+    q.M = M;
+    q.M_p = M_p;
+    q.K = K;
+    q.input_scale = c.input_scale;
+    q.q = act.q;
+    q.scale_t = act.scale;
+    q.az_t = zf ? reinterpret_cast<float*>(act.sum) : nullptr;
+    q.ninv = c.norm_inv;
+    q.nw = c.norm_w1;
+    q.d_codes = d_codes;
+    q.d_scales = d_scales;
+    q.d_sums = d_sums;
+    {
+        const dim3 grid(static_cast<unsigned>(static_cast<std::int64_t>(M_p) * (K / 32) / 256)), block(256);
+        const bool f32 = c.x_type == ACT_F32, norm = c.norm_inv != nullptr;
+#define KQ_Q8(QM, F, NM) hipLaunchKernelGGL((quantize_rows8_kernel<QM, F, NM>), grid, block, 0, stream, q)
+        if (stat) {
+            if (f32) { if (norm) KQ_Q8(QUANT_STATIC, true, true); else KQ_Q8(QUANT_STATIC, true, false); }
+            else { if (norm) KQ_Q8(QUANT_STATIC, false, true); else KQ_Q8(QUANT_STATIC, false, false); }
+        } else {
+            if (f32) { if (norm) KQ_Q8(QUANT_DYN_SYM, true, true); else KQ_Q8(QUANT_DYN_SYM, true, false); }
+            else { if (norm) KQ_Q8(QUANT_DYN_SYM, false, true); else KQ_Q8(QUANT_DYN_SYM, false, false); }
+        }
+#undef KQ_Q8
+        if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    }
+    if (quantize_only) return hipSuccess;
+    const Gemm8Plan p = gemm8_plan(w, c.M, c.gelu_gate);
+    Gemm8Args g{};
+    g.q = act.q;
+    g.scale_t = act.scale;
+    g.az_t = reinterpret_cast<const float*>(act.sum);
+    g.w = w.prefill_codes;
+    g.wmeta = reinterpret_cast<const float4*>(w.prefill_meta);
+    g.y = c.y;
+    g.dump = c.dump;
+    g.partial = act.partial;
+    g.M = M;
+    g.M_p = M_p;
+    g.N = static_cast<int>(w.geo.rows);
+    g.K = K;
+    g.NB = static_cast<int>((w.geo.rows + 31) / 32);
+    g.groups = K / 128;
+    g.m_blocks = p.m_blocks;
+    g.n_blocks = p.n_blocks;
+    g.ksplit = p.ksplit;
+    g.input_scale = c.input_scale;
+    g.output_scale = c.output_scale;
+    const bool split = p.ksplit > 1, dbg = c.dump != nullptr, sf16 = w.scale_type == META_F16;
+    const unsigned blocks = static_cast<unsigned>(p.m_blocks * p.n_blocks * p.ksplit);
+    hipError_t e;
+#define KQ_G8(SF, ST, Z) e = c.gelu_gate ? launch8_split<SF, ST, Z, true>(g, blocks, split, dbg, stream) \
+                                         : launch8_split<SF, ST, Z, false>(g, blocks, split, dbg, stream)
+    if (sf16) {
+        if (stat) KQ_G8(true, true, false);
+        else if (zf) KQ_G8(true, false, true);
+        else KQ_G8(true, false, false);
+    } else {
+        if (stat) KQ_G8(false, true, false);
+        else if (zf) KQ_G8(false, false, true);
+        else KQ_G8(false, false, false);
+    }
+#undef KQ_G8
+    if (e != hipSuccess || !split) return e;
+    const unsigned tiles = static_cast<unsigned>(p.m_blocks * p.n_blocks);
+    if (stat) {
+        if (c.gelu_gate) hipLaunchKernelGGL((gemm8_reduce_kernel<true, true>), dim3(tiles), dim3(kThreads), 0, stream, g);
+        else hipLaunchKernelGGL((gemm8_reduce_kernel<true, false>), dim3(tiles), dim3(kThreads), 0, stream, g);
+    } else {
+        if (c.gelu_gate) hipLaunchKernelGGL((gemm8_reduce_kernel<false, true>), dim3(tiles), dim3(kThreads), 0, stream, g);
+        else hipLaunchKernelGGL((gemm8_reduce_kernel<false, false>), dim3(tiles), dim3(kThreads), 0, stream, g);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace kq

@@ -32,6 +32,14 @@ struct Weight {
     std::size_t bytes = 0;
     int device = 0;
     bool scales_positive = false;   // every scale finite and > 0 (LOWBIT_PARITY's precondition)
+    // prefill copy for the g = 128 GEMM (kq_gemm8.hip), one more allocation: int8 codes with the zero point folded, in
+    // v_mfma_i32_32x32x32_i8 operand order [ceil(N/32)][K/32][64][16], and records [K/128][ceil(N/32)][32] of
+    // {s, -1.5 * 2^23 * s, z, 0}
+    bool has_prefill = false;
+    std::int8_t* prefill_codes = nullptr;
+    float* prefill_meta = nullptr;
+    void* prefill_alloc = nullptr;
+    std::size_t prefill_bytes = 0;
 };
 
 // The kernel sequence a projection call runs (kq_debug_route reports it; run_call dispatches on it).
@@ -44,7 +52,8 @@ enum Route : int {
     ROUTE_GEMV = 5,      // quantize_kernel + gemv_kernel (kq_kernels.hip)
     ROUTE_GEMM = 6,      // quantize_kernel + gemm_kernel (kq_kernels.hip)
     ROUTE_ROWMAJOR = 7,  // quantize_rowmajor_kernel + rowmajor_kernel (kq_kernels.hip)
-    ROUTE_PORTABLE = 8   // portable_kernel (kq_kernels.hip)
+    ROUTE_PORTABLE = 8,  // portable_kernel (kq_kernels.hip)
+    ROUTE_GEMM8 = 9      // quantize_rows8_kernel + gemm8_kernel (kq_gemm8.hip)
 };
 
 // Activation workspace carved out of one device buffer.
@@ -154,6 +163,20 @@ hipError_t launch_gemm_i4g_quantize_dump(const LinearCall& c, std::int8_t* codes
 
 // Records `message` as this thread's kq_last_error() and returns `code` (a kq_status value).
 int set_error(int code, const char* message);
+
+// Prefill projection (M > 16) for 4-bit weights with g = 128 and K a multiple of 256 from the weight's prefill copy
+// (kq_gemm8.hip): a row quantizer into the workspace (codes in the A-operand fragment order, scales [K/128][M_p]),
+// then the int8 GEMM on v_mfma_i32_32x32x32_i8 (K split in ranges with a reduction when the grid is small).
+struct Gemm8Plan {
+    int m_blocks = 0, n_blocks = 0, ksplit = 1;
+};
+bool gemm8_eligible(const Weight& w);  // the geometry a prefill copy is built for
+Gemm8Plan gemm8_plan(const Weight& w, std::int64_t M, bool gelu);
+bool gemm8_fits(const LinearCall& c);
+std::size_t gemm8_partial_bytes(const Weight& w, std::int64_t M, bool gelu);
+// quantize_only: the row quantizer alone (with its parity dumps when d_codes / d_scales / d_sums are set)
+hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t stream, bool quantize_only = false,
+                        std::int8_t* d_codes = nullptr, float* d_scales = nullptr, std::int32_t* d_sums = nullptr);
 
 std::size_t workspace_bytes(const Weight& w, std::int64_t M);
 // GELU gating runs after the projection (through ActBuffers::gelu_tmp) only for tiled weights whose gate/up split

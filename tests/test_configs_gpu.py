@@ -101,7 +101,7 @@ def test_config1_asymmetric_g128_decode(dev, ref, M, K, N):
 
 @pytest.mark.parametrize("M", [512, 2048])
 def test_config2_prefill(dev, ref, M):
-    run_config(ref, dev, f"configs[2] M={M}", 4, 128, M, 2048, 8192, True, 0.0, 120 + M, "gemm_i4_kernel", outliers=0.0)
+    run_config(ref, dev, f"configs[2] M={M}", 4, 128, M, 2048, 8192, True, 0.0, 120 + M, "gemm8_kernel", outliers=0.0)
 
 
 @pytest.mark.parametrize("M", [1, 2048])
@@ -115,8 +115,8 @@ def test_config3_gate_up_gelu(dev, ref, M):
     """The gate/up projection (N = 2 x 8192) through every check, then the GELU-gated form against the oracle's
     gelu_gate of the oracle's projection, and against the oracle's gelu_gate of the GPU's own projection."""
     dw, x, xt, y, y_ref = run_config(ref, dev, f"configs[3] gate/up M={M}", 4, 128, M, 2048, 2 * 8192, True, 0.0,
-                                     140 + M, "decode_kernel" if M == 1 else "gemm_i4_kernel")
-    assert dw.route(xt, 0.0, gelu_gate=True) == ("decode_kernel" if M == 1 else "gemm_i4_kernel")
+                                     140 + M, "decode_kernel" if M == 1 else "gemm8_kernel")
+    assert dw.route(xt, 0.0, gelu_gate=True) == ("decode_kernel" if M == 1 else "gemm8_kernel")
     h = dw.linear(xt, gelu_gate=True)
     torch.cuda.synchronize()
     h_np = h.cpu().numpy()
@@ -127,7 +127,7 @@ def test_config3_gate_up_gelu(dev, ref, M):
 @pytest.mark.parametrize("M", [1, 2048])
 def test_config3_down(dev, ref, M):
     run_config(ref, dev, f"configs[3] down M={M}", 4, 128, M, 8192, 2048, True, 0.0, 150 + M,
-               "decode_kernel" if M == 1 else "gemm_i4_kernel")
+               "decode_kernel" if M == 1 else "gemm8_kernel")
 
 
 @pytest.mark.parametrize("name,bits,group,zp,in_s", [("int2_g32_calibrated", 2, 32, False, 0.03),

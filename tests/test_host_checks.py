@@ -120,7 +120,7 @@ def test_truncated_blob(lib):
 
 
 # kq_debug_route values
-NONE, DECODE, SKINNY, GEMM_I4, GEMM_I4G, GEMV, GEMM, ROWMAJOR, PORTABLE = range(9)
+NONE, DECODE, SKINNY, GEMM_I4, GEMM_I4G, GEMV, GEMM, ROWMAJOR, PORTABLE, GEMM8 = range(10)
 F32, BF16 = 0, 2
 
 
@@ -132,10 +132,13 @@ def test_routes_of_baseline_shapes(lib):
     assert route(lib, 4, 128, 8192, 2048, 1, 1) == DECODE          # configs[1]
     assert route(lib, 4, 128, 2048, 8192, 1, 4) == DECODE
     assert route(lib, 4, 32, 8192, 2048, 0, 1) == DECODE           # configs[0]
-    assert route(lib, 4, 128, 8192, 2048, 1, 2048) == GEMM_I4      # configs[2]
-    assert route(lib, 4, 128, 8192, 2048, 1, 512) == GEMM_I4
+    assert route(lib, 4, 128, 8192, 2048, 1, 2048) == GEMM8        # configs[2]
+    assert route(lib, 4, 128, 8192, 2048, 1, 512) == GEMM8
     assert route(lib, 4, 32, 2560, 2048, 0, 2048) == GEMM_I4G      # configs[3] fused QKV
-    assert route(lib, 4, 128, 16384, 2048, 1, 2048, gelu=1) == GEMM_I4
+    assert route(lib, 4, 128, 16384, 2048, 1, 2048, gelu=1) == GEMM8
+    assert route(lib, 4, 128, 2048, 8192, 1, 2048) == GEMM8        # configs[3] down
+    assert route(lib, 4, 128, 8192, 2048, 2, 2048) == GEMM8        # additive float zeros
+    assert route(lib, 4, 128, 8192, 2048, 0, 2048, in_s=0.05) == GEMM8  # calibrated
     assert route(lib, 2, 32, 8192, 2048, 0, 1, in_s=0.03) == DECODE  # configs[4]
     assert route(lib, 8, 32, 262144, 2048, 0, 8) == DECODE
     assert route(lib, 4, 128, 8192, 2048, 1, 0) == NONE
@@ -154,14 +157,12 @@ def test_routes_of_other_shapes(lib):
     assert route(lib, 4, 128, 8191, 2048, 1, 1, gelu=1) == -1                # odd rows: invalid
 
 
-def test_g128_quantizer_offsets_stay_32_bit(lib):
-    """The g = 128 prefill row quantizer addresses x with 32-bit byte offsets: M * K * element bytes must stay below
-    2^32, so F32 inputs of M * K = 2^30 go to the generic GEMM and BF16 inputs of the same size stay on the fast one."""
+def test_gemm8_activation_panel_bounds(lib):
+    """gemm8's activation buffer is addressed with 32-bit offsets: M_p * K < 2^31, else the next route."""
     K = 2048
-    M = (1 << 30) // K
-    assert route(lib, 4, 128, 256, K, 1, M - 1, x=F32) == GEMM_I4
-    assert route(lib, 4, 128, 256, K, 1, M, x=F32) == GEMM
-    assert route(lib, 4, 128, 256, K, 1, M, x=BF16) == GEMM_I4
+    M = (1 << 31) // K
+    assert route(lib, 4, 128, 256, K, 1, M - 256) == GEMM8
+    assert route(lib, 4, 128, 256, K, 1, M) != GEMM8
 
 
 def test_no_environment_switches_in_launch_plans():

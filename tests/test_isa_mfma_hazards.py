@@ -17,10 +17,10 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["kq_gemm.hip", "kq_gemm_g.hip"]
+SOURCES = ["kq_gemm.hip", "kq_gemm_g.hip", "kq_gemm8.hip"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S"]
-MFMAS = ("v_mfma_i32_16x16x32_i8", "v_mfma_i32_16x16x64_i8", "v_mfma_f32_4x4x1_16b_f32")
+MFMAS = ("v_mfma_i32_16x16x32_i8", "v_mfma_i32_16x16x64_i8", "v_mfma_f32_4x4x1_16b_f32", "v_mfma_i32_32x32x32_i8")
 
 PROBE = r"""
 #include <hip/hip_runtime.h>
@@ -37,6 +37,11 @@ __global__ void p64(const v4i* a, const v4i* b, float* o) {
 __global__ void pw(const v4i* a, const v4i* b, v4i* o) {
     v4i A = a[threadIdx.x], B = b[threadIdx.x];
     o[threadIdx.x] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, A ^ B, 0, 0, 0);
+}
+typedef int v16i __attribute__((ext_vector_type(16)));
+__global__ void p32w(const v4i* a, const v4i* b, float* o) {
+    v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[threadIdx.x], b[threadIdx.x], v16i{0}, 0, 0, 0);
+    o[threadIdx.x] = (float)c[5];
 }
 __global__ void p4(const float* a, const float* b, float* o) {
     v4f c = __builtin_amdgcn_mfma_f32_4x4x1f32(a[threadIdx.x], b[threadIdx.x], v4f{0, 0, 0, 0}, 0, 0, 0);
