@@ -7,9 +7,10 @@
 // h = l / 32, byte p holding k = 8 h + p (p < 8) or 16 + 8 h + p - 8; fragments of one column block are contiguous
 // along K. Per (column, group) a record {s, -1.5 * 2^23 * s, z, 0}.
 //
-// quantize_rows8_kernel: one lane per 32 columns of a row, a lane quad per group (max |x| reduced with DPP), the
-//   codes of (row, 32 columns) written as the two 16-byte halves of the same fragment order (A operand: lane l =
-//   row l % 32), block scales transposed [groups][M_p] in natural row order (and a_s * Q for additive zeros).
+// quantize_rows8_kernel: one wave per 32 rows and one group: each lane reads the 16 columns of its fragment slot in
+//   each of the group's four fragments (A operand: lane l = row l % 32), the two halves of a row combine their max |x|
+//   across lanes l, l ^ 32, and every fragment leaves as one coalesced 1 KiB store; block scales transposed
+//   [groups][M_p] in natural row order (and a_s * Q for additive zeros).
 // gemm8_kernel: workgroup tile 256 rows x 128 columns, 8 waves of 64 x 64 (two 32-row blocks x two 32-column
 //   blocks, two waves per SIMD), one 128-column k step (one group) per iteration. Operands and per-step metadata
 //   (weight records, activation scales) reach LDS through direct copies only (buffer_load ... lds, 16 B per lane,
@@ -119,67 +120,69 @@ struct QRow8Args {
 };
 
 // One lane per 32 columns [32 j, 32 j + 32) of row m; four lanes (a quad) per group of 128 columns.
+// One wave per (32-row block, 128-column group): lane l = row l % 32, fragment half h = l / 32. For each of the group's
+// four 32-column fragments f the lane reads its two 8-column pieces (columns 32 f + 8 h + 0..7 and 32 f + 16 + 8 h +
+// 0..7), so its 16 code bytes are exactly its 16-byte slot of the fragment and each fragment is written as one
+// coalesced 1 KiB store. The row's max |x| over the group combines the two halves through lane l ^ 32.
 template <int QM, bool F32, bool NORM>
 __global__ __launch_bounds__(256) void quantize_rows8_kernel(QRow8Args a) {
-    const int units = a.K / 32;
-    const int t = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
-    const int m = t / units, j = t - m * units;
-    if (m >= a.M_p) return;  // whole waves (M_p * units is a multiple of 64)
+    const int groups = a.K / 128, KC = a.K / 32;
+    const int item = static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x >> 6);
+    if (item >= (a.M_p / 32) * groups) return;  // whole waves
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int mb = item / groups, g = item - mb * groups;
+    const int r = lane & 31, h = lane >> 5;
+    const int m = 32 * mb + r;
     const bool live = m < a.M;
-    float v[32];
+    // v[8 f + 4 p + ...]: piece p (0: columns 32 f + 8 h + 0..7, 1: 32 f + 16 + 8 h + 0..7) of fragment f
+    float v[64];
+    const int c0 = 128 * g + 8 * h;
     if (live) {
-        if constexpr (F32) {
-            const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + static_cast<std::int64_t>(m) * a.K + 32 * j);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 r = src[i];
-                v[4 * i] = r.x;
-                v[4 * i + 1] = r.y;
-                v[4 * i + 2] = r.z;
-                v[4 * i + 3] = r.w;
-            }
-        } else {
-            const uint4* src = reinterpret_cast<const uint4*>(static_cast<const std::uint16_t*>(a.x) + static_cast<std::int64_t>(m) * a.K + 32 * j);
+        for (int f = 0; f < 4; ++f)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint4 r = src[i];
-                const std::uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+            for (int pc = 0; pc < 2; ++pc) {
+                const int col = c0 + 32 * f + 16 * pc;
+                float* d = v + 16 * f + 8 * pc;
+                if constexpr (F32) {
+                    const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + static_cast<std::int64_t>(m) * a.K + col);
+                    const float4 r0 = src[0], r1 = src[1];
+                    d[0] = r0.x; d[1] = r0.y; d[2] = r0.z; d[3] = r0.w;
+                    d[4] = r1.x; d[5] = r1.y; d[6] = r1.z; d[7] = r1.w;
+                } else {
+                    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const std::uint16_t*>(a.x) + static_cast<std::int64_t>(m) * a.K + col);
+                    const std::uint32_t w4[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    v[8 * i + 2 * d] = __uint_as_float(w4[d] << 16);
-                    v[8 * i + 2 * d + 1] = __uint_as_float(w4[d] & 0xFFFF0000u);
+                    for (int e = 0; e < 4; ++e) {
+                        d[2 * e] = __uint_as_float(w4[e] << 16);
+                        d[2 * e + 1] = __uint_as_float(w4[e] & 0xFFFF0000u);
+                    }
+                }
+                if constexpr (NORM) {
+                    const float inv = a.ninv[m];
+                    const float4* wp = reinterpret_cast<const float4*>(a.nw + col);
+                    const float4 n0 = wp[0], n1 = wp[1];
+                    const float nw[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) d[e] = d[e] * inv * nw[e];
                 }
             }
-        }
-        if constexpr (NORM) {
-            const float inv = a.ninv[m];
-            const float4* wp = reinterpret_cast<const float4*>(a.nw + 32 * j);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 w = wp[i];
-                v[4 * i] = v[4 * i] * inv * w.x;
-                v[4 * i + 1] = v[4 * i + 1] * inv * w.y;
-                v[4 * i + 2] = v[4 * i + 2] * inv * w.z;
-                v[4 * i + 3] = v[4 * i + 3] * inv * w.w;
-            }
-        }
     } else {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = 0.F;
+        for (int i = 0; i < 64; ++i) v[i] = 0.F;
     }
     float mx = 0.F, mn = 0.F;
     if constexpr (QM != QUANT_STATIC) {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) quant_stat(QM, v[i], mx, mn);
-        mx = fmaxf(mx, __int_as_float(dpp<0xB1>(__float_as_int(mx))));
-        mx = fmaxf(mx, __int_as_float(dpp<0x4E>(__float_as_int(mx))));
+        for (int i = 0; i < 64; ++i) quant_stat(QM, v[i], mx, mn);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
     }
     const QuantBlock qb = quant_block(QM, mx, mn, a.input_scale, live);
-    // codes as bytes, columns in order: w[i] holds columns 4 i .. 4 i + 3
-    std::uint32_t w[8];
-    if constexpr (QM == QUANT_STATIC) {
+    // codes: w[4 f + i] holds the lane's bytes 4 i .. 4 i + 3 of fragment f (its 16-byte slot)
+    std::uint32_t w[16];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 16; ++i) {
+        if constexpr (QM == QUANT_STATIC) {
             std::uint32_t d = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -187,12 +190,9 @@ __global__ __launch_bounds__(256) void quantize_rows8_kernel(QRow8Args a) {
                 d = __builtin_amdgcn_cvt_pk_u8_f32(c + 128.F, e, d);
             }
             w[i] = d ^ 0x80808080u;
-        }
-    } else {
-        // dynamic: |x * inverse| <= 127 (1 + 2^-24) rounds to at most 127 (no clamp); adding 1.5 * 2^23 rounds
-        // x * inverse to the nearest integer (ties to even, as rint), held in the low mantissa byte
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        } else {
+            // dynamic: |x * inverse| <= 127 (1 + 2^-24) rounds to at most 127 (no clamp); adding 1.5 * 2^23 rounds
+            // x * inverse to the nearest integer (ties to even, as rint), held in the low mantissa byte
             std::uint32_t u[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) u[e] = __float_as_uint(v[4 * i + e] * qb.inverse + kBias);
@@ -200,33 +200,34 @@ __global__ __launch_bounds__(256) void quantize_rows8_kernel(QRow8Args a) {
             w[i] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
         }
     }
-    // fragment halves: h = 0 gets columns 0-7 and 16-23, h = 1 columns 8-15 and 24-31
-    const int mb = m >> 5, r = m & 31;
-    std::int8_t* frag = a.q + (static_cast<std::int64_t>(mb) * units + j) * 1024;
-    *reinterpret_cast<uint4*>(frag + r * 16) = make_uint4(w[0], w[1], w[4], w[5]);
-    *reinterpret_cast<uint4*>(frag + (r + 32) * 16) = make_uint4(w[2], w[3], w[6], w[7]);
+    std::int8_t* frag = a.q + (static_cast<std::int64_t>(mb) * KC + 4 * g) * 1024 + lane * 16;
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+        *reinterpret_cast<uint4*>(frag + f * 1024) = make_uint4(w[4 * f], w[4 * f + 1], w[4 * f + 2], w[4 * f + 3]);
     // code sums of the group (additive float zeros and the parity dump)
     int qsum = 0;
     if (a.az_t || a.d_sums) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < 16; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) qsum += static_cast<std::int8_t>((w[i] >> (8 * e)) & 0xFFu);
-        qsum += dpp<0xB1>(qsum);
-        qsum += dpp<0x4E>(qsum);
+        qsum += __shfl_xor(qsum, 32);
     }
-    const int b = j >> 2;
-    if ((j & 3) == 0) {
-        const std::int64_t o = static_cast<std::int64_t>(b) * a.M_p + m;
+    if (h == 0) {
+        const std::int64_t o = static_cast<std::int64_t>(g) * a.M_p + m;
         if (a.scale_t) a.scale_t[o] = qb.s;
         if (a.az_t) a.az_t[o] = qb.s * static_cast<float>(qsum);
-        if (live && a.d_scales) a.d_scales[static_cast<std::int64_t>(m) * (a.K / 128) + b] = QM == QUANT_STATIC ? a.input_scale : qb.s;
-        if (live && a.d_sums) a.d_sums[static_cast<std::int64_t>(m) * (a.K / 128) + b] = qsum;
+        if (live && a.d_scales) a.d_scales[static_cast<std::int64_t>(m) * groups + g] = QM == QUANT_STATIC ? a.input_scale : qb.s;
+        if (live && a.d_sums) a.d_sums[static_cast<std::int64_t>(m) * groups + g] = qsum;
     }
     if (live && a.d_codes) {
-        uint4* dst = reinterpret_cast<uint4*>(a.d_codes + static_cast<std::int64_t>(m) * a.K + 32 * j);
-        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        // natural column order: piece p of fragment f holds columns 32 f + 16 p + 8 h + 0..7
+        std::int8_t* dst = a.d_codes + static_cast<std::int64_t>(m) * a.K + c0;
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+#pragma unroll
+            for (int pc = 0; pc < 2; ++pc)
+                *reinterpret_cast<uint2*>(dst + 32 * f + 16 * pc) = make_uint2(w[4 * f + 2 * pc], w[4 * f + 2 * pc + 1]);
     }
 }
 
@@ -320,20 +321,21 @@ template <int K0, int K1, bool DBG>
 __device__ __forceinline__ void epi_dump(const v16i& P, __amdgpu_buffer_rsrc_t dres, std::uint32_t voff, std::uint32_t row_bytes,
                                          std::uint32_t g_bytes) {
     if constexpr (DBG && K0 < K1) {
-        int v;  // (inline assembly keeps this read of the MFMA result in the epilogue's place)
+        int v = 0;  // (inline assembly keeps this read of the MFMA result in the epilogue's place)
         KQ_ASM("v_subrev_u32 %0, %1, %2" : "=v"(v) : "v"(kBiasBits), "v"(P[K0]));
         __builtin_amdgcn_raw_buffer_store_b32(v, dres, voff, (8 * (K0 >> 2) + (K0 & 3)) * row_bytes + g_bytes, 0);
         epi_dump<K0 + 1, K1, DBG>(P, dres, voff, row_bytes, g_bytes);
     }
 }
 struct Dump {
-    __amdgpu_buffer_rsrc_t res;
-    std::uint32_t row_bytes;  // N * groups * 4
+    const std::int32_t* base;  // the tile's first row
+    std::uint32_t bytes;       // the buffer's extent from base
+    std::uint32_t row_bytes;   // N * groups * 4
 };
 template <int K0, int K1, bool SF16, bool STAT, bool ZF, bool DBG>
 __device__ __forceinline__ void epi_range(float (&acc)[16], v16i& P, const v4i& rec, float as, float az, const Dump& d,
                                           std::uint32_t voff, int g) {
-    epi_dump<K0, K1, DBG>(P, d.res, voff, d.row_bytes, static_cast<std::uint32_t>(g) * 4);
+    if constexpr (DBG) epi_dump<K0, K1, DBG>(P, rsrc(d.base, d.bytes), voff, d.row_bytes, static_cast<std::uint32_t>(g) * 4);
     epi_converts<K0, K1, SF16, STAT>(P, rec);
     epi_accumulates<K0, K1, SF16, STAT, ZF>(acc, P, rec, as, az);
 }
@@ -383,6 +385,82 @@ __device__ __forceinline__ void store8(const Gemm8Args& a, const float (&acc)[2]
     }
 }
 
+// 4 x 4 transpose inside each lane quad: on entry lane q of the quad holds v[e] = element (row e, column q); on exit
+// v[e] = element (row q, column e). Two butterfly rounds of quad_perm DPP moves and lane-parity selects.
+__device__ __forceinline__ void quad_transpose(float (&v)[4], int lane) {
+    const bool b0 = lane & 1, b1 = lane & 2;
+    const int x0 = __float_as_int(v[0]), x1 = __float_as_int(v[1]), x2 = __float_as_int(v[2]), x3 = __float_as_int(v[3]);
+    const int s0 = dpp<0xB1>(x1), s1 = dpp<0xB1>(x0), s2 = dpp<0xB1>(x3), s3 = dpp<0xB1>(x2);  // lanes q ^ 1
+    const int u0 = b0 ? s0 : x0, u1 = b0 ? x1 : s1, u2 = b0 ? s2 : x2, u3 = b0 ? x3 : s3;
+    const int t0 = dpp<0x4E>(u2), t1 = dpp<0x4E>(u3), t2 = dpp<0x4E>(u0), t3 = dpp<0x4E>(u1);  // lanes q ^ 2
+    v[0] = __int_as_float(b1 ? t0 : u0);
+    v[1] = __int_as_float(b1 ? t1 : u1);
+    v[2] = __int_as_float(b1 ? u2 : t2);
+    v[3] = __int_as_float(b1 ? u3 : t3);
+}
+
+// store8 with 16-byte stores: each 4 x 4 sub-block (rows 8 j + 4 h + 0..3, four columns of a lane quad) is transposed
+// in the quad, so lane q writes row 8 j + 4 h + q, columns 4 (col / 4) .. + 3. Every lane issues exactly
+// kTileStores (kTileStoresGelu) stores; rows past M and columns past N fall outside the buffer resource, whose range
+// check drops them, so the number of outstanding vector memory operations after a tile is known at compile time.
+constexpr int kTileStores = 16, kTileStoresGelu = 8;
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+template <bool STAT, bool GELU>
+__device__ __forceinline__ void store8t(const Gemm8Args& a, const float (&acc)[2][2][16], int m0, int wm, const int (&gc)[2],
+                                        int lane) {
+    const int n_out = GELU ? (a.N >> 1) : a.N;
+    const int rows = min(a.M - m0, kBM);
+    const __amdgpu_buffer_rsrc_t yres = rsrc(a.y + static_cast<std::int64_t>(m0) * n_out, static_cast<std::uint32_t>(rows) * n_out * 4);
+    const int r_lane = 64 * wm + 4 * (lane >> 5) + (lane & 3), c_lane = lane & 28;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const std::uint32_t row_off = static_cast<std::uint32_t>(r_lane + 32 * i + 8 * j) * n_out;
+#pragma unroll
+            for (int c = 0; c < (GELU ? 1 : 2); ++c) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int k = 4 * j + e;
+                    if constexpr (GELU) {
+                        float g = acc[i][0][k], up = acc[i][1][k];
+                        if (STAT) {
+                            g = g * a.input_scale;
+                            up = up * a.input_scale;
+                        }
+                        v[e] = gelu_tanh(calibrate_output(g, a.output_scale)) * calibrate_output(up, a.output_scale);
+                    } else {
+                        float x = acc[i][c][k];
+                        if (STAT) x = x * a.input_scale;
+                        v[e] = calibrate_output(x, a.output_scale);
+                    }
+                }
+                quad_transpose(v, lane);
+                const int n = 32 * gc[c] + c_lane;
+                const bool live = GELU ? (gc[0] < (a.NB >> 1) && n < n_out) : n < n_out;
+                const std::uint32_t voff = live ? (row_off + static_cast<std::uint32_t>(n)) * 4 : 0x80000000u;
+                __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])},
+                                                      yres, voff, 0, 0);
+            }
+        }
+    }
+}
+
+// One work item of gemm8_kernel: K range, tile, the tile's first row and its column block. (Declared at namespace
+// scope: local classes in a kernel template keep the host pass from emitting the kernel's launch stub.)
+struct Item {
+    int ks, tile, m0, nbk;
+};
+// Copy parameters of one item and wave: the activation and weight sources, the weight extent, the metadata offset at
+// the item's first k step, and that step.
+struct Copy {
+    const std::int8_t* abase;
+    const std::int8_t* bbase;
+    std::uint32_t bbytes, meta0;
+    int kbase;
+};
+
 template <bool SF16, bool STAT, bool ZF, bool GELU, bool SPLIT, bool DBG>
 __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
@@ -391,64 +469,113 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     const int wm = wave & 3, wn = wave >> 2;  // rows [64 wm, +64) of the tile; column blocks below
     const std::uint32_t lds0 = lds_addr(lds);
 
-    // workgroup -> (K range, row block, column block); consecutive workgroups run on different XCDs, so each XCD takes
-    // a contiguous range of tiles, row blocks fastest (the XCD's few column blocks of weights stay in its L2)
+    // Work items (K range, row block, column block) in an order that gives each XCD a contiguous range of tiles, row
+    // blocks fastest (the XCD's few column blocks of weights stay in its L2): item i of the launch is tile
+    // (i % 8) (total / 8) + i / 8 when total % 8 == 0. The launch holds at most one workgroup per CU; workgroup b runs
+    // items b, b + G, b + 2 G, ... back to back, with the copy ring running on across item boundaries, so the copies of
+    // an item's first steps are in flight during the previous item's last steps and its output stores overlap the next
+    // item's MFMAs.
     const int tiles = a.m_blocks * a.n_blocks;
     const int total = tiles * a.ksplit;
-    int bid = blockIdx.x;
-    if (total % 8 == 0) bid = (bid % 8) * (total / 8) + bid / 8;
-    const int ks = bid / tiles, tile = bid % tiles;
-    const int mb = tile % a.m_blocks, nbk = tile / a.m_blocks;
-    const int m0 = mb * kBM;
+    const int G = static_cast<int>(gridDim.x);
+    const int bx = static_cast<int>(blockIdx.x);
+    const int items = (total - bx + G - 1) / G;
     const int KC = a.K / 32;
-    const int steps = a.K / kStepK / a.ksplit, s0 = ks * steps;
+    const int steps = a.K / kStepK / a.ksplit;
+    auto item_of = [&](int r) __attribute__((always_inline)) {
+        int i = r * G + bx;
+        if (total % 8 == 0) i = (i % 8) * (total / 8) + i / 8;
+        Item it;
+        it.ks = i / tiles;
+        it.tile = i - it.ks * tiles;
+        it.m0 = (it.tile % a.m_blocks) * kBM;
+        it.nbk = it.tile / a.m_blocks;
+        return it;
+    };
 
     // ---- copies of one step: wave w brings activation row block w (4 fragments), half of weight column block w / 2
     // (2 fragments) and one metadata block: w = 0, 1 the weight records of column blocks 0-1 / 2-3, w = 2 the tile's
-    // activation scales, w = 3 its a_s * Q (additive zeros); the other copies write zeros into the dummy area
-    const __amdgpu_buffer_rsrc_t ares = rsrc(a.q + static_cast<std::int64_t>(m0 / 32) * KC * 1024,
-                                             static_cast<std::uint32_t>(kBM / 32) * KC * 1024);
+    // activation scales, w = 3 its a_s * Q (additive zeros); the other copies write zeros into the dummy area.
+    // issue(u, r, t): the copies of step t of item r (t may run past the item: the next items' steps) into stage u % 3;
+    // past the last item, the last step again, into a stage nothing reads any more.
     const int cbc = wave >> 1, ckc = 2 * (wave & 1);
-    const int gcb = col_block<GELU>(a, nbk, cbc);
-    const bool clive = gcb < a.NB;
-    const __amdgpu_buffer_rsrc_t bres = rsrc(a.w + static_cast<std::int64_t>(clive ? gcb : 0) * KC * 1024,
-                                             clive ? static_cast<std::uint32_t>(KC) * 1024 : 0u);
+    // The wave's metadata copy: its resource, per-step stride and LDS place do not depend on the item (dummy: mdst < 0).
     __amdgpu_buffer_rsrc_t mres = rsrc(a.wmeta, 0u);
-    std::uint32_t meta_base = 0x80000000u, meta_step = 0;
-    int meta_dst = kDummyOff;
+    std::uint32_t meta_step = 0;
+    int mdst = -1;
     if (wave < 2) {
-        const int blk = col_block<GELU>(a, nbk, 2 * wave);  // first of two adjacent global column blocks
         mres = rsrc(a.wmeta, static_cast<std::uint32_t>(a.groups) * a.NB * 512);
-        meta_base = static_cast<std::uint32_t>(blk) * 512 + lane * 16;
         meta_step = static_cast<std::uint32_t>(a.NB) * 512;
-        meta_dst = kWOff + wave * 1024;
+        mdst = kWOff + wave * 1024;
     } else if ((wave == 2 && !STAT) || (wave == 3 && ZF)) {
         mres = rsrc(wave == 2 ? a.scale_t : a.az_t, static_cast<std::uint32_t>(a.groups) * a.M_p * 4);
-        meta_base = static_cast<std::uint32_t>(m0) * 4 + lane * 16;
         meta_step = static_cast<std::uint32_t>(a.M_p) * 4;
-        meta_dst = wave == 2 ? kSOff : kZOff;
+        mdst = wave == 2 ? kSOff : kZOff;
     }
-    auto issue = [&](int step) {
-        const int st = step < steps ? step : steps - 1;  // past the range: the last step again, into an unread stage
-        std::uint8_t* base = lds + (step % kStages) * kStageBytes;
-        const std::uint32_t kc0 = static_cast<std::uint32_t>((s0 + st) * 4);
+    auto copy_of = [&](int r) __attribute__((always_inline)) {
+        const Item it = item_of(r);
+        Copy cp;
+        cp.kbase = it.ks * steps;
+        cp.abase = a.q + static_cast<std::int64_t>(it.m0 / 32) * KC * 1024;
+        const int gcb = col_block<GELU>(a, it.nbk, cbc);
+        const bool clive = gcb < a.NB;
+        cp.bbase = a.w + static_cast<std::int64_t>(clive ? gcb : 0) * KC * 1024;
+        cp.bbytes = clive ? static_cast<std::uint32_t>(KC) * 1024 : 0u;
+        cp.meta0 = 0x80000000u;
+        if (wave < 2)
+            cp.meta0 = static_cast<std::uint32_t>(cp.kbase) * meta_step + static_cast<std::uint32_t>(col_block<GELU>(a, it.nbk, 2 * wave)) * 512;
+        else if (mdst >= 0)
+            cp.meta0 = static_cast<std::uint32_t>(cp.kbase) * meta_step + static_cast<std::uint32_t>(it.m0) * 4;
+        return cp;
+    };
+    // part 0: activation fragments 0-1, part 1: activation fragments 2-3, part 2: weight fragments and metadata
+    auto issue_copy = [&](const Copy& cp, int u, int t, auto part) __attribute__((always_inline)) {
+        constexpr int pt = decltype(part)::value;
+        const std::uint32_t kc0 = static_cast<std::uint32_t>((cp.kbase + t) * 4);
+        std::uint8_t* base = lds + (u % kStages) * kStageBytes;
+        if constexpr (pt < 2) {
+            const __amdgpu_buffer_rsrc_t ares = rsrc(cp.abase, static_cast<std::uint32_t>(kBM / 32) * KC * 1024);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(base + kAOff + (wave * 4 + i) * 1024), 16, lane * 16,
-                                                     (static_cast<std::uint32_t>(wave) * KC + kc0 + i) * 1024, 0, 0);
+            for (int i = 2 * pt; i < 2 * pt + 2; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(base + kAOff + (wave * 4 + i) * 1024), 16, lane * 16,
+                                                         (static_cast<std::uint32_t>(wave) * KC + kc0 + i) * 1024, 0, 0);
+        } else {
+            const __amdgpu_buffer_rsrc_t bres = rsrc(cp.bbase, cp.bbytes);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(base + kBOff + (cbc * 4 + ckc + i) * 1024), 16,
-                                                     lane * 16, (kc0 + ckc + i) * 1024, 0, 0);
-        const __amdgpu_buffer_rsrc_t mr = mres;
-        std::uint8_t* mdst = meta_dst == kDummyOff ? lds + kDummyOff : base + meta_dst;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(mr, (lds_void*)mdst, 16, meta_base,
-                                                 meta_step * static_cast<std::uint32_t>(s0 + st), 0, 0);
+            for (int i = 0; i < 2; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(base + kBOff + (cbc * 4 + ckc + i) * 1024), 16,
+                                                         lane * 16, (kc0 + ckc + i) * 1024, 0, 0);
+            std::uint8_t* md = mdst < 0 ? lds + kDummyOff : base + mdst;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_void*)md, 16, lane * 16, cp.meta0 + static_cast<std::uint32_t>(t) * meta_step, 0, 0);
+        }
+    };
+    // issue(u, r, t): the copies of step t of item r into stage u % 3; t may run past the item (the next items' steps),
+    // and past the last item the last step is copied again, into a stage nothing reads any more. item_copy holds the copy
+    // parameters of the item being computed.
+    Copy item_copy = copy_of(0);
+    auto issue_part = [&](int u, int r, int t, auto part) __attribute__((always_inline)) {
+        if (t < steps) {
+            issue_copy(item_copy, u, t, part);
+            return;
+        }
+        while (t >= steps) {
+            t -= steps;
+            ++r;
+        }
+        if (r >= items) {
+            r = items - 1;
+            t = steps - 1;
+        }
+        issue_copy(copy_of(r), u, t, part);
+    };
+    auto issue = [&](int u, int r, int t) __attribute__((always_inline)) {
+        issue_part(u, r, t, std::integral_constant<int, 0>{});
+        issue_part(u, r, t, std::integral_constant<int, 1>{});
+        issue_part(u, r, t, std::integral_constant<int, 2>{});
     };
 
     // ---- the wave's fragments: row blocks 2 wm + i; column blocks (plain) 2 wn + i, (GELU) wn + 2 i
     const int cb_l0 = GELU ? wn : 2 * wn, cb_l1 = GELU ? wn + 2 : 2 * wn + 1;
-    const int gc[2] = {col_block<GELU>(a, nbk, cb_l0), col_block<GELU>(a, nbk, cb_l1)};
     const std::uint32_t a_lane = lds0 + kAOff + (2 * wm * 4) * 1024 + lane * 16;
     const std::uint32_t b_lane0 = lds0 + kBOff + (cb_l0 * 4) * 1024 + lane * 16;
     const std::uint32_t b_lane1 = lds0 + kBOff + (cb_l1 * 4) * 1024 + lane * 16;
@@ -457,7 +584,7 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     [[maybe_unused]] const std::uint32_t w_lane1 = lds0 + kWOff + (cb_l1 * 32 + col) * 16;
     [[maybe_unused]] const std::uint32_t s_lane = lds0 + kSOff + (64 * wm + bcast_row(lane)) * 4;
     [[maybe_unused]] const std::uint32_t z_lane = lds0 + kZOff + (64 * wm + bcast_row(lane)) * 4;
-    auto read_meta = [&](Meta& mt, std::uint32_t stage) {
+    auto read_meta = [&](Meta& mt, std::uint32_t stage) __attribute__((always_inline)) {
         KQ_ASM("ds_read_b128 %0, %1" : "=v"(mt.rec[0]) : "v"(w_lane0 + stage));
         KQ_ASM("ds_read_b128 %0, %1" : "=v"(mt.rec[1]) : "v"(w_lane1 + stage));
         if constexpr (!STAT) {
@@ -469,34 +596,48 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             KQ_ASM("ds_read_b32 %0, %1 offset:128" : "=v"(mt.az[1]) : "v"(z_lane + stage));
         }
     };
-    auto read4 = [&](v4i (&f)[4], std::uint32_t addr) {
+    auto read4 = [&](v4i (&f)[4], std::uint32_t addr) __attribute__((always_inline)) {
         ds_read16<0>(f[0], addr);
         ds_read16<1024>(f[1], addr);
         ds_read16<2048>(f[2], addr);
         ds_read16<3072>(f[3], addr);
     };
 
-    // parity dump (DBG): P' of element (row, column n, group g) at dump[(row N + n) G + g]; dvo[i][c] is the byte
-    // offset of the lane's element 0 in block (i, c), beyond the buffer for columns past N
+    // ---- per item: the wave's global column blocks, the tile's first row, and the parity dump's resource and offsets
+    // (DBG: P' of element (row, column n, group g) at dump[(row N + n) G + g]; dvo[i][c] is the byte offset of the lane's
+    // element 0 in block (i, c), beyond the buffer for columns past N)
+    int gc[2] = {0, 0};
+    int m0 = 0, ks = 0, tile = 0;
     Dump dmp{};
     std::uint32_t dvo[2][2] = {{0u, 0u}, {0u, 0u}};
-    if constexpr (DBG) {
-        // the resource starts at this tile's first row, so every offset stays far below 2^31
-        const std::uint64_t row_elems = static_cast<std::uint64_t>(a.N) * a.groups;
-        const std::uint64_t rest = static_cast<std::uint64_t>(a.M - m0) * row_elems * 4;
-        dmp.res = rsrc(a.dump + static_cast<std::uint64_t>(m0) * row_elems,
-                       static_cast<std::uint32_t>(rest < 0x7FFFFFFFull ? rest : 0x7FFFFFFFull));
-        dmp.row_bytes = static_cast<std::uint32_t>(row_elems * 4);
+    auto begin_item = [&](int r) __attribute__((always_inline)) {
+        const Item it = item_of(r);
+        if (r > 0) item_copy = copy_of(r);
+        m0 = it.m0;
+        ks = it.ks;
+        tile = it.tile;
+        gc[0] = col_block<GELU>(a, it.nbk, cb_l0);
+        gc[1] = col_block<GELU>(a, it.nbk, cb_l1);
+        if constexpr (DBG) {
+            // the resource starts at the tile's first row, so every offset stays far below 2^31
+            const std::uint64_t row_elems = static_cast<std::uint64_t>(a.N) * a.groups;
+            const std::uint64_t rest = static_cast<std::uint64_t>(a.M - m0) * row_elems * 4;
+            dmp.base = a.dump + static_cast<std::uint64_t>(m0) * row_elems;
+            dmp.bytes = static_cast<std::uint32_t>(rest < 0x7FFFFFFFull ? rest : 0x7FFFFFFFull);
+            dmp.row_bytes = static_cast<std::uint32_t>(row_elems * 4);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const int n = 32 * gc[c] + col, r0 = 64 * wm + 32 * i + 4 * (lane >> 5);
-                dvo[i][c] = (gc[c] < a.NB && n < a.N && m0 + r0 < a.M)
-                                ? static_cast<std::uint32_t>((static_cast<std::uint64_t>(r0) * a.N + n) * a.groups * 4)
-                                : 0x80000000u;
-            }
-    }
+                for (int c = 0; c < 2; ++c) {
+                    const int n = 32 * gc[c] + col, r0 = 64 * wm + 32 * i + 4 * (lane >> 5);
+                    dvo[i][c] = (gc[c] < a.NB && n < a.N && m0 + r0 < a.M)
+                                    ? static_cast<std::uint32_t>((static_cast<std::uint64_t>(r0) * a.N + n) * a.groups * 4)
+                                    : 0x80000000u;
+                }
+        }
+    };
+    // vector memory operations a lane issues when it stores a tile (outstanding after the tile)
+    constexpr int kStoresAfter = SPLIT ? 16 : (GELU ? kTileStoresGelu : kTileStores);
 
     float acc[2][2][16];
 #pragma unroll
@@ -510,7 +651,7 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     for (int k = 0; k < 16; ++k) bias[k] = kBiasBits;
     KQ_ASM("" : "+v"(bias));  // opaque: never rematerialized next to an MFMA
     // P[1] starts as the bias and the metadata of "step -1" as zeros: the epilogue step 0 runs for the block before its
-    // first one adds exactly 0
+    // first one adds exactly 0 (likewise at every item start)
     v16i P[2];
     P[0] = bias;
     P[1] = bias;
@@ -526,9 +667,9 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     }
 
     // prologue: three stages in flight; step 0's operands (but A row block 1) and metadata in registers
-    issue(0);
-    issue(1);
-    issue(2);
+    issue(0, 0, 0);
+    issue(1, 0, 1);
+    issue(2, 0, 2);
     KQ_ASM("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     read4(A[0], a_lane);
     read4(B0, b_lane0);
@@ -544,15 +685,15 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     //   b3 (1, 1) -> P1: gap: A row block 0 and B column block 0 of step t + 1;  epilogue of b2
     // Stage t % 3 is read from b2 of step t - 1 to b0 of step t; the mid-step barrier of step t comes after every
     // wave waited for those reads, and after every wave's copies of step t + 1 (issued at mid-step t - 2) landed.
-    auto step_body = [&](int t, auto parity) {
+    auto step_body = [&](int t, int u, int r, auto parity, bool wide) __attribute__((always_inline)) {
         constexpr int p = decltype(parity)::value;
         Meta& cur = mt[p];
         Meta& prv = mt[p ^ 1];
         v4i (&Bc)[4] = B1[p];
         v4i (&Bn)[4] = B1[p ^ 1];
-        const std::uint32_t st_now = static_cast<std::uint32_t>((t % kStages) * kStageBytes);
-        const std::uint32_t st_next = static_cast<std::uint32_t>(((t + 1) % kStages) * kStageBytes);
-        const int g = s0 + t;
+        const std::uint32_t st_now = static_cast<std::uint32_t>((u % kStages) * kStageBytes);
+        const std::uint32_t st_next = static_cast<std::uint32_t>(((u + 1) % kStages) * kStageBytes);
+        const int g = ks * steps + t;
         // ---- b0
         lgkm_wait<0>(A[0], B0, Bc, cur.rec, cur.as, cur.az);  // step t's operands and metadata (read during step t - 1)
         mfma_first(P[0], A[0][0], B0[0], bias);
@@ -576,8 +717,10 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0], cur.as[0], cur.az[0], dmp, dvo[0][0], g);
         // ---- mid-step
         lgkm_wait<0>(A[1]);
-        KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(kCopies) : "memory");
-        issue(t + 3);
+        // the first two steps after a tile's stores: those stores are younger than step t + 1's copies
+        if (wide) KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(kCopies + kStoresAfter) : "memory");
+        else KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(kCopies) : "memory");
+        issue(u + 3, r, t + 3);
         // ---- b2
         mfma_first(P[0], A[1][0], B0[0], bias);
         read4(Bn, b_lane1 + st_next);
@@ -599,28 +742,51 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         mfma_acc(P[1], A[1][3], Bc[3]);
         epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0], cur.as[1], cur.az[1], dmp, dvo[1][0], g);
     };
-    for (int t = 0; t < steps; t += 2) {
-        step_body(t, std::integral_constant<int, 0>{});
-        step_body(t + 1, std::integral_constant<int, 1>{});
-    }
-    // drain: the epilogue of the last step's b3 (step steps - 1, parity 1)
-    KQ_ASM("s_nop 11");
-    epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], mt[1].rec[1], mt[1].as[1], mt[1].az[1], dmp, dvo[1][1], s0 + steps - 1);
-    KQ_ASM("s_waitcnt vmcnt(0)" ::: "memory");  // the copies past the range land before the workgroup ends
-
-    if constexpr (SPLIT) {
-        v4f* dst = reinterpret_cast<v4f*>(a.partial + ((static_cast<std::int64_t>(ks) * tiles + tile) * kThreads + tid) * 64);
+    int u = 0;  // global step: stage u % 3
+    for (int r = 0; r < items; ++r) {
+        begin_item(r);
+        for (int t = 0; t < steps; t += 2, u += 2) {
+            const bool wide = r > 0 && t == 0;
+            step_body(t, u, r, std::integral_constant<int, 0>{}, wide);
+            step_body(t + 1, u + 1, r, std::integral_constant<int, 1>{}, wide);
+        }
+        // the reads issued in the last step (the next item's step 0 operands and metadata) land before the registers
+        // they target can be given to anything else (after the last item nothing reads them)
+        lgkm_wait<0>(A[0], B0, B1, mt[0].rec, mt[0].as, mt[0].az);
+        // drain: the epilogue of the item's last b3 (step steps - 1, parity 1)
+        KQ_ASM("s_nop 11");
+        epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], mt[1].rec[1], mt[1].as[1], mt[1].az[1], dmp, dvo[1][1],
+                                              ks * steps + steps - 1);
+        if constexpr (SPLIT) {
+            v4f* dst = reinterpret_cast<v4f*>(a.partial + ((static_cast<std::int64_t>(ks) * tiles + tile) * kThreads + tid) * 64);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4)
+                        __builtin_nontemporal_store(v4f{acc[i][c][4 * q4], acc[i][c][4 * q4 + 1], acc[i][c][4 * q4 + 2], acc[i][c][4 * q4 + 3]},
+                                                    dst + (i * 2 + c) * 4 + q4);
+        } else {
+            store8t<STAT, GELU>(a, acc, m0, wm, gc, lane);
+        }
+        // the next item starts from zero accumulators, the bias and "step -1" metadata zeros (its step 0 operands and
+        // metadata were read during this item's last step)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4)
-                    __builtin_nontemporal_store(v4f{acc[i][c][4 * q4], acc[i][c][4 * q4 + 1], acc[i][c][4 * q4 + 2], acc[i][c][4 * q4 + 3]},
-                                                dst + (i * 2 + c) * 4 + q4);
-    } else {
-        store8<STAT, GELU>(a, acc, m0, wm, gc, lane);
+                for (int k = 0; k < 16; ++k) acc[i][c][k] = 0.F;
+        P[1] = bias;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            mt[1].rec[i] = v4i{0, 0, 0, 0};
+            mt[1].as[i] = 0.F;
+            mt[1].az[i] = 0.F;
+        }
     }
+    KQ_ASM("s_waitcnt vmcnt(0)" ::: "memory");  // the copies past the range land before the workgroup ends
 }
 
 // Split K: the ranges' partial accumulators of one tile added in range order, then the same final stores.
@@ -662,6 +828,21 @@ __global__ __launch_bounds__(kThreads) void gemm8_reduce_kernel(Gemm8Args a) {
 // ------------------------------------------------------------------------------------------------------------------
 // Host side
 
+namespace {
+// Compute units of the current device (one persistent workgroup each), cached per device.
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+}  // namespace
+
 bool gemm8_eligible(const Weight& w) {
     return w.tiled && w.geo.bits == 4 && w.geo.group == 128 && w.geo.cols % 256 == 0 && w.geo.cols_p == w.geo.cols;
 }
@@ -687,6 +868,7 @@ bool gemm8_fits(const LinearCall& c) {
     if (c.path != PATH_BLOCKWISE && c.path != PATH_SYMMETRIC) return false;
     if (c.path == PATH_SYMMETRIC && w.zero_mode != ZERO_NONE) return false;
     if (c.gelu_gate && ((w.geo.rows / 2) % 32)) return false;
+    if (w.geo.rows % 4) return false;  // 16-byte output stores of four columns
     if ((reinterpret_cast<std::uintptr_t>(c.x) & 15u) || (c.norm_inv && (reinterpret_cast<std::uintptr_t>(c.norm_w1) & 15u)))
         return false;
     const std::int64_t M_p = round_up(c.M, kBM);
@@ -750,7 +932,7 @@ hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t 
     q.d_scales = d_scales;
     q.d_sums = d_sums;
     {
-        const dim3 grid(static_cast<unsigned>(static_cast<std::int64_t>(M_p) * (K / 32) / 256)), block(256);
+        const dim3 grid(static_cast<unsigned>((static_cast<std::int64_t>(M_p / 32) * (K / 128) + 3) / 4)), block(256);
         const bool f32 = c.x_type == ACT_F32, norm = c.norm_inv != nullptr;
 #define KQ_Q8(QM, F, NM) hipLaunchKernelGGL((quantize_rows8_kernel<QM, F, NM>), grid, block, 0, stream, q)
         if (stat) {
@@ -786,7 +968,8 @@ hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t 
     g.input_scale = c.input_scale;
     g.output_scale = c.output_scale;
     const bool split = p.ksplit > 1, dbg = c.dump != nullptr, sf16 = w.scale_type == META_F16;
-    const unsigned blocks = static_cast<unsigned>(p.m_blocks * p.n_blocks * p.ksplit);
+    const int total = p.m_blocks * p.n_blocks * p.ksplit;
+    const unsigned blocks = static_cast<unsigned>(std::min(total, device_cus()));  // persistent: items loop in the kernel
     hipError_t e;
 #define KQ_G8(SF, ST, Z) e = c.gelu_gate ? launch8_split<SF, ST, Z, true>(g, blocks, split, dbg, stream) \
                                          : launch8_split<SF, ST, Z, false>(g, blocks, split, dbg, stream)
