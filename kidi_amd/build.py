@@ -14,6 +14,9 @@ ROOT = os.path.dirname(HERE)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 SOURCES = ["csrc/kq_kernels.hip", "csrc/kq_skinny.hip", "csrc/kq_decode.hip", "csrc/kq_gemm.hip", "csrc/kq_gemm_g.hip", "csrc/kq_gemm8.hip", "csrc/kq_greedy.hip", "csrc/kq_norm.hip", "csrc/kq_pack.hip", "csrc/kq_noalloc.hip", "csrc/kq_api.cpp", "csrc/kq_layout_host.cpp"]
 LIB = os.path.join(HERE, "lib", "libkq_hip.so")
+# The C++ adapter over the C ABI (Kidi's PACKED_LINEAR plug-in, compiled against a restatement of its contract).
+ADAPTER_SOURCES = ["adapter/kidi_runtime.cpp", "adapter/packed_linear.cpp"]
+ADAPTER_LIB = os.path.join(HERE, "lib", "libkq_adapter.so")
 # Per-source flags: the decode kernels take their first nine scalar arguments preloaded into SGPRs at wave launch
 # (gfx950 kernel-argument preloading; on firmware without it the code object's preamble loads them as usual).
 EXTRA = {"csrc/kq_decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"]}
@@ -59,7 +62,23 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
     if not incremental:
         for o in objs:
             os.remove(o)
+    build_adapter(verbose)
     return LIB
+
+
+def build_adapter(verbose: bool = False) -> str:
+    """lib/libkq_adapter.so: the C++20 adapter, linked against lib/libkq_hip.so (found next to it at run time)."""
+    tmp = ADAPTER_LIB + ".tmp"
+    cmd = [HIPCC, "-std=c++20", "-O2", "-fPIC", "-shared", "-Wall", "-I", os.path.join(ROOT, "include"),
+           *[os.path.join(HERE, s) for s in ADAPTER_SOURCES], "-L", os.path.dirname(LIB), "-lkq_hip",
+           "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    if p.returncode != 0:
+        raise RuntimeError("hipcc failed for the adapter:\n" + p.stdout.decode(errors="replace"))
+    os.replace(tmp, ADAPTER_LIB)
+    return ADAPTER_LIB
 
 
 if __name__ == "__main__":

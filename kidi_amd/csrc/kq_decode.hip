@@ -588,7 +588,8 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
             }
         }
     }
-    __syncthreads();  // the reduction buffer is reused by the next pair
+    // the reduction buffer is reused by the next pair; greedy selection reads the running best below
+    if (GREEDY || pair + 1 < pend) __syncthreads();
     }
     if constexpr (GREEDY) {
         if (threadIdx.x < M)

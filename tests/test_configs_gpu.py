@@ -152,3 +152,34 @@ def test_config4_head_greedy(dev, ref, M):
     scale = float(np.max(np.abs(y_ref)))
     for r in range(M):
         assert y_ref[r, tok[r]] >= y_ref[r].max() - TOL * scale
+
+
+@pytest.mark.parametrize("M", [512, 2048])
+def test_config2_published_f16_zero(dev, ref, M):
+    """configs[2] shape in the published package format (benchmarks/gemma4/arm/run.py:151, :694-695): F16
+    weight_scale and F16 weight_zero = round_f16((8 - zp) * scale), an additive float zero that is not exactly
+    (8 - zp) * scale. It reaches the MFMA prefill GEMM (float-zero variant); the projection is within 2e-3 of the oracle
+    and the int32 partials sum q * c with the signed codes c = u - 8."""
+    from kidi_amd.ops import DeviceWeight
+
+    K, N = 2048, 8192
+    rng = np.random.default_rng(180 + M)
+    values, scales, zp, codes = weights(rng, N, K, 4, 128, zero_points=True)
+    zf = ((8.0 - zp.astype(np.float32)) * scales.astype(np.float32)).astype(np.float16)
+    assert np.any(zf.astype(np.float32) != (8.0 - zp.astype(np.float32)) * scales.astype(np.float32))
+    x = activations(rng, M, K, 0.001)
+    dw = DeviceWeight(to_dev(values, dev), to_dev(scales, dev), 4, 128, to_dev(zf, dev))
+    xt = to_dev(x, dev).to(torch.bfloat16)
+    assert dw.route(xt) == "gemm8_kernel"
+    y = dw.linear(xt)
+    y_d, P_d = dw.debug_partials(xt)
+    torch.cuda.synchronize()
+    y_np = y.cpu().numpy()
+    np.testing.assert_array_equal(y_np, y_d.cpu().numpy())
+    y_ref, path = ref.packed_linear(x, values, scales, 4, 128, zeros=zf, threads=THREADS)
+    assert path == ref.PATH_BLOCKWISE
+    check_close(y_np, y_ref)
+    rows, cols = sample(M, 6, rng), sample(N, 64, rng)
+    P = P_d[torch.from_numpy(rows).to(dev)][:, torch.from_numpy(cols).to(dev)].cpu().numpy().astype(np.int64)
+    q, _, _, zpa = ref.quantize_dynamic(x[rows], 128, 4)
+    np.testing.assert_array_equal(P, expected_partials(ref, q, codes[cols], zpa, 4, 128))
