@@ -153,6 +153,14 @@ kq_status kq_packed_linear_gelu_gate(const kq_weight* weight, const kq_linear_ar
  * Asynchronous on `stream`; no workspace. */
 kq_status kq_lowbit_parity_linear(const kq_weight* weight, const kq_linear_args* args, void* stream);
 
+/* Operation::GELU_MULTIPLY / SILU_MULTIPLY: y = act(gate) * value element by element over `count` F32 values of two
+ * tensors of one shape (Context::gelu_multiply / silu_multiply, src/kidi/ops/context.cpp:944-957; GatedMultiplyOp,
+ * runtime/ynn/operators.cpp:267-311), the slice form of the gated feed-forward (layers/gemma4.cpp:213-225) with the
+ * expressions of kq_packed_linear_gelu_gate's gating (GELU-tanh) and the SiLU gate. Device pointers; `y` may be `gate`
+ * or `value` (in place); asynchronous on `stream`. */
+kq_status kq_gelu_multiply(const float* gate, const float* value, int64_t count, float* y, void* stream);
+kq_status kq_silu_multiply(const float* gate, const float* value, int64_t count, float* y, void* stream);
+
 /* Gated feed-forward of one decoder layer: Context::gated_feed_forward (src/kidi/ops/context.cpp:970-996) ->
  * Operation::GATED_FEED_FORWARD, run by PackedFeedForward (runtime/ynn/operators.cpp:1321-1517) for calibrated
  * inputs. `gate_up` holds [gate rows; up rows] (2*I rows, K columns), `down` holds K rows of I columns, equal bits.

@@ -28,7 +28,7 @@ EXPORTS = (
     "kq_greedy_workspace_size", "kq_greedy_token", "kq_greedy_linear_workspace_size", "kq_packed_linear_greedy",
     "kq_weight_export_size", "kq_weight_export", "kq_weight_import", "kq_rms_norm", "kq_rms_linear_workspace_size",
     "kq_packed_linear_rms", "kq_quantize_weight", "kq_debug_read_floor", "kq_debug_route", "kq_debug_route_shape",
-    "kq_lowbit_parity_linear", "kq_packed_linear_noalloc",
+    "kq_lowbit_parity_linear", "kq_packed_linear_noalloc", "kq_gelu_multiply", "kq_silu_multiply",
 )
 
 # kq_debug_route values: the kernel sequence a projection call runs
@@ -163,6 +163,9 @@ def load() -> ctypes.CDLL:
     L.kq_greedy_workspace_size.restype = sz
     L.kq_greedy_token.argtypes = [vp, i64, i64, vp, vp, sz, vp]
     L.kq_greedy_token.restype = ctypes.c_int
+    for name in ("kq_gelu_multiply", "kq_silu_multiply"):
+        getattr(L, name).argtypes = [vp, vp, i64, vp, vp]
+        getattr(L, name).restype = ctypes.c_int
     L.kq_greedy_linear_workspace_size.argtypes = [vp, i64]
     L.kq_greedy_linear_workspace_size.restype = sz
     L.kq_packed_linear_greedy.argtypes = [vp, ctypes.POINTER(LinearArgs), vp, vp]

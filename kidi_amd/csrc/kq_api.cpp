@@ -974,6 +974,24 @@ size_t kq_greedy_workspace_size(int64_t rows, int64_t width) {
     return align_up(static_cast<std::size_t>(rows * kq::greedy_chunk_count(width)) * 16);
 }
 
+static kq_status gated_multiply(const float* gate, const float* value, int64_t count, float* y, bool silu, void* stream) {
+    if (count < 0) return fail(KQ_INVALID_ARGUMENT, silu ? "SiLU multiplication requires matching floating tensors"
+                                                         : "GELU multiplication requires matching floating tensors");
+    if (count == 0) return KQ_OK;
+    if (!gate || !value || !y) return fail(KQ_INVALID_ARGUMENT, "null gate, value or output");
+    if (hipError_t e = kq::launch_gated_multiply(gate, value, count, silu, y, static_cast<hipStream_t>(stream)); e != hipSuccess)
+        return hip_fail(e, "gated multiply launch");
+    return KQ_OK;
+}
+
+kq_status kq_gelu_multiply(const float* gate, const float* value, int64_t count, float* y, void* stream) {
+    return gated_multiply(gate, value, count, y, false, stream);
+}
+
+kq_status kq_silu_multiply(const float* gate, const float* value, int64_t count, float* y, void* stream) {
+    return gated_multiply(gate, value, count, y, true, stream);
+}
+
 kq_status kq_greedy_token(const float* logits, int64_t rows, int64_t width, int32_t* tokens, void* workspace,
                           size_t workspace_bytes, void* stream) {
     if (rows < 0 || width < 1) return fail(KQ_INVALID_ARGUMENT, "greedy selection requires [rows, width > 0] logits");

@@ -188,6 +188,7 @@ ActBuffers carve_workspace(const Weight& w, std::int64_t M, void* base);
 hipError_t launch_quantize(const LinearCall& c, hipStream_t stream);
 hipError_t launch_linear(const LinearCall& c, hipStream_t stream);
 hipError_t launch_gelu_gate(const float* in, std::int64_t M, std::int64_t I, float* out, hipStream_t stream);
+hipError_t launch_gated_multiply(const float* gate, const float* value, std::int64_t n, bool silu, float* out, hipStream_t stream);
 hipError_t launch_silu_gate(const float* in, std::int64_t M, std::int64_t I, float* out, hipStream_t stream);
 
 // Greedy token selection (kq_greedy.hip): partials {max, first index, non-finite} per (row, 4096-column chunk) of

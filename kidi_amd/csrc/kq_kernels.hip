@@ -795,6 +795,28 @@ __global__ __launch_bounds__(256) void silu_gate_kernel(const float* in, std::in
     out[id] = g / (1.F + expf(-g)) * in[m * 2 * I + I + i];
 }
 
+// act(gate) * value over two matching F32 buffers: Context::gelu_multiply / silu_multiply (ops/context.cpp:944-957),
+// the slice form of the two gate kernels above (layers/gemma4.cpp:213-225), with their expressions, so
+// gated_multiply(g, u) equals the gate kernels on [g | u] bit for bit. Four elements per thread (16-byte accesses
+// when the buffers allow).
+template <bool SILU>
+__device__ __forceinline__ float gated(float g, float u) {
+    if constexpr (SILU) return g / (1.F + expf(-g)) * u;
+    return gelu_tanh(g) * u;
+}
+template <bool SILU, bool VEC>
+__global__ __launch_bounds__(256) void gated_multiply_kernel(const float* gate, const float* value, std::int64_t n, float* out) {
+    const std::int64_t i0 = (static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+    if (i0 >= n) return;
+    if (VEC && i0 + 4 <= n) {
+        const float4 g = *reinterpret_cast<const float4*>(gate + i0), u = *reinterpret_cast<const float4*>(value + i0);
+        *reinterpret_cast<float4*>(out + i0) = make_float4(gated<SILU>(g.x, u.x), gated<SILU>(g.y, u.y), gated<SILU>(g.z, u.z),
+                                                          gated<SILU>(g.w, u.w));
+        return;
+    }
+    for (std::int64_t i = i0; i < n && i < i0 + 4; ++i) out[i] = gated<SILU>(gate[i], value[i]);
+}
+
 __global__ __launch_bounds__(256) void unpermute_kernel(const std::int8_t* q, std::int64_t M, std::int64_t K,
                                                         std::int64_t cols_p, std::int8_t* codes) {
     const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -934,6 +956,20 @@ hipError_t launch_linear(const LinearCall& c, hipStream_t stream) {
     const int kind = c.path == PATH_PORTABLE ? 2 : (c.w->tiled ? 0 : 1);
     if (c.w->scale_type == META_F16) return dispatch_bits<__half>(c, stream, kind);
     return dispatch_bits<float>(c, stream, kind);
+}
+
+hipError_t launch_gated_multiply(const float* gate, const float* value, std::int64_t n, bool silu, float* out, hipStream_t stream) {
+    const bool vec = !((reinterpret_cast<std::uintptr_t>(gate) | reinterpret_cast<std::uintptr_t>(value) |
+                        reinterpret_cast<std::uintptr_t>(out)) & 15u);
+    const dim3 grid(static_cast<unsigned>((n + 1023) / 1024)), block(256);
+    if (silu) {
+        if (vec) hipLaunchKernelGGL((gated_multiply_kernel<true, true>), grid, block, 0, stream, gate, value, n, out);
+        else hipLaunchKernelGGL((gated_multiply_kernel<true, false>), grid, block, 0, stream, gate, value, n, out);
+    } else {
+        if (vec) hipLaunchKernelGGL((gated_multiply_kernel<false, true>), grid, block, 0, stream, gate, value, n, out);
+        else hipLaunchKernelGGL((gated_multiply_kernel<false, false>), grid, block, 0, stream, gate, value, n, out);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_gelu_gate(const float* in, std::int64_t M, std::int64_t I, float* out, hipStream_t stream) {

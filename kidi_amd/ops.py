@@ -13,11 +13,14 @@ from __future__ import annotations
 import collections
 import ctypes
 import math
+import struct
+import time
 from dataclasses import dataclass
 
 import torch
 
 from . import _native as N
+from .profiling import Profiler
 
 
 class Failure(RuntimeError):
@@ -329,6 +332,19 @@ def greedy_token(logits: torch.Tensor) -> torch.Tensor:
     return tokens.reshape(logits.shape[:-1])
 
 
+def gated_multiply(gate: torch.Tensor, value: torch.Tensor, silu: bool = False) -> torch.Tensor:
+    """GELU_MULTIPLY / SILU_MULTIPLY on device F32 tensors of one shape (kq_gelu_multiply / kq_silu_multiply)."""
+    name = "SiLU" if silu else "GELU"
+    if (gate is None or value is None or gate.dtype != torch.float32 or value.dtype != gate.dtype
+            or tuple(gate.shape) != tuple(value.shape)):
+        raise Failure("INVALID_ARGUMENT", f"{name} multiplication requires matching floating tensors")
+    g, v = gate.contiguous(), value.contiguous()
+    y = torch.empty_like(g)
+    fn = N.load().kq_silu_multiply if silu else N.load().kq_gelu_multiply
+    _raise(fn(g.data_ptr(), v.data_ptr(), g.numel(), y.data_ptr(), _stream()))
+    return y
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, epsilon: float, residual: torch.Tensor | None = None,
              output_scale: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """RMS_NORM / RMS_NORM_RESIDUAL over the last axis of device F32/BF16 x (kq_rms_norm): F32 output."""
@@ -386,6 +402,11 @@ CHECKPOINT, LOWBIT_PARITY = "checkpoint", "lowbit-parity"
 _PRECISION_NAMES = {"checkpoint": CHECKPOINT, "lowbit-parity": LOWBIT_PARITY, "checkpoint-parity": LOWBIT_PARITY}
 
 
+def _f32_bits(v: float) -> int:
+    """std::bit_cast<std::int32_t>(float) (the output_scale attribute, ops/context.cpp:932)."""
+    return struct.unpack("<i", struct.pack("<f", float(v)))[0]
+
+
 class Context:
     """The packed-linear slice of ops::Context on one HIP device."""
 
@@ -398,6 +419,30 @@ class Context:
         self._zeros: dict = {}
         self._bound: dict = {}  # weight storage -> (source, PackedWeight, packed_prefill, asymmetric_clip)
         self.decode_projections = False  # Context's decode flag: bound weights take the packed path at any M
+        self._profiler = Profiler(self.device)  # KIDI_PROFILE_OPS=host|sync (kidi_amd/profiling.py)
+
+    # ---- per-operation profiling (ops/context.cpp:117-133, :406-438, :502-515) ----
+    def profile_phase(self, phase: str) -> None:
+        """Context::profile_phase: label the following calls; "encoder" / "gemma4_request" count requests for
+        KIDI_PROFILE_OPS_SKIP."""
+        self._profiler.profile_phase(phase)
+
+    def synchronize(self) -> None:
+        """Context::synchronize: wait for the device (timed per phase while profiling)."""
+        self._profiler.synchronize()
+
+    def profile_report(self) -> list[str]:
+        """The kidi_op / kidi_op_sync lines the context prints when it is closed."""
+        return self._profiler.report()
+
+    def close(self) -> None:
+        self._profiler.close()
+
+    def __del__(self):
+        try:
+            self._profiler.close()
+        except Exception:
+            pass
 
     def prepare_linear_weights(self, weight: torch.Tensor, bits: int, group_size: int = 128,
                                packed_prefill: bool = False, asymmetric_clip: bool = False) -> None:
@@ -457,7 +502,9 @@ class Context:
         if found is not None:
             self._prepared.move_to_end(key)
             return found[0]
+        started = time.perf_counter_ns()
         dw = DeviceWeight(weight, scales, bits, group_size, zeros)
+        self._profiler.prepare_ns += time.perf_counter_ns() - started
         self._prepared[key] = (dw, weight, scales, zeros)
         if len(self._prepared) > self.CAPACITY:
             self._prepared.popitem(last=False)
@@ -483,17 +530,22 @@ class Context:
                       zeros: torch.Tensor | None = None) -> torch.Tensor:
         """Context::packed_linear (ops/context.cpp:821-939): PACKED_LINEAR under CHECKPOINT precision, Kidi's
         LOWBIT_PARITY projection under that precision (:917-932). F32 [..., N] output."""
-        if self.precision == LOWBIT_PARITY:
-            return self._lowbit_parity(input, weight, scales, bits, group_size, input_scale, output_scale)
-        self._validate(input, weight, scales, bits, group_size, input_scale, output_scale)
         bound = zeros if zeros is not None else self._zeros.get(_identity(scales))
-        dw = self._prepare(weight, scales, bits, group_size, bound)
-        host = not input.is_cuda
-        x = input.to(self.device) if host else input
-        y = dw.linear(x, input_scale, output_scale)
-        if host:  # a HIP op behind a CPU tensor returns host-visible results (synchronous)
-            y = y.cpu()
-        return y
+        operands = [input, weight, scales] + ([bound] if bound is not None and self.precision != LOWBIT_PARITY else [])
+        with self._profiler.call("packed_linear", [t.shape for t in operands],
+                                 [bits, group_size, _f32_bits(output_scale)]) as rec:
+            if self.precision == LOWBIT_PARITY:
+                rec["output"] = self._lowbit_parity(input, weight, scales, bits, group_size, input_scale, output_scale)
+                return rec["output"]
+            self._validate(input, weight, scales, bits, group_size, input_scale, output_scale)
+            dw = self._prepare(weight, scales, bits, group_size, bound)
+            host = not input.is_cuda
+            x = input.to(self.device) if host else input
+            y = dw.linear(x, input_scale, output_scale)
+            if host:  # a HIP op behind a CPU tensor returns host-visible results (synchronous)
+                y = y.cpu()
+            rec["output"] = y
+            return y
 
     def _lowbit_parity(self, input, weight, scales, bits, group_size, input_scale, output_scale):
         # Context::packed_linear's scale check (ops/context.cpp:824-825), its LOWBIT_PARITY domain (:919-929), then
@@ -529,11 +581,15 @@ class Context:
         if weight.shape[0] % 2:
             raise Failure("INVALID_ARGUMENT", "GELU gate requires floating [..., 2 * intermediate] input")
         bound = zeros if zeros is not None else self._zeros.get(_identity(scales))
-        dw = self._prepare(weight, scales, bits, group_size, bound)
-        host = not input.is_cuda
-        x = input.to(self.device) if host else input
-        y = dw.linear(x, input_scale, output_scale, gelu_gate=True)
-        return y.cpu() if host else y
+        operands = [input, weight, scales] + ([bound] if bound is not None else [])
+        with self._profiler.call("packed_linear+gelu_gate", [t.shape for t in operands],
+                                 [bits, group_size, _f32_bits(output_scale)]) as rec:
+            dw = self._prepare(weight, scales, bits, group_size, bound)
+            host = not input.is_cuda
+            x = input.to(self.device) if host else input
+            y = dw.linear(x, input_scale, output_scale, gelu_gate=True)
+            rec["output"] = y.cpu() if host else y
+            return rec["output"]
 
     def gated_feed_forward(self, input: torch.Tensor, gate_up_weight: torch.Tensor, gate_up_scales: torch.Tensor,
                            down_weight: torch.Tensor, down_scales: torch.Tensor, bits: int, input_size: int,
@@ -554,13 +610,17 @@ class Context:
         self._validate(hidden, down_weight, down_scales, bits, intermediate_size, down_input_scale, down_output_scale)
         if down_weight.shape[0] != input_size:
             raise Failure("INVALID_ARGUMENT", "gated feed-forward shape mismatch")
-        gu = self._prepare(gate_up_weight, gate_up_scales, bits, input_size, None)
-        dn = self._prepare(down_weight, down_scales, bits, intermediate_size, None)
-        host = not input.is_cuda
-        x = input.to(self.device) if host else input
-        y = gated_feed_forward(gu, dn, x, gate_up_input_scale, gate_up_output_scale, down_input_scale,
-                               down_output_scale, silu)
-        return y.cpu() if host else y
+        with self._profiler.call("gated_feed_forward",
+                                 [t.shape for t in (input, gate_up_weight, gate_up_scales, down_weight, down_scales)],
+                                 [bits, input_size, intermediate_size, int(silu)]) as rec:
+            gu = self._prepare(gate_up_weight, gate_up_scales, bits, input_size, None)
+            dn = self._prepare(down_weight, down_scales, bits, intermediate_size, None)
+            host = not input.is_cuda
+            x = input.to(self.device) if host else input
+            y = gated_feed_forward(gu, dn, x, gate_up_input_scale, gate_up_output_scale, down_input_scale,
+                                   down_output_scale, silu)
+            rec["output"] = y.cpu() if host else y
+            return rec["output"]
 
     @staticmethod
     def _validate_norm(input, scale, epsilon, residual=None, output_scale=None):
@@ -577,10 +637,12 @@ class Context:
     def rms_norm(self, input: torch.Tensor, scale: torch.Tensor, epsilon: float) -> torch.Tensor:
         """Context::rms_norm (ops/context.cpp:1043-1049): F32 output; host tensors return host results."""
         self._validate_norm(input, scale, epsilon)
-        host = not input.is_cuda
-        x = input.to(self.device) if host else input
-        y = rms_norm(x, scale.to(self.device), epsilon)
-        return y.cpu() if host else y
+        with self._profiler.call("rms_norm", [input.shape, scale.shape], []) as rec:
+            host = not input.is_cuda
+            x = input.to(self.device) if host else input
+            y = rms_norm(x, scale.to(self.device), epsilon)
+            rec["output"] = y.cpu() if host else y
+            return rec["output"]
 
     def rms_norm_residual(self, input: torch.Tensor, scale: torch.Tensor, residual: torch.Tensor, epsilon: float,
                           output_scale: torch.Tensor | None = None) -> torch.Tensor:
@@ -588,19 +650,46 @@ class Context:
         if residual is None:
             raise Failure("INVALID_ARGUMENT", "invalid RMS residual normalization operands")
         self._validate_norm(input, scale, epsilon, residual, output_scale)
-        host = not input.is_cuda
-        x = input.to(self.device) if host else input
-        r = residual.to(self.device) if host else residual
-        o = output_scale.to(self.device).reshape(1) if output_scale is not None else None
-        y = rms_norm(x, scale.to(self.device), epsilon, residual=r, output_scale=o)
-        return y.cpu() if host else y
+        operands = [input, scale, residual] + ([output_scale] if output_scale is not None else [])
+        with self._profiler.call("rms_norm_residual", [t.shape for t in operands], []) as rec:
+            host = not input.is_cuda
+            x = input.to(self.device) if host else input
+            r = residual.to(self.device) if host else residual
+            o = output_scale.to(self.device).reshape(1) if output_scale is not None else None
+            y = rms_norm(x, scale.to(self.device), epsilon, residual=r, output_scale=o)
+            rec["output"] = y.cpu() if host else y
+            return rec["output"]
+
+    def gelu_multiply(self, gate: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
+        """Context::gelu_multiply (ops/context.cpp:944-950): gelu_tanh(gate) * value over matching F32 tensors, the
+        slice form of the gated feed-forward (layers/gemma4.cpp:213-225)."""
+        return self._gated_multiply(gate, value, False)
+
+    def silu_multiply(self, gate: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
+        """Context::silu_multiply (ops/context.cpp:951-957): silu(gate) * value over matching F32 tensors."""
+        return self._gated_multiply(gate, value, True)
+
+    def _gated_multiply(self, gate, value, silu):
+        name = "SiLU" if silu else "GELU"
+        if (gate is None or value is None or gate.dtype != torch.float32 or value.dtype != gate.dtype
+                or tuple(gate.shape) != tuple(value.shape)):
+            raise Failure("INVALID_ARGUMENT", f"{name} multiplication requires matching floating tensors")
+        with self._profiler.call("silu_multiply" if silu else "gelu_multiply", [gate.shape, value.shape], []) as rec:
+            host = not gate.is_cuda
+            g = gate.to(self.device) if host else gate
+            v = value.to(self.device) if not value.is_cuda else value
+            y = gated_multiply(g, v, silu)
+            rec["output"] = y.cpu() if host else y
+            return rec["output"]
 
     def greedy_token(self, logits: torch.Tensor) -> torch.Tensor:
         """Context::greedy_token: I32 [...] of F32 logits [..., width]; a scalar is INVALID_ARGUMENT
         (eager_test.cpp:254-260). Host logits return host tokens."""
         if logits.dim() == 0 or logits.shape[-1] == 0:
             raise Failure("INVALID_ARGUMENT", "greedy selection requires [..., width > 0] logits")
-        host = not logits.is_cuda
-        x = logits.to(self.device, torch.float32) if host else logits.float()
-        t = greedy_token(x)
-        return t.cpu() if host else t
+        with self._profiler.call("greedy_token", [logits.shape], []) as rec:
+            host = not logits.is_cuda
+            x = logits.to(self.device, torch.float32) if host else logits.float()
+            t = greedy_token(x)
+            rec["output"] = t.cpu() if host else t
+            return rec["output"]
