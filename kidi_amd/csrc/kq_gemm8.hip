@@ -347,44 +347,6 @@ __device__ __forceinline__ void mfma_acc(v16i& P, const v4i& A, const v4i& B) {
     KQ_ASM("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(P) : "v"(A), "v"(B));
 }
 
-// Final values of a wave's 2 x 2 blocks: calibrated inputs scale by input_scale, calibrated outputs round to
-// output_scale steps, GELU pairs column block 0 (gate) with 1 (up).
-template <bool STAT, bool GELU>
-__device__ __forceinline__ void store8(const Gemm8Args& a, const float (&acc)[2][2][16], int m0, int wm, const int (&gc)[2],
-                                       int lane) {
-    const int col = lane & 31;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const int row = m0 + 64 * wm + 32 * i + 8 * (k >> 2) + 4 * (lane >> 5) + (k & 3);
-            if (row >= a.M) continue;
-            if constexpr (GELU) {
-                const int half_n = a.N >> 1;
-                const int n = 32 * gc[0] + col;
-                if (gc[0] >= (a.NB >> 1) || n >= half_n) continue;
-                float g = acc[i][0][k], up = acc[i][1][k];
-                if (STAT) {
-                    g = g * a.input_scale;
-                    up = up * a.input_scale;
-                }
-                g = calibrate_output(g, a.output_scale);
-                up = calibrate_output(up, a.output_scale);
-                a.y[static_cast<std::int64_t>(row) * half_n + n] = gelu_tanh(g) * up;
-            } else {
-#pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const int n = 32 * gc[c] + col;
-                    if (n >= a.N) continue;
-                    float v = acc[i][c][k];
-                    if (STAT) v = v * a.input_scale;
-                    a.y[static_cast<std::int64_t>(row) * a.N + n] = calibrate_output(v, a.output_scale);
-                }
-            }
-        }
-    }
-}
-
 // 4 x 4 transpose inside each lane quad: on entry lane q of the quad holds v[e] = element (row e, column q); on exit
 // v[e] = element (row q, column e). Two butterfly rounds of quad_perm DPP moves and lane-parity selects.
 __device__ __forceinline__ void quad_transpose(float (&v)[4], int lane) {
@@ -399,7 +361,8 @@ __device__ __forceinline__ void quad_transpose(float (&v)[4], int lane) {
     v[3] = __int_as_float(b1 ? u3 : t3);
 }
 
-// store8 with 16-byte stores: each 4 x 4 sub-block (rows 8 j + 4 h + 0..3, four columns of a lane quad) is transposed
+// Final values of a wave's 2 x 2 blocks (calibrated inputs scale by input_scale, calibrated outputs round to
+// output_scale steps, GELU pairs column block 0 (gate) with 1 (up)), stored with 16-byte stores: each 4 x 4 sub-block (rows 8 j + 4 h + 0..3, four columns of a lane quad) is transposed
 // in the quad, so lane q writes row 8 j + 4 h + q, columns 4 (col / 4) .. + 3. Every lane issues exactly
 // kTileStores (kTileStoresGelu) stores; rows past M and columns past N fall outside the buffer resource, whose range
 // check drops them, so the number of outstanding vector memory operations after a tile is known at compile time.
@@ -758,15 +721,16 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], mt[1].rec[1], mt[1].as[1], mt[1].az[1], dmp, dvo[1][1],
                                               ks * steps + steps - 1);
         if constexpr (SPLIT) {
-            v4f* dst = reinterpret_cast<v4f*>(a.partial + ((static_cast<std::int64_t>(ks) * tiles + tile) * kThreads + tid) * 64);
+            // partial tile [16 chunks][512 threads][4 floats]: chunk j of every thread is one coalesced 8 KiB run
+            v4f* dst = reinterpret_cast<v4f*>(a.partial) + (static_cast<std::int64_t>(ks) * tiles + tile) * 16 * kThreads + tid;
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int c = 0; c < 2; ++c)
 #pragma unroll
                     for (int q4 = 0; q4 < 4; ++q4)
-                        __builtin_nontemporal_store(v4f{acc[i][c][4 * q4], acc[i][c][4 * q4 + 1], acc[i][c][4 * q4 + 2], acc[i][c][4 * q4 + 3]},
-                                                    dst + (i * 2 + c) * 4 + q4);
+                        dst[((i * 2 + c) * 4 + q4) * kThreads] =
+                            v4f{acc[i][c][4 * q4], acc[i][c][4 * q4 + 1], acc[i][c][4 * q4 + 2], acc[i][c][4 * q4 + 3]};
         } else {
             store8t<STAT, GELU>(a, acc, m0, wm, gc, lane);
         }
@@ -805,22 +769,27 @@ __global__ __launch_bounds__(kThreads) void gemm8_reduce_kernel(Gemm8Args a) {
 #pragma unroll
             for (int k = 0; k < 16; ++k) acc[i][c][k] = 0.F;
     for (int ks = 0; ks < a.ksplit; ++ks) {
-        const v4f* src = reinterpret_cast<const v4f*>(a.partial + ((static_cast<std::int64_t>(ks) * tiles + tile) * kThreads + tid) * 64);
+        const v4f* src = reinterpret_cast<const v4f*>(a.partial) + (static_cast<std::int64_t>(ks) * tiles + tile) * 16 * kThreads + tid;
+        v4f v[16];  // all of a range's chunks in flight at once
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = src[j * kThreads];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) KQ_ASM("" : "+v"(v[j]));  // every load issued before the first add
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) {
-                    const v4f v = __builtin_nontemporal_load(src + (i * 2 + c) * 4 + q4);
-                    acc[i][c][4 * q4] += v[0];
-                    acc[i][c][4 * q4 + 1] += v[1];
-                    acc[i][c][4 * q4 + 2] += v[2];
-                    acc[i][c][4 * q4 + 3] += v[3];
+                    const v4f& w = v[(i * 2 + c) * 4 + q4];
+                    acc[i][c][4 * q4] += w[0];
+                    acc[i][c][4 * q4 + 1] += w[1];
+                    acc[i][c][4 * q4 + 2] += w[2];
+                    acc[i][c][4 * q4 + 3] += w[3];
                 }
     }
     const int gc[2] = {col_block<GELU>(a, nbk, GELU ? wn : 2 * wn), col_block<GELU>(a, nbk, GELU ? wn + 2 : 2 * wn + 1)};
-    store8<STAT, GELU>(a, acc, mb * kBM, wm, gc, lane);
+    store8t<STAT, GELU>(a, acc, mb * kBM, wm, gc, lane);
 }
 
 }  // namespace
