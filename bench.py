@@ -52,6 +52,9 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-extras", action="store_true",
                    help="skip the configs[3]/configs[4] projections and the fused-operator timings")
+    p.add_argument("--floor-sweep", action="store_true",
+                   help="print the single-launch read floor and empty-launch cost over launch geometries "
+                        "(kq_debug_read_floor_shape) as a table and exit")
     p.add_argument("--pmc-workload", action="store_true",
                    help="run the HBM-traffic workload for rocprofv3 --pmc passes (a plain 256 MiB copy for calibration, "
                         "then every rotated decode projection twice, one launch each, no graphs) and exit")
@@ -216,6 +219,58 @@ def cpu_baseline(torch, values, scales, zp, x, g, budget_s):
             "label": "build restatement of the reference CPU path (the reference's ynnpack path cannot be built)"}
 
 
+def floor_sweep(torch, lib, dev, gen, args):
+    """Single-launch read floor of the configs[1] decode's bytes over launch geometries: per (threads per workgroup,
+    16-byte loads per lane) the device time per launch of kq_debug_read_floor_shape over R rotated buffers, timed as
+    `value` is (exactly --steps launches right behind the cache flush, median of five regions), and of an empty kernel
+    of the same grid (graph-replayed, per launch)."""
+    fb = -(-gemv_bytes(M_DEC, K_DEC, N_DEC, G_DEC) // 16) * 16
+    R = args.rotate
+    bufs = [torch.randint(0, 256, (fb,), dtype=torch.uint8, device=dev, generator=gen) for _ in range(R)]
+    sink = torch.zeros((1,), dtype=torch.int32, device=dev)
+    quiet = Quiet(torch, dev, lib)
+    stream_ptr = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    print(f"read floor sweep: {fb} bytes per launch, {R} rotated buffers, {args.steps} launches per timed region")
+    print("| threads | loads/lane | workgroups | waves | read us/launch | GB/s | % of 8 TB/s | empty us/launch |")
+    print("|---|---|---|---|---|---|---|---|")
+    for threads in (64, 128, 256, 512, 1024):
+        for loads in (1, 2, 4, 8, 16):
+            blocks = -(-fb // (16 * threads * loads))
+            if blocks < 16:
+                continue
+            res = {}
+            for empty in (0, 1):
+                calls = [lambda st, b=b, e=empty: _ok(lib, lib.kq_debug_read_floor_shape(b.data_ptr(), fb, threads, loads, e,
+                                                                                         sink.data_ptr(), st))
+                         for b in bufs]
+                for c in calls:
+                    c(stream_ptr())
+                torch.cuda.synchronize()
+                g = capture(torch, calls, stream_ptr)
+                g.replay()
+                torch.cuda.synchronize()
+                if empty:
+                    res[empty] = timed(torch, quiet, lambda: [g.replay() for _ in range(10)]) * 1e3 / (10 * R)
+                else:
+                    rem = {}
+
+                    def graph_rem(n):
+                        if n not in rem:
+                            rem[n] = capture(torch, calls[:n], stream_ptr)
+                        return rem[n]
+
+                    if args.steps % R:
+                        graph_rem(args.steps % R)
+                    reps = [timed(torch, quiet, lambda: run_steps(torch, calls, 0, args.steps, g, graph_rem, stream_ptr))
+                            for _ in range(5)]
+                    res[empty] = sorted(reps)[2] * 1e3 / args.steps
+                    del rem
+                del g
+            gbs = fb / (res[0] * 1e-6) / 1e9
+            print(f"| {threads} | {loads} | {blocks} | {blocks * threads // 64} | {res[0]:.3f} | {gbs:.0f} | "
+                  f"{100 * gbs / HBM_PEAK_GBS:.1f} | {res[1]:.3f} |", flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -236,6 +291,9 @@ def main():
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
     stream_ptr = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    if args.floor_sweep:
+        floor_sweep(torch, lib, dev, gen, args)
+        return
 
     if args.pmc_workload:
         src = torch.rand((64 << 20,), device=dev, generator=gen)  # 256 MiB float32
@@ -329,7 +387,21 @@ def main():
         gr.replay()
     torch.cuda.synchronize()
     floor_us = timed(torch, quiet, lambda: [gr.replay() for _ in range(20)]) * 1e3 / (20 * R)
-    del gr, bufs, floor_calls
+    # ... and timed exactly as `value` is: --steps launches over the rotated buffers right behind the cache flush,
+    # median of five regions
+    floor_rem = {}
+
+    def floor_graph_rem(n):
+        if n not in floor_rem:
+            floor_rem[n] = capture(torch, floor_calls[:n], stream_ptr)
+        return floor_rem[n]
+
+    if args.steps % R:
+        floor_graph_rem(args.steps % R)
+    floor_reps = [timed(torch, quiet, lambda: run_steps(torch, floor_calls, 0, args.steps, gr, floor_graph_rem, stream_ptr))
+                  for _ in range(5)]
+    floor_like_us = sorted(floor_reps)[2] * 1e3 / args.steps
+    del gr, floor_rem, bufs, floor_calls
 
     del graph_full, rem_graphs
     first_cpu = tuple(t.cpu() for t in first)
@@ -399,9 +471,13 @@ def main():
         "ms_per_step_repeats": [round(v / args.steps, 6) for v in reps_ms],
         "parity": parity,
         "mall_resident_gbs": round(bytes_step / (mall_ms * 1e-3) / 1e9, 1),
-        "read_floor": {"us_per_launch": round(floor_us, 3), "gbs": round(bytes_step / (floor_us * 1e-6) / 1e9, 1),
-                       "frac": round(bytes_step / (floor_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                       "how": "kq_debug_read_floor: one launch reading the same bytes once, rotated buffers, HIP graph"},
+        "read_floor": {"us_per_launch": round(floor_like_us, 3),
+                       "gbs": round(bytes_step / (floor_like_us * 1e-6) / 1e9, 1),
+                       "frac": round(bytes_step / (floor_like_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                       "how": "kq_debug_read_floor: one launch reading the same bytes once (the fastest geometry of "
+                              "bench.py --floor-sweep), rotated buffers, HIP graph, timed exactly as value",
+                       "decode_vs_floor": round(floor_like_us / (ms_per_step * 1e3), 4),
+                       "steady_rotation_us": round(floor_us, 3)},
         "prefill": {"workload": "GEMM M=2048 K=2048 N=8192 asymmetric int4 g=128 (configs[2])",
                     "calls_per_graph": 10,
                     "ms": round(pre_ms, 5), "tops": round(pre_tops, 2),

@@ -297,10 +297,16 @@ int32_t kq_debug_route_shape(int32_t bits, int32_t group_size, int64_t rows, int
 
 /* ---- measurement instrumentation (no counterpart in the reference) ----------------------------------------- */
 
-/* One launch that only reads `bytes` (a multiple of 16, at most 2 GiB) of device memory once, with the launch
- * shape and argument preloading of the decode kernel; `sink` is a device int32 it writes only by chance. Its
- * per-launch time is the floor of any single-launch kernel that streams a buffer of that size. */
+/* One launch that only reads `bytes` (a multiple of 16, at most 2 GiB) of device memory once (512-lane workgroups,
+ * one 16-byte load per lane: the fastest geometry of kq_debug_read_floor_shape's sweep on MI355X; arguments
+ * preloaded as the decode kernel's); `sink` is a device int32 it writes only by chance. Its per-launch time is the
+ * floor of any single-launch kernel that streams a buffer of that size. */
 kq_status kq_debug_read_floor(const void* data, size_t bytes, int32_t* sink, void* stream);
+/* The same read at a chosen launch geometry: `threads` per workgroup (64, 128, 256, 512 or 1024), `loads` 16-byte
+ * loads per lane (1, 2, 4, 8 or 16), ceil(bytes / (16 threads loads)) workgroups; with `empty` nonzero an empty
+ * kernel of that grid instead (the launch cost alone). */
+kq_status kq_debug_read_floor_shape(const void* data, size_t bytes, int32_t threads, int32_t loads, int32_t empty,
+                                    int32_t* sink, void* stream);
 
 /* Host-only (no GPU): the gfx950 tile layout of a Kidi-layout weight and its inverse, for layout tests. */
 size_t kq_layout_bytes(int32_t bits, int32_t group_size, int64_t rows, int64_t cols);

@@ -27,7 +27,8 @@ EXPORTS = (
     "kq_layout_encode_host", "kq_layout_decode_host", "kq_ffn_workspace_size", "kq_gated_feed_forward",
     "kq_greedy_workspace_size", "kq_greedy_token", "kq_greedy_linear_workspace_size", "kq_packed_linear_greedy",
     "kq_weight_export_size", "kq_weight_export", "kq_weight_import", "kq_rms_norm", "kq_rms_linear_workspace_size",
-    "kq_packed_linear_rms", "kq_quantize_weight", "kq_debug_read_floor", "kq_debug_route", "kq_debug_route_shape",
+    "kq_packed_linear_rms", "kq_quantize_weight", "kq_debug_read_floor", "kq_debug_read_floor_shape",
+    "kq_debug_route", "kq_debug_route_shape",
     "kq_lowbit_parity_linear", "kq_packed_linear_noalloc", "kq_gelu_multiply", "kq_silu_multiply",
 )
 
@@ -180,6 +181,8 @@ def load() -> ctypes.CDLL:
     L.kq_quantize_weight.restype = ctypes.c_int
     L.kq_debug_read_floor.argtypes = [vp, ctypes.c_size_t, vp, vp]
     L.kq_debug_read_floor.restype = ctypes.c_int
+    L.kq_debug_read_floor_shape.argtypes = [vp, ctypes.c_size_t, i32, i32, i32, vp, vp]
+    L.kq_debug_read_floor_shape.restype = ctypes.c_int
     L.kq_packed_linear_noalloc.argtypes = [vp, ctypes.POINTER(LinearArgs), vp]
     L.kq_packed_linear_noalloc.restype = ctypes.c_int
     L.kq_lowbit_parity_linear.argtypes = [vp, ctypes.POINTER(LinearArgs), vp]

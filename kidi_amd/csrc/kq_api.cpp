@@ -1352,6 +1352,20 @@ kq_status kq_debug_read_floor(const void* data, size_t bytes, int32_t* sink, voi
     return KQ_OK;
 }
 
+kq_status kq_debug_read_floor_shape(const void* data, size_t bytes, int32_t threads, int32_t loads, int32_t empty,
+                                    int32_t* sink, void* stream) {
+    if (!data || !sink || bytes == 0 || bytes > (std::size_t{1} << 31) || bytes % 16)
+        return fail(KQ_INVALID_ARGUMENT, "read floor: device buffer of 16-byte multiple size up to 2 GiB");
+    if ((threads != 64 && threads != 128 && threads != 256 && threads != 512 && threads != 1024) ||
+        (loads != 1 && loads != 2 && loads != 4 && loads != 8 && loads != 16))
+        return fail(KQ_INVALID_ARGUMENT, "read floor: threads 64/128/256/512/1024 and loads 1/2/4/8/16 per lane");
+    if (hipError_t e = kq::launch_read_floor_shape(data, static_cast<std::uint32_t>(bytes), threads, loads, empty != 0, sink,
+                                                   static_cast<hipStream_t>(stream));
+        e != hipSuccess)
+        return hip_fail(e, "read floor launch");
+    return KQ_OK;
+}
+
 size_t kq_layout_bytes(int32_t bits, int32_t group_size, int64_t rows, int64_t cols) {
     if ((bits != 2 && bits != 4 && bits != 8) || rows <= 0 || cols <= 0) return 0;
     return static_cast<size_t>(kq::Geometry::make(bits, group_size, rows, cols).tile_bytes_total());

@@ -642,21 +642,33 @@ hipError_t launch_modes(const DecodeArgs& a, int g, bool gelu, bool dbg, bool gr
 
 int wave_bytes(int g, int mr) { return mr * 512 + 3 * 4 * mr * (512 / g) + 16; }
 
-// Measurement instrumentation: one launch that reads `bytes` once (8 x 16 bytes per lane, 256-lane workgroups,
-// arguments preloaded like the decode kernel's) and stores nothing unless the data XOR to a magic value: the floor
-// of any single-launch kernel that streams a buffer of this size.
-constexpr int kFloorLoads = 8;
-__global__ __launch_bounds__(256) void read_floor_kernel(const void* data, unsigned bytes, int* sink) {
+// Measurement instrumentation: one launch that reads `bytes` once (one 16-byte load per lane, 512-lane workgroups:
+// the fastest geometry of the launch-geometry sweep below; arguments preloaded like the decode kernel's) and stores
+// nothing unless the data XOR to a magic value: the floor of any single-launch kernel that streams a buffer of this
+// size.
+__global__ __launch_bounds__(512) void read_floor_kernel(const void* data, unsigned bytes, int* sink) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(data, bytes);
+    const unsigned t = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint4 v = ld16(r, 16u * t);  // past `bytes`: zeros
+    if ((v.x ^ v.y ^ v.z ^ v.w) == 0x9e3779b9u) sink[0] = static_cast<int>(t);
+}
+// The same read at another launch geometry (L loads of 16 bytes per lane, any workgroup size up to 1024), and an
+// empty kernel of the same grid, for the launch-geometry sweep of the floor.
+template <int L>
+__global__ __launch_bounds__(1024) void read_floor_shape_kernel(const void* data, unsigned bytes, int* sink) {
     const __amdgpu_buffer_rsrc_t r = rsrc(data, bytes);
     const unsigned total = gridDim.x * blockDim.x;
     const unsigned t = blockIdx.x * blockDim.x + threadIdx.x;
-    uint4 v[kFloorLoads];
+    uint4 v[L];
 #pragma unroll
-    for (int i = 0; i < kFloorLoads; ++i) v[i] = ld16(r, 16u * (t + i * total));  // past `bytes`: zeros
+    for (int i = 0; i < L; ++i) v[i] = ld16(r, 16u * (t + i * total));
     unsigned acc = 0;
 #pragma unroll
-    for (int i = 0; i < kFloorLoads; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    for (int i = 0; i < L; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
     if (acc == 0x9e3779b9u) sink[0] = static_cast<int>(t);
+}
+__global__ __launch_bounds__(1024) void empty_shape_kernel(const void*, unsigned bytes, int* sink) {
+    if (threadIdx.x == 4096) sink[0] = static_cast<int>(bytes);  // never: blockDim.x <= 1024
 }
 
 }  // namespace
@@ -678,9 +690,27 @@ bool decode_fits(const LinearCall& c) {
 }
 
 hipError_t launch_read_floor(const void* data, std::uint32_t bytes, int* sink, hipStream_t stream) {
-    const std::uint32_t per_block = 16u * kFloorLoads * 256u;
-    const unsigned blocks = (bytes + per_block - 1) / per_block;
-    hipLaunchKernelGGL(read_floor_kernel, dim3(blocks), dim3(256), 0, stream, data, bytes, sink);
+    const unsigned blocks = (bytes + 16u * 512u - 1) / (16u * 512u);
+    hipLaunchKernelGGL(read_floor_kernel, dim3(blocks), dim3(512), 0, stream, data, bytes, sink);
+    return hipGetLastError();
+}
+
+hipError_t launch_read_floor_shape(const void* data, std::uint32_t bytes, int threads, int loads, bool empty, int* sink,
+                                   hipStream_t stream) {
+    const std::uint32_t per_block = 16u * static_cast<std::uint32_t>(loads * threads);
+    const dim3 grid((bytes + per_block - 1) / per_block), block(threads);
+    if (empty) {
+        hipLaunchKernelGGL(empty_shape_kernel, grid, block, 0, stream, data, bytes, sink);
+        return hipGetLastError();
+    }
+    switch (loads) {
+        case 1: hipLaunchKernelGGL(read_floor_shape_kernel<1>, grid, block, 0, stream, data, bytes, sink); break;
+        case 2: hipLaunchKernelGGL(read_floor_shape_kernel<2>, grid, block, 0, stream, data, bytes, sink); break;
+        case 4: hipLaunchKernelGGL(read_floor_shape_kernel<4>, grid, block, 0, stream, data, bytes, sink); break;
+        case 8: hipLaunchKernelGGL(read_floor_shape_kernel<8>, grid, block, 0, stream, data, bytes, sink); break;
+        case 16: hipLaunchKernelGGL(read_floor_shape_kernel<16>, grid, block, 0, stream, data, bytes, sink); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

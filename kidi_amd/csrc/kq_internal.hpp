@@ -120,6 +120,8 @@ hipError_t launch_rms_norm(const NormLaunch& n, hipStream_t stream);
 
 // Measurement instrumentation (kq_decode.hip): one launch that only reads `bytes` of `data` once.
 hipError_t launch_read_floor(const void* data, std::uint32_t bytes, int* sink, hipStream_t stream);
+hipError_t launch_read_floor_shape(const void* data, std::uint32_t bytes, int threads, int loads, bool empty, int* sink,
+                                   hipStream_t stream);
 
 // Load-time weight quantization (kq_pack.hip): float weights -> Kidi-layout codes, scales, zeros; error: 1 non-finite
 // weight, 2 symmetric scale underflow (OR-ed into *error).

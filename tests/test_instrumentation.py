@@ -1,6 +1,7 @@
 """Measurement instrumentation of the C ABI: kq_debug_read_floor (the single-launch read floor bench.py reports beside
-the decode roofline) rejects bad arguments on the host and, on the GPU, reads a buffer without writing anything
-but its sink (which it touches only when the data XOR to a magic value)."""
+the decode roofline) and kq_debug_read_floor_shape (the same read at a chosen launch geometry, or an empty kernel of
+that grid) reject bad arguments on the host and, on the GPU, read a buffer without writing anything but their sink
+(which they touch only when the data XOR to a magic value)."""
 
 import ctypes
 
@@ -31,6 +32,15 @@ def test_read_floor_rejects_invalid(native, bad):
         size = (1 << 31) + 16
     assert lib.kq_debug_read_floor(data, size, sink, None) == native.KQ_INVALID_ARGUMENT
     assert lib.kq_last_error()
+    assert lib.kq_debug_read_floor_shape(data, size, 256, 8, 0, sink, None) == native.KQ_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("threads,loads", [(32, 8), (96, 8), (2048, 8), (256, 0), (256, 3), (256, 32)])
+def test_read_floor_shape_rejects_geometry(native, threads, loads):
+    lib = native.load()
+    assert lib.kq_debug_read_floor_shape(ctypes.c_void_p(256), 4096, threads, loads, 0, ctypes.c_void_p(512),
+                                         None) == native.KQ_INVALID_ARGUMENT
+    assert b"threads" in lib.kq_last_error()
 
 
 @pytest.mark.gpu
@@ -48,3 +58,24 @@ def test_read_floor_reads_without_writing():
         torch.cuda.synchronize()
         assert int(sink.item()) == -7
         assert int(buf.sum().item()) == 0
+
+
+@pytest.mark.gpu
+def test_read_floor_shape_reads_without_writing():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from kidi_amd import _native
+
+    lib = _native.load()
+    dev = torch.device("cuda:0")
+    size = 8753152
+    buf = torch.zeros((size,), dtype=torch.uint8, device=dev)
+    sink = torch.full((1,), -7, dtype=torch.int32, device=dev)
+    for threads in (64, 256, 1024):
+        for loads in (1, 4, 16):
+            for empty in (0, 1):
+                assert lib.kq_debug_read_floor_shape(buf.data_ptr(), size, threads, loads, empty, sink.data_ptr(),
+                                                     None) == _native.KQ_OK
+    torch.cuda.synchronize()
+    assert int(sink.item()) == -7
+    assert int(buf.sum().item()) == 0
