@@ -40,21 +40,37 @@ using namespace dev;
 typedef __attribute__((address_space(3))) void lds_void;
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 
-constexpr int kBM = 256, kStepK = 128;  // tile rows (columns: 4 blocks of 32), k step
+constexpr int kBM = 256;  // tile rows (columns: 4 blocks of 32)
 constexpr int kWaves = 8, kThreads = 64 * kWaves;
-// One LDS stage (one k step): activation fragments [8 row blocks][4 k-chunks][1 KiB], weight fragments
-// [4 column blocks][4 k-chunks][1 KiB], the 256 rows' activation scales, a_s * Q (additive zeros), and the weight
-// records [4 column blocks][32 columns][16 B]. After the 3 stages, 1 KiB that dummy copies write into.
-constexpr int kAOff = 0, kBOff = 32768, kSOff = 49152, kZOff = 50176, kWOff = 51200;
-constexpr int kStageBytes = 53248;
-constexpr int kStages = 3;
-constexpr int kDummyOff = kStages * kStageBytes;
-constexpr int kLds = kDummyOff + 1024;               // 157 KiB
-[[maybe_unused]] constexpr int kCopies = 7;                           // direct copies per wave and step (4 A + 2 B + 1 metadata/dummy)
 constexpr float kBias = 12582912.F;                  // 1.5 * 2^23
 constexpr int kBiasBits = 0x4B400000;
-static_assert(kLds <= 160 * 1024, "LDS budget");
+
+// Step geometry of the GEMM for weight group size G. One k step is 128 columns (one group) for G = 128 and 64 columns
+// (one group of 64 or two of 32) otherwise. One LDS stage (one k step): activation fragments [8 row blocks][CH k-chunks]
+// [1 KiB], weight fragments [4 column blocks][CH][1 KiB], the 256 rows' activation scales [GPS groups][256], a_s * Q
+// (additive zeros) likewise, and the weight records [GPS][4 column blocks][32 columns][16 B]. After the stages, 1 KiB
+// that dummy copies write into. Direct copies per wave and step: CH activation fragments, CH / 2 weight fragments,
+// one metadata block (or a dummy).
+template <int G>
+struct Geo8 {
+    static constexpr int kStepK = G == 128 ? 128 : 64;
+    static constexpr int CH = kStepK / 32;           // 32-column chunks per step
+    static constexpr int GPS = kStepK / G;           // groups per step
+    static constexpr int kAOff = 0;
+    static constexpr int kBOff = kAOff + 8 * CH * 1024;
+    static constexpr int kSOff = kBOff + 4 * CH * 1024;
+    static constexpr int kZOff = kSOff + GPS * 1024;
+    static constexpr int kWOff = kZOff + GPS * 1024;
+    static constexpr int kStageBytes = kWOff + GPS * 2048;
+    static constexpr int kStages = G == 128 ? 3 : 4;
+    static constexpr int kDummyOff = kStages * kStageBytes;
+    static constexpr int kLds = kDummyOff + 1024;  // G = 128: 157 KiB; 64: 113 KiB; 32: 129 KiB
+    static constexpr int kCopies = CH + CH / 2 + 1;
+    static_assert(kLds <= 160 * 1024, "LDS budget");
+    static_assert(4 * GPS <= kWaves, "one metadata copy per wave");
+};
 
 #if defined(__HIP_DEVICE_COMPILE__)
 #define KQ_ASM(...) asm volatile(__VA_ARGS__)
@@ -109,28 +125,29 @@ struct QRow8Args {
     int M, M_p, K;
     float input_scale;
     std::int8_t* q;         // [M_p/32][K/32][64][16]
-    float* scale_t;         // [K/128][M_p] (dynamic)
-    float* az_t;            // [K/128][M_p] a_s * Q (additive float zeros), or null
+    float* scale_t;         // [K/G][M_p] (dynamic)
+    float* az_t;            // [K/G][M_p] a_s * Q (additive float zeros), or null
     const float* ninv;      // NORM: per-row inverse RMS [M]
     const float* nw;        // NORM: norm weight [K]
     // parity dumps (natural order), or null
     std::int8_t* d_codes;   // [M][K]
-    float* d_scales;        // [M][K/128]
-    std::int32_t* d_sums;   // [M][K/128]
+    float* d_scales;        // [M][K/G]
+    std::int32_t* d_sums;   // [M][K/G]
 };
 
-// One lane per 32 columns [32 j, 32 j + 32) of row m; four lanes (a quad) per group of 128 columns.
-// One wave per (32-row block, 128-column group): lane l = row l % 32, fragment half h = l / 32. For each of the group's
-// four 32-column fragments f the lane reads its two 8-column pieces (columns 32 f + 8 h + 0..7 and 32 f + 16 + 8 h +
-// 0..7), so its 16 code bytes are exactly its 16-byte slot of the fragment and each fragment is written as one
-// coalesced 1 KiB store. The row's max |x| over the group combines the two halves through lane l ^ 32.
-template <int QM, bool F32, bool NORM>
+// One wave per (32-row block, 128-column chunk): lane l = row l % 32, fragment half h = l / 32. For each of the
+// chunk's four 32-column fragments f the lane reads its two 8-column pieces (columns 32 f + 8 h + 0..7 and
+// 32 f + 16 + 8 h + 0..7), so its 16 code bytes are exactly its 16-byte slot of the fragment and each fragment is
+// written as one coalesced 1 KiB store. Activation blocks are the weight's groups (G = 32, 64 or 128 columns: one, two
+// or four fragments); a row's max |x| over a block combines the two halves through lane l ^ 32.
+template <int QM, bool F32, bool NORM, int G>
 __global__ __launch_bounds__(256) void quantize_rows8_kernel(QRow8Args a) {
-    const int groups = a.K / 128, KC = a.K / 32;
+    constexpr int NBLK = 128 / G, FPB = G / 32;  // blocks per chunk, fragments per block
+    const int chunks = a.K / 128, KC = a.K / 32, groups = a.K / G;
     const int item = static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x >> 6);
-    if (item >= (a.M_p / 32) * groups) return;  // whole waves
+    if (item >= (a.M_p / 32) * chunks) return;  // whole waves
     const int lane = static_cast<int>(threadIdx.x) & 63;
-    const int mb = item / groups, g = item - mb * groups;
+    const int mb = item / chunks, g = item - mb * chunks;
     const int r = lane & 31, h = lane >> 5;
     const int m = 32 * mb + r;
     const bool live = m < a.M;
@@ -171,17 +188,22 @@ __global__ __launch_bounds__(256) void quantize_rows8_kernel(QRow8Args a) {
 #pragma unroll
         for (int i = 0; i < 64; ++i) v[i] = 0.F;
     }
-    float mx = 0.F, mn = 0.F;
-    if constexpr (QM != QUANT_STATIC) {
+    QuantBlock qbs[NBLK];
 #pragma unroll
-        for (int i = 0; i < 64; ++i) quant_stat(QM, v[i], mx, mn);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+    for (int bb = 0; bb < NBLK; ++bb) {
+        float mx = 0.F, mn = 0.F;
+        if constexpr (QM != QUANT_STATIC) {
+#pragma unroll
+            for (int i = 16 * FPB * bb; i < 16 * FPB * (bb + 1); ++i) quant_stat(QM, v[i], mx, mn);
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+        }
+        qbs[bb] = quant_block(QM, mx, mn, a.input_scale, live);
     }
-    const QuantBlock qb = quant_block(QM, mx, mn, a.input_scale, live);
     // codes: w[4 f + i] holds the lane's bytes 4 i .. 4 i + 3 of fragment f (its 16-byte slot)
     std::uint32_t w[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
+        const QuantBlock& qb = qbs[i / (4 * FPB)];
         if constexpr (QM == QUANT_STATIC) {
             std::uint32_t d = 0;
 #pragma unroll
@@ -204,21 +226,25 @@ __global__ __launch_bounds__(256) void quantize_rows8_kernel(QRow8Args a) {
 #pragma unroll
     for (int f = 0; f < 4; ++f)
         *reinterpret_cast<uint4*>(frag + f * 1024) = make_uint4(w[4 * f], w[4 * f + 1], w[4 * f + 2], w[4 * f + 3]);
-    // code sums of the group (additive float zeros and the parity dump)
-    int qsum = 0;
-    if (a.az_t || a.d_sums) {
+    // per block: code sums (additive float zeros and the parity dump), scales
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+    for (int bb = 0; bb < NBLK; ++bb) {
+        int qsum = 0;
+        if (a.az_t || a.d_sums) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) qsum += static_cast<std::int8_t>((w[i] >> (8 * e)) & 0xFFu);
-        qsum += __shfl_xor(qsum, 32);
-    }
-    if (h == 0) {
-        const std::int64_t o = static_cast<std::int64_t>(g) * a.M_p + m;
-        if (a.scale_t) a.scale_t[o] = qb.s;
-        if (a.az_t) a.az_t[o] = qb.s * static_cast<float>(qsum);
-        if (live && a.d_scales) a.d_scales[static_cast<std::int64_t>(m) * groups + g] = QM == QUANT_STATIC ? a.input_scale : qb.s;
-        if (live && a.d_sums) a.d_sums[static_cast<std::int64_t>(m) * groups + g] = qsum;
+            for (int i = 4 * FPB * bb; i < 4 * FPB * (bb + 1); ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qsum += static_cast<std::int8_t>((w[i] >> (8 * e)) & 0xFFu);
+            qsum += __shfl_xor(qsum, 32);
+        }
+        if (h == 0) {
+            const int gb = NBLK * g + bb;  // the block's group index
+            const std::int64_t o = static_cast<std::int64_t>(gb) * a.M_p + m;
+            if (a.scale_t) a.scale_t[o] = qbs[bb].s;
+            if (a.az_t) a.az_t[o] = qbs[bb].s * static_cast<float>(qsum);
+            if (live && a.d_scales) a.d_scales[static_cast<std::int64_t>(m) * groups + gb] = QM == QUANT_STATIC ? a.input_scale : qbs[bb].s;
+            if (live && a.d_sums) a.d_sums[static_cast<std::int64_t>(m) * groups + gb] = qsum;
+        }
     }
     if (live && a.d_codes) {
         // natural column order: piece p of fragment f holds columns 32 f + 16 p + 8 h + 0..7
@@ -264,10 +290,12 @@ __device__ __forceinline__ int col_block(const Gemm8Args& a, int nb, int cb) {
 // The DPP broadcast register of a row block holds, at lane 16 r + k, the value of that row for lanes of row r.
 __device__ __forceinline__ int bcast_row(int lane) { return 8 * ((lane & 15) >> 2) + 4 * (lane >> 5) + (lane & 3); }
 
+template <int GPS>
 struct Meta {  // one k step's epilogue operands of a wave: weight records of its two column blocks, scales of its rows
-    v4i rec[2];      // {s, -1.5 * 2^23 * s, z, 0} of the lane's column in column blocks 0, 1
-    float as[2];     // a_s of DPP row bcast_row(lane) in row blocks 0, 1
-    float az[2];     // a_s * Q likewise (additive zeros)
+    v2i rec[2][GPS];   // {s, -1.5 * 2^23 * s} of the lane's column in column blocks 0, 1, per group of the step
+    float z[2][GPS];   // its additive zero z (additive zeros)
+    float as[2][GPS];  // a_s of DPP row bcast_row(lane) in row blocks 0, 1
+    float az[2][GPS];  // a_s * Q likewise (additive zeros)
 };
 
 // Epilogue of elements [K0, K1) of one block; P holds the biased int32 partials (as f32: 12582912 + P'). Each slice
@@ -279,7 +307,7 @@ struct Meta {  // one k step's epilogue operands of a wave: weight records of it
 //   F32 scales, calibrated: P = P - 12582912;          acc += P * s
 //   additive zeros:         acc += (a_s * Q)[row] * z
 template <int K, bool SF16, bool STAT>
-__device__ __forceinline__ void epi_convert(int& P, const v4i& rec) {
+__device__ __forceinline__ void epi_convert(int& P, const v2i& rec) {
     if constexpr (SF16) {
         KQ_ASM("v_fma_f32 %0, %0, %1, %2" : "+v"(P) : "v"(rec[0]), "v"(rec[1]));
     } else {
@@ -288,7 +316,7 @@ __device__ __forceinline__ void epi_convert(int& P, const v4i& rec) {
     }
 }
 template <int K, bool SF16, bool STAT, bool ZF>
-__device__ __forceinline__ void epi_accumulate(float& acc, int P, const v4i& rec, float as, float az) {
+__device__ __forceinline__ void epi_accumulate(float& acc, int P, const v2i& rec, float z, float as, float az) {
     if constexpr (STAT) {
         if constexpr (SF16) KQ_ASM("v_add_f32 %0, %0, %1" : "+v"(acc) : "v"(P));
         else KQ_ASM("v_fmac_f32 %0, %1, %2" : "+v"(acc) : "v"(P), "v"(rec[0]));
@@ -296,10 +324,10 @@ __device__ __forceinline__ void epi_accumulate(float& acc, int P, const v4i& rec
         KQ_ASM("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(as), "v"(P), "n"(K));
     }
     if constexpr (ZF)
-        KQ_ASM("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(az), "v"(rec[2]), "n"(K));
+        KQ_ASM("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(az), "v"(z), "n"(K));
 }
 template <int K0, int K1, bool SF16, bool STAT>
-__device__ __forceinline__ void epi_converts(v16i& P, const v4i& rec) {
+__device__ __forceinline__ void epi_converts(v16i& P, const v2i& rec) {
     if constexpr (K0 < K1) {
         int p = P[K0];
         epi_convert<K0, SF16, STAT>(p, rec);
@@ -308,10 +336,10 @@ __device__ __forceinline__ void epi_converts(v16i& P, const v4i& rec) {
     }
 }
 template <int K0, int K1, bool SF16, bool STAT, bool ZF>
-__device__ __forceinline__ void epi_accumulates(float (&acc)[16], const v16i& P, const v4i& rec, float as, float az) {
+__device__ __forceinline__ void epi_accumulates(float (&acc)[16], const v16i& P, const v2i& rec, float z, float as, float az) {
     if constexpr (K0 < K1) {
-        epi_accumulate<K0, SF16, STAT, ZF>(acc[K0], P[K0], rec, as, az);
-        epi_accumulates<K0 + 1, K1, SF16, STAT, ZF>(acc, P, rec, as, az);
+        epi_accumulate<K0, SF16, STAT, ZF>(acc[K0], P[K0], rec, z, as, az);
+        epi_accumulates<K0 + 1, K1, SF16, STAT, ZF>(acc, P, rec, z, as, az);
     }
 }
 // DBG first stores P' = P - 0x4B400000 to the dump through a buffer resource: element k of the block is at byte
@@ -333,11 +361,11 @@ struct Dump {
     std::uint32_t row_bytes;   // N * groups * 4
 };
 template <int K0, int K1, bool SF16, bool STAT, bool ZF, bool DBG>
-__device__ __forceinline__ void epi_range(float (&acc)[16], v16i& P, const v4i& rec, float as, float az, const Dump& d,
+__device__ __forceinline__ void epi_range(float (&acc)[16], v16i& P, const v2i& rec, float z, float as, float az, const Dump& d,
                                           std::uint32_t voff, int g) {
     if constexpr (DBG) epi_dump<K0, K1, DBG>(P, rsrc(d.base, d.bytes), voff, d.row_bytes, static_cast<std::uint32_t>(g) * 4);
     epi_converts<K0, K1, SF16, STAT>(P, rec);
-    epi_accumulates<K0, K1, SF16, STAT, ZF>(acc, P, rec, as, az);
+    epi_accumulates<K0, K1, SF16, STAT, ZF>(acc, P, rec, z, as, az);
 }
 
 __device__ __forceinline__ void mfma_first(v16i& P, const v4i& A, const v4i& B, const v16i& bias) {
@@ -362,11 +390,13 @@ __device__ __forceinline__ void quad_transpose(float (&v)[4], int lane) {
 }
 
 // Final values of a wave's 2 x 2 blocks (calibrated inputs scale by input_scale, calibrated outputs round to
-// output_scale steps, GELU pairs column block 0 (gate) with 1 (up)), stored with 16-byte stores: each 4 x 4 sub-block (rows 8 j + 4 h + 0..3, four columns of a lane quad) is transposed
-// in the quad, so lane q writes row 8 j + 4 h + q, columns 4 (col / 4) .. + 3. Every lane issues exactly
-// kTileStores (kTileStoresGelu) stores; rows past M and columns past N fall outside the buffer resource, whose range
-// check drops them, so the number of outstanding vector memory operations after a tile is known at compile time.
-constexpr int kTileStores = 16, kTileStoresGelu = 8;
+// output_scale steps, GELU pairs column block 0 (gate) with 1 (up)), stored with 16-byte stores: each 4 x 4 sub-block
+// (rows 8 j + 4 h + 0..3, four columns of a lane quad) is transposed in the quad, so lane q writes row 8 j + 4 h + q,
+// columns 4 (col / 4) .. + 3. Every lane issues exactly 16 (GELU: kTileStoresGelu) stores; rows past M and columns
+// past N fall outside the buffer resource, whose range check drops them, so the number of outstanding vector memory
+// operations after a tile is known at compile time. (Plain projections use store8d below.)
+constexpr int kTileStoresGelu = 8;
+constexpr int min63(int n) { return n < 63 ? n : 63; }
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 template <bool STAT, bool GELU>
 __device__ __forceinline__ void store8t(const Gemm8Args& a, const float (&acc)[2][2][16], int m0, int wm, const int (&gc)[2],
@@ -410,6 +440,40 @@ __device__ __forceinline__ void store8t(const Gemm8Args& a, const float (&acc)[2
     }
 }
 
+// Final values of a wave's 2 x 2 blocks for plain projections, stored straight from the accumulators with 4-byte
+// stores (no transpose: every VALU instruction counts in this VALU-bound kernel). Element k of block (i, c) is row
+// 64 wm + 32 i + 8 (k / 4) + 4 (lane / 32) + k % 4, column 32 gc[c] + lane % 32: one store instruction writes two
+// 128-byte row segments. Every lane issues exactly kTileStoresD stores; rows past M and columns past N get a
+// per-lane offset beyond the buffer resource, whose range check drops them.
+constexpr int kTileStoresD = 64;
+template <bool STAT>
+__device__ __forceinline__ void store8d(const Gemm8Args& a, const float (&acc)[2][2][16], int m0, int wm, const int (&gc)[2],
+                                        int lane) {
+    const int n_out = a.N;
+    const int rows = min(a.M - m0, kBM);
+    const __amdgpu_buffer_rsrc_t yres = rsrc(a.y + static_cast<std::int64_t>(m0) * n_out, static_cast<std::uint32_t>(rows) * n_out * 4);
+    const std::uint32_t row_bytes = static_cast<std::uint32_t>(n_out) * 4;
+    const bool cal = a.output_scale > 0.F;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int n = 32 * gc[c] + (lane & 31);
+        // dead columns: an offset past the buffer that stays past it for every row added below (rows * row_bytes < 2^31)
+        const std::uint32_t col_off = n < n_out ? static_cast<std::uint32_t>(n) * 4 : 0x80000000u;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const std::uint32_t base = col_off + static_cast<std::uint32_t>(64 * wm + 32 * i + 4 * (lane >> 5)) * row_bytes;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                float x = acc[i][c][k];
+                if (STAT) x = x * a.input_scale;
+                if (cal) x = calibrate_output(x, a.output_scale);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), yres,
+                                                      base + static_cast<std::uint32_t>(8 * (k >> 2) + (k & 3)) * row_bytes, 0, 0);
+            }
+        }
+    }
+}
+
 // One work item of gemm8_kernel: K range, tile, the tile's first row and its column block. (Declared at namespace
 // scope: local classes in a kernel template keep the host pass from emitting the kernel's launch stub.)
 struct Item {
@@ -424,8 +488,10 @@ struct Copy {
     int kbase;
 };
 
-template <bool SF16, bool STAT, bool ZF, bool GELU, bool SPLIT, bool DBG>
+template <int G, bool SF16, bool STAT, bool ZF, bool GELU, bool SPLIT, bool DBG>
 __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
+    using Q = Geo8<G>;
+    constexpr int CH = Q::CH, GPS = Q::GPS, NS = Q::kStages;
     extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -435,18 +501,18 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     // Work items (K range, row block, column block) in an order that gives each XCD a contiguous range of tiles, row
     // blocks fastest (the XCD's few column blocks of weights stay in its L2): item i of the launch is tile
     // (i % 8) (total / 8) + i / 8 when total % 8 == 0. The launch holds at most one workgroup per CU; workgroup b runs
-    // items b, b + G, b + 2 G, ... back to back, with the copy ring running on across item boundaries, so the copies of
-    // an item's first steps are in flight during the previous item's last steps and its output stores overlap the next
-    // item's MFMAs.
+    // items b, b + W, b + 2 W, ... (W workgroups) back to back, with the copy ring running on across item boundaries,
+    // so the copies of an item's first steps are in flight during the previous item's last steps and its output
+    // stores overlap the next item's MFMAs.
     const int tiles = a.m_blocks * a.n_blocks;
     const int total = tiles * a.ksplit;
-    const int G = static_cast<int>(gridDim.x);
+    const int W = static_cast<int>(gridDim.x);
     const int bx = static_cast<int>(blockIdx.x);
-    const int items = (total - bx + G - 1) / G;
+    const int items = (total - bx + W - 1) / W;
     const int KC = a.K / 32;
-    const int steps = a.K / kStepK / a.ksplit;
+    const int steps = a.K / Q::kStepK / a.ksplit;
     auto item_of = [&](int r) __attribute__((always_inline)) {
-        int i = r * G + bx;
+        int i = r * W + bx;
         if (total % 8 == 0) i = (i % 8) * (total / 8) + i / 8;
         Item it;
         it.ks = i / tiles;
@@ -456,24 +522,29 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         return it;
     };
 
-    // ---- copies of one step: wave w brings activation row block w (4 fragments), half of weight column block w / 2
-    // (2 fragments) and one metadata block: w = 0, 1 the weight records of column blocks 0-1 / 2-3, w = 2 the tile's
-    // activation scales, w = 3 its a_s * Q (additive zeros); the other copies write zeros into the dummy area.
-    // issue(u, r, t): the copies of step t of item r (t may run past the item: the next items' steps) into stage u % 3;
-    // past the last item, the last step again, into a stage nothing reads any more.
-    const int cbc = wave >> 1, ckc = 2 * (wave & 1);
+    // ---- copies of one step: wave w brings activation row block w (CH fragments), half of weight column block w / 2
+    // (CH / 2 fragments) and one metadata block: waves 0 .. 2 GPS - 1 the weight records of group w / 2 of the step,
+    // column blocks 0-1 (w even) or 2-3; the next GPS waves the tile's activation scales of one group each; the next
+    // GPS its a_s * Q (additive zeros); the other copies write into the dummy area.
+    const int cbc = wave >> 1, ckc = (CH / 2) * (wave & 1);
     // The wave's metadata copy: its resource, per-step stride and LDS place do not depend on the item (dummy: mdst < 0).
+    // meta_gg: the offset of the wave's group within a step's metadata (0 when a step holds one group)
     __amdgpu_buffer_rsrc_t mres = rsrc(a.wmeta, 0u);
-    std::uint32_t meta_step = 0;
+    std::uint32_t meta_step = 0, meta_gg = 0;
     int mdst = -1;
-    if (wave < 2) {
+    if (wave < 2 * GPS) {
+        const int mgg = GPS == 1 ? 0 : wave >> 1;
         mres = rsrc(a.wmeta, static_cast<std::uint32_t>(a.groups) * a.NB * 512);
-        meta_step = static_cast<std::uint32_t>(a.NB) * 512;
-        mdst = kWOff + wave * 1024;
-    } else if ((wave == 2 && !STAT) || (wave == 3 && ZF)) {
-        mres = rsrc(wave == 2 ? a.scale_t : a.az_t, static_cast<std::uint32_t>(a.groups) * a.M_p * 4);
-        meta_step = static_cast<std::uint32_t>(a.M_p) * 4;
-        mdst = wave == 2 ? kSOff : kZOff;
+        meta_step = static_cast<std::uint32_t>(GPS * a.NB) * 512;
+        meta_gg = static_cast<std::uint32_t>(mgg * a.NB) * 512;
+        mdst = Q::kWOff + mgg * 2048 + (wave & 1) * 1024;
+    } else if ((wave < 3 * GPS && !STAT) || (wave >= 3 * GPS && wave < 4 * GPS && ZF)) {
+        const bool sc = wave < 3 * GPS;
+        const int mgg = GPS == 1 ? 0 : wave - (sc ? 2 : 3) * GPS;
+        mres = rsrc(sc ? a.scale_t : a.az_t, static_cast<std::uint32_t>(a.groups) * a.M_p * 4);
+        meta_step = static_cast<std::uint32_t>(GPS * a.M_p) * 4;
+        meta_gg = static_cast<std::uint32_t>(mgg * a.M_p) * 4;
+        mdst = (sc ? Q::kSOff : Q::kZOff) + mgg * 1024;
     }
     auto copy_of = [&](int r) __attribute__((always_inline)) {
         const Item it = item_of(r);
@@ -485,36 +556,37 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         cp.bbase = a.w + static_cast<std::int64_t>(clive ? gcb : 0) * KC * 1024;
         cp.bbytes = clive ? static_cast<std::uint32_t>(KC) * 1024 : 0u;
         cp.meta0 = 0x80000000u;
-        if (wave < 2)
-            cp.meta0 = static_cast<std::uint32_t>(cp.kbase) * meta_step + static_cast<std::uint32_t>(col_block<GELU>(a, it.nbk, 2 * wave)) * 512;
+        if (wave < 2 * GPS)
+            cp.meta0 = static_cast<std::uint32_t>(cp.kbase) * meta_step + meta_gg +
+                       static_cast<std::uint32_t>(col_block<GELU>(a, it.nbk, 2 * (wave & 1))) * 512;
         else if (mdst >= 0)
-            cp.meta0 = static_cast<std::uint32_t>(cp.kbase) * meta_step + static_cast<std::uint32_t>(it.m0) * 4;
+            cp.meta0 = static_cast<std::uint32_t>(cp.kbase) * meta_step + meta_gg + static_cast<std::uint32_t>(it.m0) * 4;
         return cp;
     };
-    // part 0: activation fragments 0-1, part 1: activation fragments 2-3, part 2: weight fragments and metadata
+    // part 0: activation fragments [0, CH / 2), part 1: [CH / 2, CH), part 2: weight fragments and metadata
     auto issue_copy = [&](const Copy& cp, int u, int t, auto part) __attribute__((always_inline)) {
         constexpr int pt = decltype(part)::value;
-        const std::uint32_t kc0 = static_cast<std::uint32_t>((cp.kbase + t) * 4);
-        std::uint8_t* base = lds + (u % kStages) * kStageBytes;
+        const std::uint32_t kc0 = static_cast<std::uint32_t>((cp.kbase + t) * CH);
+        std::uint8_t* base = lds + (u % NS) * Q::kStageBytes;
         if constexpr (pt < 2) {
             const __amdgpu_buffer_rsrc_t ares = rsrc(cp.abase, static_cast<std::uint32_t>(kBM / 32) * KC * 1024);
 #pragma unroll
-            for (int i = 2 * pt; i < 2 * pt + 2; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(base + kAOff + (wave * 4 + i) * 1024), 16, lane * 16,
+            for (int i = pt * (CH / 2); i < (pt + 1) * (CH / 2); ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(base + Q::kAOff + (wave * CH + i) * 1024), 16, lane * 16,
                                                          (static_cast<std::uint32_t>(wave) * KC + kc0 + i) * 1024, 0, 0);
         } else {
             const __amdgpu_buffer_rsrc_t bres = rsrc(cp.bbase, cp.bbytes);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(base + kBOff + (cbc * 4 + ckc + i) * 1024), 16,
+            for (int i = 0; i < CH / 2; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(bres, (lds_void*)(base + Q::kBOff + (cbc * CH + ckc + i) * 1024), 16,
                                                          lane * 16, (kc0 + ckc + i) * 1024, 0, 0);
-            std::uint8_t* md = mdst < 0 ? lds + kDummyOff : base + mdst;
+            std::uint8_t* md = mdst < 0 ? lds + Q::kDummyOff : base + mdst;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_void*)md, 16, lane * 16, cp.meta0 + static_cast<std::uint32_t>(t) * meta_step, 0, 0);
         }
     };
-    // issue(u, r, t): the copies of step t of item r into stage u % 3; t may run past the item (the next items' steps),
-    // and past the last item the last step is copied again, into a stage nothing reads any more. item_copy holds the copy
-    // parameters of the item being computed.
+    // issue(u, r, t): the copies of step t of item r into stage u % NS; t may run past the item (the next items' steps),
+    // and past the last item the item's last step is copied again, into a stage nothing reads any more. item_copy holds
+    // the copy parameters of the item being computed.
     Copy item_copy = copy_of(0);
     auto issue_part = [&](int u, int r, int t, auto part) __attribute__((always_inline)) {
         if (t < steps) {
@@ -525,11 +597,8 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             t -= steps;
             ++r;
         }
-        if (r >= items) {
-            r = items - 1;
-            t = steps - 1;
-        }
-        issue_copy(copy_of(r), u, t, part);
+        if (r >= items) issue_copy(item_copy, u, steps - 1, part);
+        else issue_copy(copy_of(r), u, t, part);
     };
     auto issue = [&](int u, int r, int t) __attribute__((always_inline)) {
         issue_part(u, r, t, std::integral_constant<int, 0>{});
@@ -539,31 +608,40 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
 
     // ---- the wave's fragments: row blocks 2 wm + i; column blocks (plain) 2 wn + i, (GELU) wn + 2 i
     const int cb_l0 = GELU ? wn : 2 * wn, cb_l1 = GELU ? wn + 2 : 2 * wn + 1;
-    const std::uint32_t a_lane = lds0 + kAOff + (2 * wm * 4) * 1024 + lane * 16;
-    const std::uint32_t b_lane0 = lds0 + kBOff + (cb_l0 * 4) * 1024 + lane * 16;
-    const std::uint32_t b_lane1 = lds0 + kBOff + (cb_l1 * 4) * 1024 + lane * 16;
+    const std::uint32_t a_lane = lds0 + Q::kAOff + (2 * wm * CH) * 1024 + lane * 16;
+    const std::uint32_t b_lane0 = lds0 + Q::kBOff + (cb_l0 * CH) * 1024 + lane * 16;
+    const std::uint32_t b_lane1 = lds0 + Q::kBOff + (cb_l1 * CH) * 1024 + lane * 16;
     const int col = lane & 31;
-    [[maybe_unused]] const std::uint32_t w_lane0 = lds0 + kWOff + (cb_l0 * 32 + col) * 16;
-    [[maybe_unused]] const std::uint32_t w_lane1 = lds0 + kWOff + (cb_l1 * 32 + col) * 16;
-    [[maybe_unused]] const std::uint32_t s_lane = lds0 + kSOff + (64 * wm + bcast_row(lane)) * 4;
-    [[maybe_unused]] const std::uint32_t z_lane = lds0 + kZOff + (64 * wm + bcast_row(lane)) * 4;
-    auto read_meta = [&](Meta& mt, std::uint32_t stage) __attribute__((always_inline)) {
-        KQ_ASM("ds_read_b128 %0, %1" : "=v"(mt.rec[0]) : "v"(w_lane0 + stage));
-        KQ_ASM("ds_read_b128 %0, %1" : "=v"(mt.rec[1]) : "v"(w_lane1 + stage));
-        if constexpr (!STAT) {
-            KQ_ASM("ds_read_b32 %0, %1" : "=v"(mt.as[0]) : "v"(s_lane + stage));
-            KQ_ASM("ds_read_b32 %0, %1 offset:128" : "=v"(mt.as[1]) : "v"(s_lane + stage));
-        }
-        if constexpr (ZF) {
-            KQ_ASM("ds_read_b32 %0, %1" : "=v"(mt.az[0]) : "v"(z_lane + stage));
-            KQ_ASM("ds_read_b32 %0, %1 offset:128" : "=v"(mt.az[1]) : "v"(z_lane + stage));
+    [[maybe_unused]] const std::uint32_t w_lane0 = lds0 + Q::kWOff + (cb_l0 * 32 + col) * 16;
+    [[maybe_unused]] const std::uint32_t w_lane1 = lds0 + Q::kWOff + (cb_l1 * 32 + col) * 16;
+    [[maybe_unused]] const std::uint32_t s_lane = lds0 + Q::kSOff + (64 * wm + bcast_row(lane)) * 4;
+    [[maybe_unused]] const std::uint32_t z_lane = lds0 + Q::kZOff + (64 * wm + bcast_row(lane)) * 4;
+    auto read_meta = [&](Meta<GPS>& mt, std::uint32_t stage) __attribute__((always_inline)) {
+#pragma unroll
+        for (int gg = 0; gg < GPS; ++gg) {
+            KQ_ASM("ds_read_b64 %0, %1 offset:%2" : "=v"(mt.rec[0][gg]) : "v"(w_lane0 + stage), "n"(gg * 2048));
+            KQ_ASM("ds_read_b64 %0, %1 offset:%2" : "=v"(mt.rec[1][gg]) : "v"(w_lane1 + stage), "n"(gg * 2048));
+            if constexpr (ZF) {
+                KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.z[0][gg]) : "v"(w_lane0 + stage), "n"(gg * 2048 + 8));
+                KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.z[1][gg]) : "v"(w_lane1 + stage), "n"(gg * 2048 + 8));
+            }
+            if constexpr (!STAT) {
+                KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.as[0][gg]) : "v"(s_lane + stage), "n"(gg * 1024));
+                KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.as[1][gg]) : "v"(s_lane + stage), "n"(gg * 1024 + 128));
+            }
+            if constexpr (ZF) {
+                KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.az[0][gg]) : "v"(z_lane + stage), "n"(gg * 1024));
+                KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.az[1][gg]) : "v"(z_lane + stage), "n"(gg * 1024 + 128));
+            }
         }
     };
-    auto read4 = [&](v4i (&f)[4], std::uint32_t addr) __attribute__((always_inline)) {
+    auto read_frags = [&](v4i (&f)[CH], std::uint32_t addr) __attribute__((always_inline)) {
         ds_read16<0>(f[0], addr);
         ds_read16<1024>(f[1], addr);
-        ds_read16<2048>(f[2], addr);
-        ds_read16<3072>(f[3], addr);
+        if constexpr (CH == 4) {
+            ds_read16<2048>(f[2], addr);
+            ds_read16<3072>(f[3], addr);
+        }
     };
 
     // ---- per item: the wave's global column blocks, the tile's first row, and the parity dump's resource and offsets
@@ -600,7 +678,8 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         }
     };
     // vector memory operations a lane issues when it stores a tile (outstanding after the tile)
-    constexpr int kStoresAfter = SPLIT ? 16 : (GELU ? kTileStoresGelu : kTileStores);
+    // (the parity-dump instances keep the 16-byte stores: the 4-byte form would need more registers than they have)
+    [[maybe_unused]] constexpr int kStoresAfter = SPLIT ? 16 : (GELU ? kTileStoresGelu : (DBG ? 16 : kTileStoresD));
 
     float acc[2][2][16];
 #pragma unroll
@@ -613,113 +692,175 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
 #pragma unroll
     for (int k = 0; k < 16; ++k) bias[k] = kBiasBits;
     KQ_ASM("" : "+v"(bias));  // opaque: never rematerialized next to an MFMA
-    // P[1] starts as the bias and the metadata of "step -1" as zeros: the epilogue step 0 runs for the block before its
+    // P[1] starts as the bias and the metadata of "step -1" as zeros: the epilogue step 0 runs for the unit before its
     // first one adds exactly 0 (likewise at every item start)
     v16i P[2];
     P[0] = bias;
     P[1] = bias;
-    v4i A[2][4], B0[4], B1[2][4];
-    Meta mt[2];
+    v4i A[2][CH], B0[CH], B1[2][CH];
+    Meta<GPS> mt[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        mt[1].rec[i] = v4i{0, 0, 0, 0};
-        mt[1].as[i] = 0.F;
-        mt[1].az[i] = 0.F;
-        mt[0].as[i] = 0.F;
-        mt[0].az[i] = 0.F;
-    }
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int gg = 0; gg < GPS; ++gg) {
+            mt[1].rec[i][gg] = v2i{0, 0};
+            mt[1].z[i][gg] = 0.F;
+            mt[0].z[i][gg] = 0.F;
+            mt[1].as[i][gg] = 0.F;
+            mt[1].az[i][gg] = 0.F;
+            mt[0].as[i][gg] = 0.F;
+            mt[0].az[i][gg] = 0.F;
+        }
 
-    // prologue: three stages in flight; step 0's operands (but A row block 1) and metadata in registers
-    issue(0, 0, 0);
-    issue(1, 0, 1);
-    issue(2, 0, 2);
+    // prologue: NS stages in flight; step 0's operands (but A row block 1) and metadata in registers
+#pragma unroll
+    for (int i = 0; i < NS; ++i) issue(i, 0, i);
     KQ_ASM("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    read4(A[0], a_lane);
-    read4(B0, b_lane0);
-    read4(B1[0], b_lane1);
+    read_frags(A[0], a_lane);
+    read_frags(B0, b_lane0);
+    read_frags(B1[0], b_lane1);
     read_meta(mt[0], 0);
 
-    // Step t (parity p) in four blocks (row block, column block) of four MFMAs each; the epilogue of a block runs in
-    // the VALU slots after MFMAs 2-4 of the next block. Reads (ds_read_b128) go into the gap after a block's MFMA 1:
-    //   b0 (0, 0) -> P0: gap: A row block 1 of step t;         epilogue of b3 of step t - 1
-    //   b1 (0, 1) -> P1:                                        epilogue of b0
-    //   [lgkmcnt(0), vmcnt(7), barrier: stage t + 1 complete, stage t free; copies of step t + 3 into stage t]
-    //   b2 (1, 0) -> P0: gap: B column block 1 and metadata of step t + 1;  epilogue of b1
-    //   b3 (1, 1) -> P1: gap: A row block 0 and B column block 0 of step t + 1;  epilogue of b2
-    // Stage t % 3 is read from b2 of step t - 1 to b0 of step t; the mid-step barrier of step t comes after every
-    // wave waited for those reads, and after every wave's copies of step t + 1 (issued at mid-step t - 2) landed.
+    // Step t (parity p) in four blocks (row block, column block) = b0 (0, 0), b1 (0, 1), b2 (1, 0), b3 (1, 1). An
+    // epilogue unit is one block and group: per G = 128 block CH = 4 MFMAs, per G = 64 block 2, per G = 32 block two
+    // units of one MFMA each. The epilogue of a unit runs in the VALU slots after the next unit's MFMAs (G = 128: after
+    // MFMAs 2-4 of the next block). Reads (ds_read_b128) go into the gap after a block's first MFMA:
+    //   b0: A row block 1 of step t;   b2: B column block 1 and metadata of step t + 1;
+    //   b3: A row block 0 and B column block 0 of step t + 1
+    //   between b1 and b2: lgkmcnt(0), vmcnt, barrier: stage t + 1 complete, stage t free; copies of step t + NS into
+    //   stage t.
+    // Stage t % NS is read from b2 of step t - 1 to b0 of step t; the mid-step barrier of step t comes after every
+    // wave waited for those reads, and after every wave's copies of step t + 1 (issued at mid-step t + 1 - NS) landed.
     auto step_body = [&](int t, int u, int r, auto parity, bool wide) __attribute__((always_inline)) {
         constexpr int p = decltype(parity)::value;
-        Meta& cur = mt[p];
-        Meta& prv = mt[p ^ 1];
-        v4i (&Bc)[4] = B1[p];
-        v4i (&Bn)[4] = B1[p ^ 1];
-        const std::uint32_t st_now = static_cast<std::uint32_t>((u % kStages) * kStageBytes);
-        const std::uint32_t st_next = static_cast<std::uint32_t>(((u + 1) % kStages) * kStageBytes);
-        const int g = ks * steps + t;
-        // ---- b0
-        lgkm_wait<0>(A[0], B0, Bc, cur.rec, cur.as, cur.az);  // step t's operands and metadata (read during step t - 1)
-        mfma_first(P[0], A[0][0], B0[0], bias);
-        ds_read16<4096>(A[1][0], a_lane + st_now);
-        ds_read16<5120>(A[1][1], a_lane + st_now);
-        ds_read16<6144>(A[1][2], a_lane + st_now);
-        ds_read16<7168>(A[1][3], a_lane + st_now);
-        mfma_acc(P[0], A[0][1], B0[1]);
-        epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1], prv.as[1], prv.az[1], dmp, t > 0 ? dvo[1][1] : 0x80000000u, g - 1);
-        mfma_acc(P[0], A[0][2], B0[2]);
-        epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1], prv.as[1], prv.az[1], dmp, t > 0 ? dvo[1][1] : 0x80000000u, g - 1);
-        mfma_acc(P[0], A[0][3], B0[3]);
-        epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1], prv.as[1], prv.az[1], dmp, t > 0 ? dvo[1][1] : 0x80000000u, g - 1);
-        // ---- b1
-        mfma_first(P[1], A[0][0], Bc[0], bias);
-        mfma_acc(P[1], A[0][1], Bc[1]);
-        epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0], cur.as[0], cur.az[0], dmp, dvo[0][0], g);
-        mfma_acc(P[1], A[0][2], Bc[2]);
-        epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0], cur.as[0], cur.az[0], dmp, dvo[0][0], g);
-        mfma_acc(P[1], A[0][3], Bc[3]);
-        epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0], cur.as[0], cur.az[0], dmp, dvo[0][0], g);
-        // ---- mid-step
-        lgkm_wait<0>(A[1]);
-        // the first two steps after a tile's stores: those stores are younger than step t + 1's copies
-        if (wide) KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(kCopies + kStoresAfter) : "memory");
-        else KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(kCopies) : "memory");
-        issue(u + 3, r, t + 3);
-        // ---- b2
-        mfma_first(P[0], A[1][0], B0[0], bias);
-        read4(Bn, b_lane1 + st_next);
-        read_meta(prv, st_next);
-        mfma_acc(P[0], A[1][1], B0[1]);
-        epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1], cur.as[0], cur.az[0], dmp, dvo[0][1], g);
-        mfma_acc(P[0], A[1][2], B0[2]);
-        epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1], cur.as[0], cur.az[0], dmp, dvo[0][1], g);
-        mfma_acc(P[0], A[1][3], B0[3]);
-        epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1], cur.as[0], cur.az[0], dmp, dvo[0][1], g);
-        // ---- b3
-        mfma_first(P[1], A[1][0], Bc[0], bias);
-        read4(A[0], a_lane + st_next);
-        read4(B0, b_lane0 + st_next);
-        mfma_acc(P[1], A[1][1], Bc[1]);
-        epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0], cur.as[1], cur.az[1], dmp, dvo[1][0], g);
-        mfma_acc(P[1], A[1][2], Bc[2]);
-        epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0], cur.as[1], cur.az[1], dmp, dvo[1][0], g);
-        mfma_acc(P[1], A[1][3], Bc[3]);
-        epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0], cur.as[1], cur.az[1], dmp, dvo[1][0], g);
+        Meta<GPS>& cur = mt[p];
+        Meta<GPS>& prv = mt[p ^ 1];
+        v4i (&Bc)[CH] = B1[p];
+        v4i (&Bn)[CH] = B1[p ^ 1];
+        const std::uint32_t st_now = static_cast<std::uint32_t>((u % NS) * Q::kStageBytes);
+        const std::uint32_t st_next = static_cast<std::uint32_t>(((u + 1) % NS) * Q::kStageBytes);
+        const int g = (ks * steps + t) * GPS;  // global index of the step's first group
+        const std::uint32_t dvo_prev = t > 0 ? dvo[1][1] : 0x80000000u;
+        auto mid_step = [&]() __attribute__((always_inline)) {
+            lgkm_wait<0>(A[1]);
+            // the first NS - 1 steps after a tile's stores: those stores are younger than step t + 1's copies
+            // (vmcnt counts to 63: a larger allowance waits for some of the stores too, which is only stricter)
+            if (wide) KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(min63((NS - 2) * Q::kCopies + kStoresAfter)) : "memory");
+            else KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * Q::kCopies) : "memory");
+            issue(u + NS, r, t + NS);
+        };
+        lgkm_wait<0>(A[0], B0, Bc, cur.rec, cur.z, cur.as, cur.az);  // step t's operands and metadata (read during step t - 1)
+        if constexpr (G == 128) {
+            // ---- b0
+            mfma_first(P[0], A[0][0], B0[0], bias);
+            ds_read16<4096>(A[1][0], a_lane + st_now);
+            ds_read16<5120>(A[1][1], a_lane + st_now);
+            ds_read16<6144>(A[1][2], a_lane + st_now);
+            ds_read16<7168>(A[1][3], a_lane + st_now);
+            mfma_acc(P[0], A[0][1], B0[1]);
+            epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[1][0], prv.az[1][0], dmp, dvo_prev, g - 1);
+            mfma_acc(P[0], A[0][2], B0[2]);
+            epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[1][0], prv.az[1][0], dmp, dvo_prev, g - 1);
+            mfma_acc(P[0], A[0][3], B0[3]);
+            epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[1][0], prv.az[1][0], dmp, dvo_prev, g - 1);
+            // ---- b1
+            mfma_first(P[1], A[0][0], Bc[0], bias);
+            mfma_acc(P[1], A[0][1], Bc[1]);
+            epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            mfma_acc(P[1], A[0][2], Bc[2]);
+            epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            mfma_acc(P[1], A[0][3], Bc[3]);
+            epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            mid_step();
+            // ---- b2
+            mfma_first(P[0], A[1][0], B0[0], bias);
+            read_frags(Bn, b_lane1 + st_next);
+            read_meta(prv, st_next);
+            mfma_acc(P[0], A[1][1], B0[1]);
+            epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
+            mfma_acc(P[0], A[1][2], B0[2]);
+            epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
+            mfma_acc(P[0], A[1][3], B0[3]);
+            epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
+            // ---- b3
+            mfma_first(P[1], A[1][0], Bc[0], bias);
+            read_frags(A[0], a_lane + st_next);
+            read_frags(B0, b_lane0 + st_next);
+            mfma_acc(P[1], A[1][1], Bc[1]);
+            epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
+            mfma_acc(P[1], A[1][2], Bc[2]);
+            epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
+            mfma_acc(P[1], A[1][3], Bc[3]);
+            epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
+        } else if constexpr (G == 64) {
+            // ---- b0
+            mfma_first(P[0], A[0][0], B0[0], bias);
+            ds_read16<2048>(A[1][0], a_lane + st_now);
+            ds_read16<3072>(A[1][1], a_lane + st_now);
+            mfma_acc(P[0], A[0][1], B0[1]);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[1][0], prv.az[1][0], dmp, dvo_prev, g - 1);
+            // ---- b1
+            mfma_first(P[1], A[0][0], Bc[0], bias);
+            mfma_acc(P[1], A[0][1], Bc[1]);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            mid_step();
+            // ---- b2
+            mfma_first(P[0], A[1][0], B0[0], bias);
+            read_frags(Bn, b_lane1 + st_next);
+            read_meta(prv, st_next);
+            mfma_acc(P[0], A[1][1], B0[1]);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
+            // ---- b3
+            mfma_first(P[1], A[1][0], Bc[0], bias);
+            read_frags(A[0], a_lane + st_next);
+            read_frags(B0, b_lane0 + st_next);
+            mfma_acc(P[1], A[1][1], Bc[1]);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
+        } else {
+            // G = 32: unit (block, k) is one MFMA over chunk k = group g + k; P[k] holds it
+            // ---- b0
+            mfma_first(P[0], A[0][0], B0[0], bias);
+            ds_read16<2048>(A[1][0], a_lane + st_now);
+            ds_read16<3072>(A[1][1], a_lane + st_now);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1][1], prv.z[1][1], prv.as[1][1], prv.az[1][1], dmp, dvo_prev, g - 1);
+            mfma_first(P[1], A[0][1], B0[1], bias);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            // ---- b1
+            mfma_first(P[0], A[0][0], Bc[0], bias);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[0][0], P[1], cur.rec[0][1], cur.z[0][1], cur.as[0][1], cur.az[0][1], dmp, dvo[0][0], g + 1);
+            mfma_first(P[1], A[0][1], Bc[1], bias);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[0][1], P[0], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
+            mid_step();
+            // ---- b2
+            mfma_first(P[0], A[1][0], B0[0], bias);
+            read_frags(Bn, b_lane1 + st_next);
+            read_meta(prv, st_next);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1][1], cur.z[1][1], cur.as[0][1], cur.az[0][1], dmp, dvo[0][1], g + 1);
+            mfma_first(P[1], A[1][1], B0[1], bias);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
+            // ---- b3
+            mfma_first(P[0], A[1][0], Bc[0], bias);
+            read_frags(A[0], a_lane + st_next);
+            read_frags(B0, b_lane0 + st_next);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][0], P[1], cur.rec[0][1], cur.z[0][1], cur.as[1][1], cur.az[1][1], dmp, dvo[1][0], g + 1);
+            mfma_first(P[1], A[1][1], Bc[1], bias);
+            epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[0], cur.rec[1][0], cur.z[1][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][1], g);
+        }
     };
-    int u = 0;  // global step: stage u % 3
+    int u = 0;  // global step: stage u % NS
     for (int r = 0; r < items; ++r) {
         begin_item(r);
         for (int t = 0; t < steps; t += 2, u += 2) {
-            const bool wide = r > 0 && t == 0;
-            step_body(t, u, r, std::integral_constant<int, 0>{}, wide);
-            step_body(t + 1, u + 1, r, std::integral_constant<int, 1>{}, wide);
+            step_body(t, u, r, std::integral_constant<int, 0>{}, r > 0 && t <= NS - 2);
+            step_body(t + 1, u + 1, r, std::integral_constant<int, 1>{}, r > 0 && t + 1 <= NS - 2);
         }
         // the reads issued in the last step (the next item's step 0 operands and metadata) land before the registers
         // they target can be given to anything else (after the last item nothing reads them)
-        lgkm_wait<0>(A[0], B0, B1, mt[0].rec, mt[0].as, mt[0].az);
-        // drain: the epilogue of the item's last b3 (step steps - 1, parity 1)
+        lgkm_wait<0>(A[0], B0, B1, mt[0].rec, mt[0].z, mt[0].as, mt[0].az);
+        // drain: the epilogue of the item's last unit (block b3 and the step's last group, step steps - 1, parity 1)
         KQ_ASM("s_nop 11");
-        epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], mt[1].rec[1], mt[1].as[1], mt[1].az[1], dmp, dvo[1][1],
-                                              ks * steps + steps - 1);
+        epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], mt[1].rec[1][GPS - 1], mt[1].z[1][GPS - 1], mt[1].as[1][GPS - 1], mt[1].az[1][GPS - 1],
+                                              dmp, dvo[1][1], (ks * steps + steps) * GPS - 1);
         if constexpr (SPLIT) {
             // partial tile [16 chunks][512 threads][4 floats]: chunk j of every thread is one coalesced 8 KiB run
             v4f* dst = reinterpret_cast<v4f*>(a.partial) + (static_cast<std::int64_t>(ks) * tiles + tile) * 16 * kThreads + tid;
@@ -732,7 +873,8 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
                         dst[((i * 2 + c) * 4 + q4) * kThreads] =
                             v4f{acc[i][c][4 * q4], acc[i][c][4 * q4 + 1], acc[i][c][4 * q4 + 2], acc[i][c][4 * q4 + 3]};
         } else {
-            store8t<STAT, GELU>(a, acc, m0, wm, gc, lane);
+            if constexpr (GELU || DBG) store8t<STAT, GELU>(a, acc, m0, wm, gc, lane);
+            else store8d<STAT>(a, acc, m0, wm, gc, lane);
         }
         // the next item starts from zero accumulators, the bias and "step -1" metadata zeros (its step 0 operands and
         // metadata were read during this item's last step)
@@ -744,11 +886,14 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
                 for (int k = 0; k < 16; ++k) acc[i][c][k] = 0.F;
         P[1] = bias;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            mt[1].rec[i] = v4i{0, 0, 0, 0};
-            mt[1].as[i] = 0.F;
-            mt[1].az[i] = 0.F;
-        }
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int gg = 0; gg < GPS; ++gg) {
+                mt[1].rec[i][gg] = v2i{0, 0};
+                mt[1].z[i][gg] = 0.F;
+                mt[1].as[i][gg] = 0.F;
+                mt[1].az[i][gg] = 0.F;
+            }
     }
     KQ_ASM("s_waitcnt vmcnt(0)" ::: "memory");  // the copies past the range land before the workgroup ends
 }
@@ -789,7 +934,8 @@ __global__ __launch_bounds__(kThreads) void gemm8_reduce_kernel(Gemm8Args a) {
                 }
     }
     const int gc[2] = {col_block<GELU>(a, nbk, GELU ? wn : 2 * wn), col_block<GELU>(a, nbk, GELU ? wn + 2 : 2 * wn + 1)};
-    store8t<STAT, GELU>(a, acc, mb * kBM, wm, gc, lane);
+    if constexpr (GELU) store8t<STAT, true>(a, acc, mb * kBM, wm, gc, lane);
+    else store8d<STAT>(a, acc, mb * kBM, wm, gc, lane);
 }
 
 }  // namespace
@@ -813,7 +959,10 @@ int device_cus() {
 }  // namespace
 
 bool gemm8_eligible(const Weight& w) {
-    return w.tiled && w.geo.bits == 4 && w.geo.group == 128 && w.geo.cols % 256 == 0 && w.geo.cols_p == w.geo.cols;
+    const int g = w.geo.group;
+    // k steps of 128 (g = 128) or 64 columns, walked in pairs
+    return w.tiled && w.geo.bits == 4 && (g == 32 || g == 64 || g == 128) && w.geo.cols % (g == 128 ? 256 : 128) == 0 &&
+           w.geo.cols_p == w.geo.cols;
 }
 
 Gemm8Plan gemm8_plan(const Weight& w, std::int64_t M, bool gelu) {
@@ -821,10 +970,12 @@ Gemm8Plan gemm8_plan(const Weight& w, std::int64_t M, bool gelu) {
     const int NB = static_cast<int>((w.geo.rows + 31) / 32);
     p.m_blocks = static_cast<int>((M + kBM - 1) / kBM);
     p.n_blocks = gelu ? (NB / 2 + 1) / 2 : (NB + 3) / 4;
-    const int k_steps = static_cast<int>(w.geo.cols / kStepK);
+    const int k_steps = static_cast<int>(w.geo.cols / (w.geo.group == 128 ? 128 : 64));
     const int tiles = p.m_blocks * p.n_blocks;
+    // split K only as far as the items still fit one wave of the 256 CUs: a split that leaves some CUs with two items
+    // takes as long as no split and adds the partial traffic
     p.ksplit = 1;
-    for (int sp = 2; sp <= 8 && tiles * p.ksplit < 256; sp *= 2) {
+    for (int sp = 2; sp <= 8 && tiles * sp <= 256; sp *= 2) {
         if (k_steps % (2 * sp) || k_steps / sp < 4) break;
         p.ksplit = sp;
     }
@@ -836,12 +987,13 @@ bool gemm8_fits(const LinearCall& c) {
     if (!w.has_prefill || !gemm8_eligible(w) || c.M <= 16) return false;
     if (c.path != PATH_BLOCKWISE && c.path != PATH_SYMMETRIC) return false;
     if (c.path == PATH_SYMMETRIC && w.zero_mode != ZERO_NONE) return false;
-    if (c.gelu_gate && ((w.geo.rows / 2) % 32)) return false;
+    if (c.gelu_gate && ((w.geo.rows / 2) % 32 || w.geo.group != 128)) return false;
     if (w.geo.rows % 4) return false;  // 16-byte output stores of four columns
+    if (w.geo.rows >= (std::int64_t{1} << 21)) return false;  // a tile's output offsets (256 rows) stay below 2^31
     if ((reinterpret_cast<std::uintptr_t>(c.x) & 15u) || (c.norm_inv && (reinterpret_cast<std::uintptr_t>(c.norm_w1) & 15u)))
         return false;
     const std::int64_t M_p = round_up(c.M, kBM);
-    const std::int64_t NB = (w.geo.rows + 31) / 32, groups = w.geo.cols / 128;
+    const std::int64_t NB = (w.geo.rows + 31) / 32, groups = w.geo.cols / w.geo.group;
     if (M_p * w.geo.cols >= (std::int64_t{1} << 31) || groups * NB * 512 >= (std::int64_t{1} << 31) ||
         groups * M_p * 4 >= (std::int64_t{1} << 31) || M_p >= (std::int64_t{1} << 24))
         return false;
@@ -855,26 +1007,59 @@ std::size_t gemm8_partial_bytes(const Weight& w, std::int64_t M, bool gelu) {
 }
 
 namespace {
-template <bool SF16, bool STAT, bool ZF, bool GELU, bool SPLIT, bool DBG>
+template <int G, bool SF16, bool STAT, bool ZF, bool GELU, bool SPLIT, bool DBG>
 hipError_t launch8(const Gemm8Args& g, unsigned blocks, hipStream_t stream) {
-    auto kern = gemm8_kernel<SF16, STAT, ZF, GELU, SPLIT, DBG>;
+    auto kern = gemm8_kernel<G, SF16, STAT, ZF, GELU, SPLIT, DBG>;
+    constexpr int lds = Geo8<G>::kLds;
     static bool configured = false;  // per instance: the dynamic LDS limit is raised once
     if (!configured) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), kLds, stream, g);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, stream, g);
     return hipGetLastError();
 }
-template <bool SF16, bool STAT, bool ZF, bool GELU>
+template <int G, bool SF16, bool STAT, bool ZF, bool GELU>
 hipError_t launch8_split(const Gemm8Args& g, unsigned blocks, bool split, bool dbg, hipStream_t stream) {
     if constexpr (!GELU) {  // the parity dump covers plain projections
-        if (dbg) return split ? launch8<SF16, STAT, ZF, false, true, true>(g, blocks, stream)
-                              : launch8<SF16, STAT, ZF, false, false, true>(g, blocks, stream);
+        if (dbg) return split ? launch8<G, SF16, STAT, ZF, false, true, true>(g, blocks, stream)
+                              : launch8<G, SF16, STAT, ZF, false, false, true>(g, blocks, stream);
     }
-    return split ? launch8<SF16, STAT, ZF, GELU, true, false>(g, blocks, stream)
-                 : launch8<SF16, STAT, ZF, GELU, false, false>(g, blocks, stream);
+    return split ? launch8<G, SF16, STAT, ZF, GELU, true, false>(g, blocks, stream)
+                 : launch8<G, SF16, STAT, ZF, GELU, false, false>(g, blocks, stream);
+}
+template <int G, bool SF16, bool STAT, bool ZF>
+hipError_t launch8_gelu(const Gemm8Args& g, unsigned blocks, bool gelu, bool split, bool dbg, hipStream_t stream) {
+    if constexpr (G == 128) {  // the gate/up pairing serves g = 128 weights
+        if (gelu) return launch8_split<G, SF16, STAT, ZF, true>(g, blocks, split, dbg, stream);
+    }
+    return launch8_split<G, SF16, STAT, ZF, false>(g, blocks, split, dbg, stream);
+}
+template <int G>
+hipError_t launch8_modes(const Gemm8Args& g, unsigned blocks, bool sf16, bool stat, bool zf, bool gelu, bool split, bool dbg,
+                         hipStream_t stream) {
+    if (sf16) {
+        if (stat) return launch8_gelu<G, true, true, false>(g, blocks, gelu, split, dbg, stream);
+        if (zf) return launch8_gelu<G, true, false, true>(g, blocks, gelu, split, dbg, stream);
+        return launch8_gelu<G, true, false, false>(g, blocks, gelu, split, dbg, stream);
+    }
+    if (stat) return launch8_gelu<G, false, true, false>(g, blocks, gelu, split, dbg, stream);
+    if (zf) return launch8_gelu<G, false, false, true>(g, blocks, gelu, split, dbg, stream);
+    return launch8_gelu<G, false, false, false>(g, blocks, gelu, split, dbg, stream);
+}
+template <int G>
+void launch_quantize8(const QRow8Args& q, bool stat, bool f32, bool norm, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((static_cast<std::int64_t>(q.M_p / 32) * (q.K / 128) + 3) / 4)), block(256);
+#define KQ_Q8(QM, F, NM) hipLaunchKernelGGL((quantize_rows8_kernel<QM, F, NM, G>), grid, block, 0, stream, q)
+    if (stat) {
+        if (f32) { if (norm) KQ_Q8(QUANT_STATIC, true, true); else KQ_Q8(QUANT_STATIC, true, false); }
+        else { if (norm) KQ_Q8(QUANT_STATIC, false, true); else KQ_Q8(QUANT_STATIC, false, false); }
+    } else {
+        if (f32) { if (norm) KQ_Q8(QUANT_DYN_SYM, true, true); else KQ_Q8(QUANT_DYN_SYM, true, false); }
+        else { if (norm) KQ_Q8(QUANT_DYN_SYM, false, true); else KQ_Q8(QUANT_DYN_SYM, false, false); }
+    }
+#undef KQ_Q8
 }
 }  // namespace
 
@@ -885,6 +1070,7 @@ hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t 
     const bool zf = w.zero_mode == ZERO_FLOAT;
     const int M = static_cast<int>(c.M), K = static_cast<int>(w.geo.cols);
     const int M_p = static_cast<int>(round_up(c.M, kBM));
+    const int G = w.geo.group;
     // activation quantization into the workspace
     QRow8Args q{};
     q.x = c.x;
@@ -901,17 +1087,10 @@ hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t 
     q.d_scales = d_scales;
     q.d_sums = d_sums;
     {
-        const dim3 grid(static_cast<unsigned>((static_cast<std::int64_t>(M_p / 32) * (K / 128) + 3) / 4)), block(256);
         const bool f32 = c.x_type == ACT_F32, norm = c.norm_inv != nullptr;
-#define KQ_Q8(QM, F, NM) hipLaunchKernelGGL((quantize_rows8_kernel<QM, F, NM>), grid, block, 0, stream, q)
-        if (stat) {
-            if (f32) { if (norm) KQ_Q8(QUANT_STATIC, true, true); else KQ_Q8(QUANT_STATIC, true, false); }
-            else { if (norm) KQ_Q8(QUANT_STATIC, false, true); else KQ_Q8(QUANT_STATIC, false, false); }
-        } else {
-            if (f32) { if (norm) KQ_Q8(QUANT_DYN_SYM, true, true); else KQ_Q8(QUANT_DYN_SYM, true, false); }
-            else { if (norm) KQ_Q8(QUANT_DYN_SYM, false, true); else KQ_Q8(QUANT_DYN_SYM, false, false); }
-        }
-#undef KQ_Q8
+        if (G == 128) launch_quantize8<128>(q, stat, f32, norm, stream);
+        else if (G == 64) launch_quantize8<64>(q, stat, f32, norm, stream);
+        else launch_quantize8<32>(q, stat, f32, norm, stream);
         if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
     if (quantize_only) return hipSuccess;
@@ -930,7 +1109,7 @@ hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t 
     g.N = static_cast<int>(w.geo.rows);
     g.K = K;
     g.NB = static_cast<int>((w.geo.rows + 31) / 32);
-    g.groups = K / 128;
+    g.groups = K / G;
     g.m_blocks = p.m_blocks;
     g.n_blocks = p.n_blocks;
     g.ksplit = p.ksplit;
@@ -940,18 +1119,9 @@ hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t 
     const int total = p.m_blocks * p.n_blocks * p.ksplit;
     const unsigned blocks = static_cast<unsigned>(std::min(total, device_cus()));  // persistent: items loop in the kernel
     hipError_t e;
-#define KQ_G8(SF, ST, Z) e = c.gelu_gate ? launch8_split<SF, ST, Z, true>(g, blocks, split, dbg, stream) \
-                                         : launch8_split<SF, ST, Z, false>(g, blocks, split, dbg, stream)
-    if (sf16) {
-        if (stat) KQ_G8(true, true, false);
-        else if (zf) KQ_G8(true, false, true);
-        else KQ_G8(true, false, false);
-    } else {
-        if (stat) KQ_G8(false, true, false);
-        else if (zf) KQ_G8(false, false, true);
-        else KQ_G8(false, false, false);
-    }
-#undef KQ_G8
+    if (G == 128) e = launch8_modes<128>(g, blocks, sf16, stat, zf, c.gelu_gate, split, dbg, stream);
+    else if (G == 64) e = launch8_modes<64>(g, blocks, sf16, stat, zf, false, split, dbg, stream);
+    else e = launch8_modes<32>(g, blocks, sf16, stat, zf, false, split, dbg, stream);
     if (e != hipSuccess || !split) return e;
     const unsigned tiles = static_cast<unsigned>(p.m_blocks * p.n_blocks);
     if (stat) {

@@ -134,7 +134,7 @@ def test_routes_of_baseline_shapes(lib):
     assert route(lib, 4, 32, 8192, 2048, 0, 1) == DECODE           # configs[0]
     assert route(lib, 4, 128, 8192, 2048, 1, 2048) == GEMM8        # configs[2]
     assert route(lib, 4, 128, 8192, 2048, 1, 512) == GEMM8
-    assert route(lib, 4, 32, 2560, 2048, 0, 2048) == GEMM_I4G      # configs[3] fused QKV
+    assert route(lib, 4, 32, 2560, 2048, 0, 2048) == GEMM8         # configs[3] fused QKV
     assert route(lib, 4, 128, 16384, 2048, 1, 2048, gelu=1) == GEMM8
     assert route(lib, 4, 128, 2048, 8192, 1, 2048) == GEMM8        # configs[3] down
     assert route(lib, 4, 128, 8192, 2048, 2, 2048) == GEMM8        # additive float zeros
@@ -145,6 +145,10 @@ def test_routes_of_baseline_shapes(lib):
 
 
 def test_routes_of_other_shapes(lib):
+    assert route(lib, 4, 64, 2560, 2048, 1, 300) == GEMM8          # g = 64 prefill
+    assert route(lib, 4, 32, 2560, 2048, 2, 300) == GEMM8          # g = 32 with additive float zeros
+    assert route(lib, 4, 32, 2562, 2048, 0, 300) == GEMM_I4G       # N % 4 != 0: no 16-byte output stores
+    assert route(lib, 4, 32, 2560, 2048, 0, 300, gelu=1) == GEMM   # gate/up pairing is for g = 128 weights
     assert route(lib, 4, 128, 256, 512, 1, 12) == SKINNY
     assert route(lib, 4, 96, 256, 384, 1, 3) == ROWMAJOR
     assert route(lib, 2, 32, 256, 512, 0, 1) == PORTABLE           # dynamic 2-bit: Kidi's portable path

@@ -103,13 +103,18 @@ CASES = [
     (4, 128, 64, 4096, 256, "zp", 0.0, True, 0.0),
     (4, 128, 300, 8192, 256, None, 0.0, False, 0.001),
     (4, 128, 40, 8192, 144, None, 0.05, False, 0.0),
-    # 4-bit g = 32 / 64 prefill GEMM (two-stage LDS int8 MFMA kernel): fused-QKV-like K, ragged M and N, zero points,
-    # calibrated inputs, a single k step
+    # 4-bit g = 32 / 64 prefill (gemm8_kernel from the prefill copy: one or two groups per 64-column step):
+    # fused-QKV-like K, ragged M and N, zero points, additive float zeros, calibrated inputs, a single item step pair
     (4, 32, 300, 2048, 640, None, 0.0, True, 0.001),
     (4, 32, 64, 1024, 272, "zp", 0.0, True, 0.0),
     (4, 64, 140, 1536, 400, "zp", 0.0, False, 0.001),
     (4, 64, 33, 512, 128, None, 0.05, False, 0.0),
     (4, 32, 129, 128, 256, None, 0.0, False, 0.0),
+    (4, 32, 260, 1024, 256, "f16", 0.0, True, 0.001),
+    (4, 64, 100, 512, 144, "f16", 0.0, False, 0.0),
+    # 4-bit g = 32 / 64 with N % 4 != 0 (no 16-byte output stores): the two-stage LDS kernel gemm_i4g_kernel
+    (4, 32, 100, 512, 270, None, 0.0, False, 0.0),
+    (4, 64, 70, 1024, 142, "zp", 0.0, True, 0.001),
     # group sizes the tiles cannot carry (row-major integer path)
     (4, 96, 3, 384, 256, "zp", 0.0, False, 0.0),
     (8, 48, 2, 288, 96, None, 0.0, False, 0.0),

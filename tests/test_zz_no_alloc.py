@@ -56,7 +56,8 @@ def _both(N_, lib, dw, x, input_scale=0.0):
 @pytest.mark.parametrize("bits,group,K,N,zp,route,rows", [
     (4, 128, 1024, 400, True, "gemm8_kernel", (300, 40)),       # g = 128 prefill GEMM (codes, transposed scales)
     (4, 128, 8192, 256, True, "gemm8_kernel", (300, 64)),       # split K: partial tiles in the scratch
-    (4, 32, 1024, 272, False, "gemm_i4g_kernel", (200, 33)),    # g = 32 prefill GEMM
+    (4, 32, 1024, 272, False, "gemm8_kernel", (200, 33)),       # g = 32 prefill GEMM
+    (4, 32, 1024, 270, False, "gemm_i4g_kernel", (200, 33)),    # g = 32, N % 4 != 0: the two-stage LDS GEMM
     (8, 32, 512, 200, False, "gemm_kernel", (150, 20)),         # generic quantizer + GEMM
     (4, 128, 2048, 8192, True, "decode_kernel", (4, 1)),        # decode: the scratch is passed, not needed
 ])
