@@ -42,32 +42,34 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 
-constexpr int kBM = 256;  // tile rows (columns: 4 blocks of 32)
+constexpr int kBM = 256;  // rows of the activation row padding (M_p) and of the wide tile (columns: 4 blocks of 32)
 constexpr int kWaves = 8, kThreads = 64 * kWaves;
 constexpr float kBias = 12582912.F;                  // 1.5 * 2^23
 constexpr int kBiasBits = 0x4B400000;
 
-// Step geometry of the GEMM for weight group size G. One k step is 128 columns (one group) for G = 128 and 64 columns
-// (one group of 64 or two of 32) otherwise. One LDS stage (one k step): activation fragments [8 row blocks][CH k-chunks]
-// [1 KiB], weight fragments [4 column blocks][CH][1 KiB], the 256 rows' activation scales [GPS groups][256], a_s * Q
-// (additive zeros) likewise, and the weight records [GPS][4 column blocks][32 columns][16 B]. After the stages, 1 KiB
-// that dummy copies write into. Direct copies per wave and step: CH activation fragments, CH / 2 weight fragments,
-// one metadata block (or a dummy).
-template <int G>
+// Step geometry of the GEMM for weight group size G and RB 32-row blocks per wave (tile rows TM = 128 RB). One k step
+// is 128 columns (one group) for G = 128 and 64 columns (one group of 64 or two of 32) otherwise. One LDS stage (one k
+// step): activation fragments [4 RB row blocks][CH k-chunks][1 KiB], weight fragments [4 column blocks][CH][1 KiB], the
+// tile's activation scales [GPS groups][256 rows], a_s * Q (additive zeros) likewise, and the weight records [GPS][4
+// column blocks][32 columns][16 B]. After the stages, 1 KiB that dummy copies write into. Direct copies per wave and
+// step: RB CH / 2 activation fragments, CH / 2 weight fragments, one metadata block (or a dummy).
+template <int G, int RB = 2>
 struct Geo8 {
+    static constexpr int TM = 128 * RB;
     static constexpr int kStepK = G == 128 ? 128 : 64;
     static constexpr int CH = kStepK / 32;           // 32-column chunks per step
     static constexpr int GPS = kStepK / G;           // groups per step
     static constexpr int kAOff = 0;
-    static constexpr int kBOff = kAOff + 8 * CH * 1024;
+    static constexpr int kBOff = kAOff + 4 * RB * CH * 1024;
     static constexpr int kSOff = kBOff + 4 * CH * 1024;
     static constexpr int kZOff = kSOff + GPS * 1024;
     static constexpr int kWOff = kZOff + GPS * 1024;
     static constexpr int kStageBytes = kWOff + GPS * 2048;
-    static constexpr int kStages = G == 128 ? 3 : 4;
+    static constexpr int kStages = (G == 128 && RB == 2) ? 3 : 4;
     static constexpr int kDummyOff = kStages * kStageBytes;
-    static constexpr int kLds = kDummyOff + 1024;  // G = 128: 157 KiB; 64: 113 KiB; 32: 129 KiB
-    static constexpr int kCopies = CH + CH / 2 + 1;
+    static constexpr int kLds = kDummyOff + 1024;  // RB = 2: G = 128: 157 KiB; 64: 113 KiB; 32: 129 KiB. RB = 1, G = 128: 145 KiB
+    static constexpr int kACopies = RB * CH / 2;
+    static constexpr int kCopies = kACopies + CH / 2 + 1;
     static_assert(kLds <= 160 * 1024, "LDS budget");
     static_assert(4 * GPS <= kWaves, "one metadata copy per wave");
 };
@@ -398,15 +400,15 @@ __device__ __forceinline__ void quad_transpose(float (&v)[4], int lane) {
 constexpr int kTileStoresGelu = 8;
 constexpr int min63(int n) { return n < 63 ? n : 63; }
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-template <bool STAT, bool GELU>
-__device__ __forceinline__ void store8t(const Gemm8Args& a, const float (&acc)[2][2][16], int m0, int wm, const int (&gc)[2],
+template <bool STAT, bool GELU, int RB = 2>
+__device__ __forceinline__ void store8t(const Gemm8Args& a, const float (&acc)[RB][2][16], int m0, int wm, const int (&gc)[2],
                                         int lane) {
     const int n_out = GELU ? (a.N >> 1) : a.N;
-    const int rows = min(a.M - m0, kBM);
+    const int rows = min(a.M - m0, 128 * RB);
     const __amdgpu_buffer_rsrc_t yres = rsrc(a.y + static_cast<std::int64_t>(m0) * n_out, static_cast<std::uint32_t>(rows) * n_out * 4);
-    const int r_lane = 64 * wm + 4 * (lane >> 5) + (lane & 3), c_lane = lane & 28;
+    const int r_lane = 32 * RB * wm + 4 * (lane >> 5) + (lane & 3), c_lane = lane & 28;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < RB; ++i) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const std::uint32_t row_off = static_cast<std::uint32_t>(r_lane + 32 * i + 8 * j) * n_out;
@@ -440,17 +442,16 @@ __device__ __forceinline__ void store8t(const Gemm8Args& a, const float (&acc)[2
     }
 }
 
-// Final values of a wave's 2 x 2 blocks for plain projections, stored straight from the accumulators with 4-byte
+// Final values of a wave's RB x 2 blocks for plain projections, stored straight from the accumulators with 4-byte
 // stores (no transpose: every VALU instruction counts in this VALU-bound kernel). Element k of block (i, c) is row
-// 64 wm + 32 i + 8 (k / 4) + 4 (lane / 32) + k % 4, column 32 gc[c] + lane % 32: one store instruction writes two
-// 128-byte row segments. Every lane issues exactly kTileStoresD stores; rows past M and columns past N get a
-// per-lane offset beyond the buffer resource, whose range check drops them.
-constexpr int kTileStoresD = 64;
-template <bool STAT>
-__device__ __forceinline__ void store8d(const Gemm8Args& a, const float (&acc)[2][2][16], int m0, int wm, const int (&gc)[2],
+// 32 RB wm + 32 i + 8 (k / 4) + 4 (lane / 32) + k % 4, column 32 gc[c] + lane % 32: one store instruction writes two
+// 128-byte row segments. Every lane issues exactly 32 RB stores; rows past M and columns past N get a per-lane
+// offset beyond the buffer resource, whose range check drops them.
+template <bool STAT, int RB = 2>
+__device__ __forceinline__ void store8d(const Gemm8Args& a, const float (&acc)[RB][2][16], int m0, int wm, const int (&gc)[2],
                                         int lane) {
     const int n_out = a.N;
-    const int rows = min(a.M - m0, kBM);
+    const int rows = min(a.M - m0, 128 * RB);
     const __amdgpu_buffer_rsrc_t yres = rsrc(a.y + static_cast<std::int64_t>(m0) * n_out, static_cast<std::uint32_t>(rows) * n_out * 4);
     const std::uint32_t row_bytes = static_cast<std::uint32_t>(n_out) * 4;
     const bool cal = a.output_scale > 0.F;
@@ -460,8 +461,8 @@ __device__ __forceinline__ void store8d(const Gemm8Args& a, const float (&acc)[2
         // dead columns: an offset past the buffer that stays past it for every row added below (rows * row_bytes < 2^31)
         const std::uint32_t col_off = n < n_out ? static_cast<std::uint32_t>(n) * 4 : 0x80000000u;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const std::uint32_t base = col_off + static_cast<std::uint32_t>(64 * wm + 32 * i + 4 * (lane >> 5)) * row_bytes;
+        for (int i = 0; i < RB; ++i) {
+            const std::uint32_t base = col_off + static_cast<std::uint32_t>(32 * RB * wm + 32 * i + 4 * (lane >> 5)) * row_bytes;
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
                 float x = acc[i][c][k];
@@ -488,14 +489,15 @@ struct Copy {
     int kbase;
 };
 
-template <int G, bool SF16, bool STAT, bool ZF, bool GELU, bool SPLIT, bool DBG>
+template <int G, int RB, bool SF16, bool STAT, bool ZF, bool GELU, bool SPLIT, bool DBG>
 __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
-    using Q = Geo8<G>;
-    constexpr int CH = Q::CH, GPS = Q::GPS, NS = Q::kStages;
+    using Q = Geo8<G, RB>;
+    constexpr int CH = Q::CH, GPS = Q::GPS, NS = Q::kStages, TM = Q::TM;
+    static_assert(RB == 2 || (G == 128 && !GELU && !SPLIT), "the 128-row tile serves plain g = 128 projections without split K");
     extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 3, wn = wave >> 2;  // rows [64 wm, +64) of the tile; column blocks below
+    const int wm = wave & 3, wn = wave >> 2;  // rows [32 RB wm, +32 RB) of the tile; column blocks below
     const std::uint32_t lds0 = lds_addr(lds);
 
     // Work items (K range, row block, column block) in an order that gives each XCD a contiguous range of tiles, row
@@ -517,13 +519,13 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         Item it;
         it.ks = i / tiles;
         it.tile = i - it.ks * tiles;
-        it.m0 = (it.tile % a.m_blocks) * kBM;
+        it.m0 = (it.tile % a.m_blocks) * TM;
         it.nbk = it.tile / a.m_blocks;
         return it;
     };
 
-    // ---- copies of one step: wave w brings activation row block w (CH fragments), half of weight column block w / 2
-    // (CH / 2 fragments) and one metadata block: waves 0 .. 2 GPS - 1 the weight records of group w / 2 of the step,
+    // ---- copies of one step: wave w brings RB CH / 2 activation fragments (RB = 2: row block w; RB = 1: half of row
+    // block w / 2), half of weight column block w / 2 (CH / 2 fragments) and one metadata block: waves 0 .. 2 GPS - 1 the weight records of group w / 2 of the step,
     // column blocks 0-1 (w even) or 2-3; the next GPS waves the tile's activation scales of one group each; the next
     // GPS its a_s * Q (additive zeros); the other copies write into the dummy area.
     const int cbc = wave >> 1, ckc = (CH / 2) * (wave & 1);
@@ -550,7 +552,7 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         const Item it = item_of(r);
         Copy cp;
         cp.kbase = it.ks * steps;
-        cp.abase = a.q + static_cast<std::int64_t>(it.m0 / 32) * KC * 1024;
+        cp.abase = a.q + static_cast<std::int64_t>(it.m0 / 32) * KC * 1024;  // the tile's first row block
         const int gcb = col_block<GELU>(a, it.nbk, cbc);
         const bool clive = gcb < a.NB;
         cp.bbase = a.w + static_cast<std::int64_t>(clive ? gcb : 0) * KC * 1024;
@@ -563,17 +565,21 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             cp.meta0 = static_cast<std::uint32_t>(cp.kbase) * meta_step + meta_gg + static_cast<std::uint32_t>(it.m0) * 4;
         return cp;
     };
-    // part 0: activation fragments [0, CH / 2), part 1: [CH / 2, CH), part 2: weight fragments and metadata
+    // part 0: activation fragments [0, CH / 2) of the wave's row block (RB = 1: its half of the chunks), part 1 (RB =
+    // 2): [CH / 2, CH), part 2: weight fragments and metadata
+    const int arb = RB == 2 ? wave : wave >> 1, ack = RB == 2 ? 0 : (CH / 2) * (wave & 1);
     auto issue_copy = [&](const Copy& cp, int u, int t, auto part) __attribute__((always_inline)) {
         constexpr int pt = decltype(part)::value;
         const std::uint32_t kc0 = static_cast<std::uint32_t>((cp.kbase + t) * CH);
         std::uint8_t* base = lds + (u % NS) * Q::kStageBytes;
         if constexpr (pt < 2) {
-            const __amdgpu_buffer_rsrc_t ares = rsrc(cp.abase, static_cast<std::uint32_t>(kBM / 32) * KC * 1024);
+            if constexpr (RB == 2 || pt == 0) {
+                const __amdgpu_buffer_rsrc_t ares = rsrc(cp.abase, static_cast<std::uint32_t>(TM / 32) * KC * 1024);
 #pragma unroll
-            for (int i = pt * (CH / 2); i < (pt + 1) * (CH / 2); ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(base + Q::kAOff + (wave * CH + i) * 1024), 16, lane * 16,
-                                                         (static_cast<std::uint32_t>(wave) * KC + kc0 + i) * 1024, 0, 0);
+                for (int i = ack + pt * (CH / 2); i < ack + (pt + 1) * (CH / 2); ++i)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (lds_void*)(base + Q::kAOff + (arb * CH + i) * 1024), 16,
+                                                             lane * 16, (static_cast<std::uint32_t>(arb) * KC + kc0 + i) * 1024, 0, 0);
+            }
         } else {
             const __amdgpu_buffer_rsrc_t bres = rsrc(cp.bbase, cp.bbytes);
 #pragma unroll
@@ -606,16 +612,16 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         issue_part(u, r, t, std::integral_constant<int, 2>{});
     };
 
-    // ---- the wave's fragments: row blocks 2 wm + i; column blocks (plain) 2 wn + i, (GELU) wn + 2 i
+    // ---- the wave's fragments: row blocks RB wm + i; column blocks (plain) 2 wn + i, (GELU) wn + 2 i
     const int cb_l0 = GELU ? wn : 2 * wn, cb_l1 = GELU ? wn + 2 : 2 * wn + 1;
-    const std::uint32_t a_lane = lds0 + Q::kAOff + (2 * wm * CH) * 1024 + lane * 16;
+    const std::uint32_t a_lane = lds0 + Q::kAOff + (RB * wm * CH) * 1024 + lane * 16;
     const std::uint32_t b_lane0 = lds0 + Q::kBOff + (cb_l0 * CH) * 1024 + lane * 16;
     const std::uint32_t b_lane1 = lds0 + Q::kBOff + (cb_l1 * CH) * 1024 + lane * 16;
     const int col = lane & 31;
     [[maybe_unused]] const std::uint32_t w_lane0 = lds0 + Q::kWOff + (cb_l0 * 32 + col) * 16;
     [[maybe_unused]] const std::uint32_t w_lane1 = lds0 + Q::kWOff + (cb_l1 * 32 + col) * 16;
-    [[maybe_unused]] const std::uint32_t s_lane = lds0 + Q::kSOff + (64 * wm + bcast_row(lane)) * 4;
-    [[maybe_unused]] const std::uint32_t z_lane = lds0 + Q::kZOff + (64 * wm + bcast_row(lane)) * 4;
+    [[maybe_unused]] const std::uint32_t s_lane = lds0 + Q::kSOff + (32 * RB * wm + bcast_row(lane)) * 4;
+    [[maybe_unused]] const std::uint32_t z_lane = lds0 + Q::kZOff + (32 * RB * wm + bcast_row(lane)) * 4;
     auto read_meta = [&](Meta<GPS>& mt, std::uint32_t stage) __attribute__((always_inline)) {
 #pragma unroll
         for (int gg = 0; gg < GPS; ++gg) {
@@ -627,11 +633,13 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             }
             if constexpr (!STAT) {
                 KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.as[0][gg]) : "v"(s_lane + stage), "n"(gg * 1024));
-                KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.as[1][gg]) : "v"(s_lane + stage), "n"(gg * 1024 + 128));
+                if constexpr (RB == 2)
+                    KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.as[1][gg]) : "v"(s_lane + stage), "n"(gg * 1024 + 128));
             }
             if constexpr (ZF) {
                 KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.az[0][gg]) : "v"(z_lane + stage), "n"(gg * 1024));
-                KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.az[1][gg]) : "v"(z_lane + stage), "n"(gg * 1024 + 128));
+                if constexpr (RB == 2)
+                    KQ_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(mt.az[1][gg]) : "v"(z_lane + stage), "n"(gg * 1024 + 128));
             }
         }
     };
@@ -650,7 +658,7 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     int gc[2] = {0, 0};
     int m0 = 0, ks = 0, tile = 0;
     Dump dmp{};
-    std::uint32_t dvo[2][2] = {{0u, 0u}, {0u, 0u}};
+    std::uint32_t dvo[RB][2] = {};
     auto begin_item = [&](int r) __attribute__((always_inline)) {
         const Item it = item_of(r);
         if (r > 0) item_copy = copy_of(r);
@@ -667,10 +675,10 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             dmp.bytes = static_cast<std::uint32_t>(rest < 0x7FFFFFFFull ? rest : 0x7FFFFFFFull);
             dmp.row_bytes = static_cast<std::uint32_t>(row_elems * 4);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < RB; ++i)
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
-                    const int n = 32 * gc[c] + col, r0 = 64 * wm + 32 * i + 4 * (lane >> 5);
+                    const int n = 32 * gc[c] + col, r0 = 32 * RB * wm + 32 * i + 4 * (lane >> 5);
                     dvo[i][c] = (gc[c] < a.NB && n < a.N && m0 + r0 < a.M)
                                     ? static_cast<std::uint32_t>((static_cast<std::uint64_t>(r0) * a.N + n) * a.groups * 4)
                                     : 0x80000000u;
@@ -679,11 +687,12 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     };
     // vector memory operations a lane issues when it stores a tile (outstanding after the tile)
     // (the parity-dump instances keep the 16-byte stores: the 4-byte form would need more registers than they have)
-    [[maybe_unused]] constexpr int kStoresAfter = SPLIT ? 16 : (GELU ? kTileStoresGelu : (DBG ? 16 : kTileStoresD));
+    // (store8d: 32 RB 4-byte stores; store8t: 8 RB 16-byte stores, 8 with GELU; split partials: 16)
+    [[maybe_unused]] constexpr int kStoresAfter = SPLIT ? 16 : (GELU ? kTileStoresGelu : (DBG ? 8 * RB : 32 * RB));
 
-    float acc[2][2][16];
+    float acc[RB][2][16];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -697,7 +706,7 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     v16i P[2];
     P[0] = bias;
     P[1] = bias;
-    v4i A[2][CH], B0[CH], B1[2][CH];
+    v4i A[RB][CH], B0[CH], B1[2][CH];
     Meta<GPS> mt[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -740,9 +749,9 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         const std::uint32_t st_now = static_cast<std::uint32_t>((u % NS) * Q::kStageBytes);
         const std::uint32_t st_next = static_cast<std::uint32_t>(((u + 1) % NS) * Q::kStageBytes);
         const int g = (ks * steps + t) * GPS;  // global index of the step's first group
-        const std::uint32_t dvo_prev = t > 0 ? dvo[1][1] : 0x80000000u;
+        const std::uint32_t dvo_prev = t > 0 ? dvo[RB - 1][1] : 0x80000000u;
         auto mid_step = [&]() __attribute__((always_inline)) {
-            lgkm_wait<0>(A[1]);
+            if constexpr (RB == 2) lgkm_wait<0>(A[1]);
             // the first NS - 1 steps after a tile's stores: those stores are younger than step t + 1's copies
             // (vmcnt counts to 63: a larger allowance waits for some of the stores too, which is only stricter)
             if (wide) KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(min63((NS - 2) * Q::kCopies + kStoresAfter)) : "memory");
@@ -750,7 +759,31 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             issue(u + NS, r, t + NS);
         };
         lgkm_wait<0>(A[0], B0, Bc, cur.rec, cur.z, cur.as, cur.az);  // step t's operands and metadata (read during step t - 1)
-        if constexpr (G == 128) {
+        if constexpr (RB == 1) {
+            // 128-row tile, G = 128: two blocks b0 (0, 0), b1 (0, 1) per step; every operand of step t + 1 is read
+            // during step t (after the mid-step barrier), so stage t is free at the barrier of step t as well
+            // ---- b0
+            mfma_first(P[0], A[0][0], B0[0], bias);
+            mfma_acc(P[0], A[0][1], B0[1]);
+            epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[0][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[0][0], prv.az[0][0], dmp, dvo_prev, g - 1);
+            mfma_acc(P[0], A[0][2], B0[2]);
+            epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[0][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[0][0], prv.az[0][0], dmp, dvo_prev, g - 1);
+            mfma_acc(P[0], A[0][3], B0[3]);
+            epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[0][0], prv.az[0][0], dmp, dvo_prev, g - 1);
+            // ---- b1
+            mfma_first(P[1], A[0][0], Bc[0], bias);
+            mid_step();
+            read_frags(Bn, b_lane1 + st_next);
+            read_meta(prv, st_next);
+            read_frags(B0, b_lane0 + st_next);
+            mfma_acc(P[1], A[0][1], Bc[1]);
+            epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            mfma_acc(P[1], A[0][2], Bc[2]);
+            epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            mfma_acc(P[1], A[0][3], Bc[3]);
+            epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            read_frags(A[0], a_lane + st_next);  // after the last MFMA that reads A[0] (and ten VALU)
+        } else if constexpr (G == 128) {
             // ---- b0
             mfma_first(P[0], A[0][0], B0[0], bias);
             ds_read16<4096>(A[1][0], a_lane + st_now);
@@ -859,8 +892,9 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         lgkm_wait<0>(A[0], B0, B1, mt[0].rec, mt[0].z, mt[0].as, mt[0].az);
         // drain: the epilogue of the item's last unit (block b3 and the step's last group, step steps - 1, parity 1)
         KQ_ASM("s_nop 11");
-        epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], mt[1].rec[1][GPS - 1], mt[1].z[1][GPS - 1], mt[1].as[1][GPS - 1], mt[1].az[1][GPS - 1],
-                                              dmp, dvo[1][1], (ks * steps + steps) * GPS - 1);
+        epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[RB - 1][1], P[1], mt[1].rec[1][GPS - 1], mt[1].z[1][GPS - 1],
+                                              mt[1].as[RB - 1][GPS - 1], mt[1].az[RB - 1][GPS - 1], dmp, dvo[RB - 1][1],
+                                              (ks * steps + steps) * GPS - 1);
         if constexpr (SPLIT) {
             // partial tile [16 chunks][512 threads][4 floats]: chunk j of every thread is one coalesced 8 KiB run
             v4f* dst = reinterpret_cast<v4f*>(a.partial) + (static_cast<std::int64_t>(ks) * tiles + tile) * 16 * kThreads + tid;
@@ -873,13 +907,13 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
                         dst[((i * 2 + c) * 4 + q4) * kThreads] =
                             v4f{acc[i][c][4 * q4], acc[i][c][4 * q4 + 1], acc[i][c][4 * q4 + 2], acc[i][c][4 * q4 + 3]};
         } else {
-            if constexpr (GELU || DBG) store8t<STAT, GELU>(a, acc, m0, wm, gc, lane);
-            else store8d<STAT>(a, acc, m0, wm, gc, lane);
+            if constexpr (GELU || DBG) store8t<STAT, GELU, RB>(a, acc, m0, wm, gc, lane);
+            else store8d<STAT, RB>(a, acc, m0, wm, gc, lane);
         }
         // the next item starts from zero accumulators, the bias and "step -1" metadata zeros (its step 0 operands and
         // metadata were read during this item's last step)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < RB; ++i)
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -972,9 +1006,17 @@ Gemm8Plan gemm8_plan(const Weight& w, std::int64_t M, bool gelu) {
     p.n_blocks = gelu ? (NB / 2 + 1) / 2 : (NB + 3) / 4;
     const int k_steps = static_cast<int>(w.geo.cols / (w.geo.group == 128 ? 128 : 64));
     const int tiles = p.m_blocks * p.n_blocks;
+    p.ksplit = 1;
+    // fewer 256-row tiles than CUs: 128-row tiles fill the chip without splitting K (no partial tiles, no reduction
+    // kernel), where they are enough to
+    const int m128 = static_cast<int>((M + 127) / 128);
+    if (w.geo.group == 128 && !gelu && tiles < 256 && m128 * p.n_blocks >= 32) {
+        p.rb = 1;
+        p.m_blocks = m128;
+        return p;
+    }
     // split K only as far as the items still fit one wave of the 256 CUs: a split that leaves some CUs with two items
     // takes as long as no split and adds the partial traffic
-    p.ksplit = 1;
     for (int sp = 2; sp <= 8 && tiles * sp <= 256; sp *= 2) {
         if (k_steps % (2 * sp) || k_steps / sp < 4) break;
         p.ksplit = sp;
@@ -1007,10 +1049,10 @@ std::size_t gemm8_partial_bytes(const Weight& w, std::int64_t M, bool gelu) {
 }
 
 namespace {
-template <int G, bool SF16, bool STAT, bool ZF, bool GELU, bool SPLIT, bool DBG>
+template <int G, int RB, bool SF16, bool STAT, bool ZF, bool GELU, bool SPLIT, bool DBG>
 hipError_t launch8(const Gemm8Args& g, unsigned blocks, hipStream_t stream) {
-    auto kern = gemm8_kernel<G, SF16, STAT, ZF, GELU, SPLIT, DBG>;
-    constexpr int lds = Geo8<G>::kLds;
+    auto kern = gemm8_kernel<G, RB, SF16, STAT, ZF, GELU, SPLIT, DBG>;
+    constexpr int lds = Geo8<G, RB>::kLds;
     static bool configured = false;  // per instance: the dynamic LDS limit is raised once
     if (!configured) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -1023,30 +1065,32 @@ hipError_t launch8(const Gemm8Args& g, unsigned blocks, hipStream_t stream) {
 template <int G, bool SF16, bool STAT, bool ZF, bool GELU>
 hipError_t launch8_split(const Gemm8Args& g, unsigned blocks, bool split, bool dbg, hipStream_t stream) {
     if constexpr (!GELU) {  // the parity dump covers plain projections
-        if (dbg) return split ? launch8<G, SF16, STAT, ZF, false, true, true>(g, blocks, stream)
-                              : launch8<G, SF16, STAT, ZF, false, false, true>(g, blocks, stream);
+        if (dbg) return split ? launch8<G, 2, SF16, STAT, ZF, false, true, true>(g, blocks, stream)
+                              : launch8<G, 2, SF16, STAT, ZF, false, false, true>(g, blocks, stream);
     }
-    return split ? launch8<G, SF16, STAT, ZF, GELU, true, false>(g, blocks, stream)
-                 : launch8<G, SF16, STAT, ZF, GELU, false, false>(g, blocks, stream);
+    return split ? launch8<G, 2, SF16, STAT, ZF, GELU, true, false>(g, blocks, stream)
+                 : launch8<G, 2, SF16, STAT, ZF, GELU, false, false>(g, blocks, stream);
 }
 template <int G, bool SF16, bool STAT, bool ZF>
-hipError_t launch8_gelu(const Gemm8Args& g, unsigned blocks, bool gelu, bool split, bool dbg, hipStream_t stream) {
-    if constexpr (G == 128) {  // the gate/up pairing serves g = 128 weights
+hipError_t launch8_gelu(const Gemm8Args& g, unsigned blocks, bool gelu, bool split, bool dbg, bool rb1, hipStream_t stream) {
+    if constexpr (G == 128) {  // the gate/up pairing and the 128-row tile serve g = 128 weights
         if (gelu) return launch8_split<G, SF16, STAT, ZF, true>(g, blocks, split, dbg, stream);
+        if (rb1) return dbg ? launch8<G, 1, SF16, STAT, ZF, false, false, true>(g, blocks, stream)
+                            : launch8<G, 1, SF16, STAT, ZF, false, false, false>(g, blocks, stream);
     }
     return launch8_split<G, SF16, STAT, ZF, false>(g, blocks, split, dbg, stream);
 }
 template <int G>
 hipError_t launch8_modes(const Gemm8Args& g, unsigned blocks, bool sf16, bool stat, bool zf, bool gelu, bool split, bool dbg,
-                         hipStream_t stream) {
+                         bool rb1, hipStream_t stream) {
     if (sf16) {
-        if (stat) return launch8_gelu<G, true, true, false>(g, blocks, gelu, split, dbg, stream);
-        if (zf) return launch8_gelu<G, true, false, true>(g, blocks, gelu, split, dbg, stream);
-        return launch8_gelu<G, true, false, false>(g, blocks, gelu, split, dbg, stream);
+        if (stat) return launch8_gelu<G, true, true, false>(g, blocks, gelu, split, dbg, rb1, stream);
+        if (zf) return launch8_gelu<G, true, false, true>(g, blocks, gelu, split, dbg, rb1, stream);
+        return launch8_gelu<G, true, false, false>(g, blocks, gelu, split, dbg, rb1, stream);
     }
-    if (stat) return launch8_gelu<G, false, true, false>(g, blocks, gelu, split, dbg, stream);
-    if (zf) return launch8_gelu<G, false, false, true>(g, blocks, gelu, split, dbg, stream);
-    return launch8_gelu<G, false, false, false>(g, blocks, gelu, split, dbg, stream);
+    if (stat) return launch8_gelu<G, false, true, false>(g, blocks, gelu, split, dbg, rb1, stream);
+    if (zf) return launch8_gelu<G, false, false, true>(g, blocks, gelu, split, dbg, rb1, stream);
+    return launch8_gelu<G, false, false, false>(g, blocks, gelu, split, dbg, rb1, stream);
 }
 template <int G>
 void launch_quantize8(const QRow8Args& q, bool stat, bool f32, bool norm, hipStream_t stream) {
@@ -1119,9 +1163,10 @@ hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t 
     const int total = p.m_blocks * p.n_blocks * p.ksplit;
     const unsigned blocks = static_cast<unsigned>(std::min(total, device_cus()));  // persistent: items loop in the kernel
     hipError_t e;
-    if (G == 128) e = launch8_modes<128>(g, blocks, sf16, stat, zf, c.gelu_gate, split, dbg, stream);
-    else if (G == 64) e = launch8_modes<64>(g, blocks, sf16, stat, zf, false, split, dbg, stream);
-    else e = launch8_modes<32>(g, blocks, sf16, stat, zf, false, split, dbg, stream);
+    const bool rb1 = p.rb == 1;
+    if (G == 128) e = launch8_modes<128>(g, blocks, sf16, stat, zf, c.gelu_gate, split, dbg, rb1, stream);
+    else if (G == 64) e = launch8_modes<64>(g, blocks, sf16, stat, zf, false, split, dbg, false, stream);
+    else e = launch8_modes<32>(g, blocks, sf16, stat, zf, false, split, dbg, false, stream);
     if (e != hipSuccess || !split) return e;
     const unsigned tiles = static_cast<unsigned>(p.m_blocks * p.n_blocks);
     if (stat) {

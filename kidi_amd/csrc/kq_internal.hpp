@@ -171,6 +171,7 @@ int set_error(int code, const char* message);
 // then the int8 GEMM on v_mfma_i32_32x32x32_i8 (K split in ranges with a reduction when the grid is small).
 struct Gemm8Plan {
     int m_blocks = 0, n_blocks = 0, ksplit = 1;
+    int rb = 2;  // 32-row blocks per wave: 2 (256-row tiles) or 1 (128-row tiles, plain g = 128 projections)
 };
 bool gemm8_eligible(const Weight& w);  // the geometry a prefill copy is built for
 Gemm8Plan gemm8_plan(const Weight& w, std::int64_t M, bool gelu);

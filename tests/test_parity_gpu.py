@@ -99,6 +99,10 @@ CASES = [
     (4, 128, 17, 2048, 128, None, 0.05, False, 0.0),
     (4, 128, 64, 512, 1040, "zp", 0.0, True, 0.0),
     (4, 128, 260, 1536, 144, "zp", 0.0, False, 0.001),
+    # 128-row tiles (fewer 256-row tiles than CUs): ragged M and N, calibrated inputs, float zeros
+    (4, 128, 300, 1024, 2048, "zp", 0.0, True, 0.001),
+    (4, 128, 250, 512, 2052, None, 0.05, False, 0.0),
+    (4, 128, 129, 512, 2560, "f16", 0.0, True, 0.0),
     # split K (2 or 4 ranges per output tile, summed in range order by a reduction kernel)
     (4, 128, 64, 4096, 256, "zp", 0.0, True, 0.0),
     (4, 128, 300, 8192, 256, None, 0.0, False, 0.001),
