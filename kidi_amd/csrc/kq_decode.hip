@@ -550,7 +550,18 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
 #pragma unroll
         for (int h = 0; h < (GELU ? 2 : 1); ++h) {
             const int rr = GELU ? h : r;
-            for (int w = 0; w < W; ++w) v[h] = v[h] + red[((w * RT + rr) * MR + i) * 16 + c];
+            if (W % 4 == 0) {
+                // four waves' partials per LDS round trip, added in wave order
+                for (int w = 0; w < W; w += 4) {
+                    float part[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) part[j] = red[(((w + j) * RT + rr) * MR + i) * 16 + c];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) v[h] = v[h] + part[j];
+                }
+            } else {
+                for (int w = 0; w < W; ++w) v[h] = v[h] + red[((w * RT + rr) * MR + i) * 16 + c];
+            }
             if (QM == QUANT_STATIC) v[h] = v[h] * a.input_scale;
             v[h] = calibrate_output(v[h], a.output_scale);
         }

@@ -64,6 +64,8 @@ class PackedWeight:
 class DeviceWeight:
     """A packed weight re-laid out for gfx950 and resident in HBM (kq_weight)."""
 
+    _free = None  # kq_weight_free, bound when the first weight is created
+
     def __init__(self, values, scales, bits: int, group_size: int, zeros=None, concat=None):
         lib = N.load()
         parts = concat if concat is not None else [(values, scales, zeros)]
@@ -104,6 +106,8 @@ class DeviceWeight:
         self._keep = None
         _raise(status)
         self.handle = handle
+        if DeviceWeight._free is None:
+            DeviceWeight._free = N.load().kq_weight_free
         self.bits, self.group_size, self.rows = bits, group_size, rows
         self.cols = descs[0].cols
         self.has_zeros = parts[0][2] is not None
@@ -113,6 +117,8 @@ class DeviceWeight:
         """Adopt a kq_weight (e.g. one kq_weight_import made); the object frees it."""
         self = cls.__new__(cls)
         self.handle = handle
+        if DeviceWeight._free is None:
+            DeviceWeight._free = N.load().kq_weight_free
         b, g, r, c, z = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int32()
         _raise(N.load().kq_weight_info(handle, ctypes.byref(b), ctypes.byref(g), ctypes.byref(r), ctypes.byref(c),
                                        ctypes.byref(z), None))
@@ -138,7 +144,10 @@ class DeviceWeight:
     def __del__(self):
         h = getattr(self, "handle", None)
         if h is not None and h.value:
-            N.load().kq_weight_free(h)
+            # the library's free routine is taken from the class attribute bound at first use, so it stays callable
+            # while the interpreter tears modules down
+            free = type(self)._free or N.load().kq_weight_free
+            free(h)
             self.handle = None
 
     def path(self, input_scale: float) -> int:
