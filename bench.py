@@ -55,6 +55,9 @@ def parse():
     p.add_argument("--floor-sweep", action="store_true",
                    help="print the single-launch read floor and empty-launch cost over launch geometries "
                         "(kq_debug_read_floor_shape) as a table and exit")
+    p.add_argument("--prefill-workload", choices=("configs2", "qkv"), default=None,
+                   help="run one prefill projection ten times, eagerly, and exit (for rocprofv3 --pmc passes): "
+                        "configs2 = M=2048 K=2048 N=8192 asym int4 g=128, qkv = M=2048 K=2048 N=2560 sym int4 g=32")
     p.add_argument("--pmc-workload", action="store_true",
                    help="run the HBM-traffic workload for rocprofv3 --pmc passes (a plain 256 MiB copy for calibration, "
                         "then every rotated decode projection twice, one launch each, no graphs) and exit")
@@ -293,6 +296,19 @@ def main():
     stream_ptr = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     if args.floor_sweep:
         floor_sweep(torch, lib, dev, gen, args)
+        return
+    if args.prefill_workload:
+        N = N_PRE if args.prefill_workload == "configs2" else 2560
+        g = G_PRE if args.prefill_workload == "configs2" else 32
+        values = torch.randint(0, 256, (N, K_PRE // 2), dtype=torch.uint8, device=dev, generator=gen)
+        scales = (torch.rand((N, K_PRE // g), device=dev, generator=gen) * 0.018 + 0.002).to(torch.float16)
+        zp = torch.randint(0, 16, (N, K_PRE // g), dtype=torch.uint8, device=dev, generator=gen) \
+            if args.prefill_workload == "configs2" else None
+        proj = Projection(torch, N_, lib, values, scales, zp, K_PRE, g, M_PRE, make_x(torch, dev, gen, M_PRE, K_PRE), dev)
+        for _ in range(10):
+            proj(stream_ptr())
+        torch.cuda.synchronize()
+        print(f"prefill workload {args.prefill_workload} done", flush=True)
         return
 
     if args.pmc_workload:
