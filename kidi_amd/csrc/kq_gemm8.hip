@@ -568,10 +568,10 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     // part 0: activation fragments [0, CH / 2) of the wave's row block (RB = 1: its half of the chunks), part 1 (RB =
     // 2): [CH / 2, CH), part 2: weight fragments and metadata
     const int arb = RB == 2 ? wave : wave >> 1, ack = RB == 2 ? 0 : (CH / 2) * (wave & 1);
-    auto issue_copy = [&](const Copy& cp, int u, int t, auto part) __attribute__((always_inline)) {
+    // st: byte offset of the target stage; kc0: the step's first 32-column chunk
+    auto issue_copy = [&](const Copy& cp, std::uint32_t st, std::uint32_t kc0, int t, auto part) __attribute__((always_inline)) {
         constexpr int pt = decltype(part)::value;
-        const std::uint32_t kc0 = static_cast<std::uint32_t>((cp.kbase + t) * CH);
-        std::uint8_t* base = lds + (u % NS) * Q::kStageBytes;
+        std::uint8_t* base = lds + st;
         if constexpr (pt < 2) {
             if constexpr (RB == 2 || pt == 0) {
                 const __amdgpu_buffer_rsrc_t ares = rsrc(cp.abase, static_cast<std::uint32_t>(TM / 32) * KC * 1024);
@@ -590,26 +590,28 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_void*)md, 16, lane * 16, cp.meta0 + static_cast<std::uint32_t>(t) * meta_step, 0, 0);
         }
     };
-    // issue(u, r, t): the copies of step t of item r into stage u % NS; t may run past the item (the next items' steps),
-    // and past the last item the item's last step is copied again, into a stage nothing reads any more. item_copy holds
-    // the copy parameters of the item being computed.
+    // issue(st, r, t): the copies of step t of item r into the stage at byte offset st; t may run past the item (the
+    // next items' steps), and past the last item the item's last step is copied again, into a stage nothing reads any
+    // more. item_copy holds the copy parameters of the item being computed. The scalar work is done once per step (not
+    // per part), and the item-boundary path runs only in the last NS steps of an item.
     Copy item_copy = copy_of(0);
-    auto issue_part = [&](int u, int r, int t, auto part) __attribute__((always_inline)) {
+    auto issue_all = [&](const Copy& cp, std::uint32_t st, int t) __attribute__((always_inline)) {
+        const std::uint32_t kc0 = static_cast<std::uint32_t>((cp.kbase + t) * CH);
+        issue_copy(cp, st, kc0, t, std::integral_constant<int, 0>{});
+        issue_copy(cp, st, kc0, t, std::integral_constant<int, 1>{});
+        issue_copy(cp, st, kc0, t, std::integral_constant<int, 2>{});
+    };
+    auto issue = [&](std::uint32_t st, int r, int t) __attribute__((always_inline)) {
         if (t < steps) {
-            issue_copy(item_copy, u, t, part);
+            issue_all(item_copy, st, t);
             return;
         }
         while (t >= steps) {
             t -= steps;
             ++r;
         }
-        if (r >= items) issue_copy(item_copy, u, steps - 1, part);
-        else issue_copy(copy_of(r), u, t, part);
-    };
-    auto issue = [&](int u, int r, int t) __attribute__((always_inline)) {
-        issue_part(u, r, t, std::integral_constant<int, 0>{});
-        issue_part(u, r, t, std::integral_constant<int, 1>{});
-        issue_part(u, r, t, std::integral_constant<int, 2>{});
+        if (r >= items) issue_all(item_copy, st, steps - 1);
+        else issue_all(copy_of(r), st, t);
     };
 
     // ---- the wave's fragments: row blocks RB wm + i; column blocks (plain) 2 wn + i, (GELU) wn + 2 i
@@ -723,7 +725,7 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
 
     // prologue: NS stages in flight; step 0's operands (but A row block 1) and metadata in registers
 #pragma unroll
-    for (int i = 0; i < NS; ++i) issue(i, 0, i);
+    for (int i = 0; i < NS; ++i) issue(static_cast<std::uint32_t>(i * Q::kStageBytes), 0, i);
     KQ_ASM("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     read_frags(A[0], a_lane);
     read_frags(B0, b_lane0);
@@ -740,14 +742,14 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     //   stage t.
     // Stage t % NS is read from b2 of step t - 1 to b0 of step t; the mid-step barrier of step t comes after every
     // wave waited for those reads, and after every wave's copies of step t + 1 (issued at mid-step t + 1 - NS) landed.
-    auto step_body = [&](int t, int u, int r, auto parity, bool wide) __attribute__((always_inline)) {
+    // st_now: byte offset of stage u % NS (u: the global step), st_next: of stage (u + 1) % NS; the copies of step
+    // t + NS go into stage u % NS as well
+    auto step_body = [&](int t, std::uint32_t st_now, std::uint32_t st_next, int r, auto parity, bool wide) __attribute__((always_inline)) {
         constexpr int p = decltype(parity)::value;
         Meta<GPS>& cur = mt[p];
         Meta<GPS>& prv = mt[p ^ 1];
         v4i (&Bc)[CH] = B1[p];
         v4i (&Bn)[CH] = B1[p ^ 1];
-        const std::uint32_t st_now = static_cast<std::uint32_t>((u % NS) * Q::kStageBytes);
-        const std::uint32_t st_next = static_cast<std::uint32_t>(((u + 1) % NS) * Q::kStageBytes);
         const int g = (ks * steps + t) * GPS;  // global index of the step's first group
         const std::uint32_t dvo_prev = t > 0 ? dvo[RB - 1][1] : 0x80000000u;
         auto mid_step = [&]() __attribute__((always_inline)) {
@@ -756,7 +758,7 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             // (vmcnt counts to 63: a larger allowance waits for some of the stores too, which is only stricter)
             if (wide) KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(min63((NS - 2) * Q::kCopies + kStoresAfter)) : "memory");
             else KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * Q::kCopies) : "memory");
-            issue(u + NS, r, t + NS);
+            issue(st_now, r, t + NS);
         };
         lgkm_wait<0>(A[0], B0, Bc, cur.rec, cur.z, cur.as, cur.az);  // step t's operands and metadata (read during step t - 1)
         if constexpr (RB == 1) {
@@ -880,12 +882,20 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[0], cur.rec[1][0], cur.z[1][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][1], g);
         }
     };
-    int u = 0;  // global step: stage u % NS
+    // byte offset of stage u % NS for the global step u, advanced step by step
+    constexpr std::uint32_t kRing = static_cast<std::uint32_t>(NS * Q::kStageBytes);
+    auto next_stage = [](std::uint32_t st) __attribute__((always_inline)) {
+        const std::uint32_t n = st + static_cast<std::uint32_t>(Q::kStageBytes);
+        return n == kRing ? 0u : n;
+    };
+    std::uint32_t st0 = 0;
     for (int r = 0; r < items; ++r) {
         begin_item(r);
-        for (int t = 0; t < steps; t += 2, u += 2) {
-            step_body(t, u, r, std::integral_constant<int, 0>{}, r > 0 && t <= NS - 2);
-            step_body(t + 1, u + 1, r, std::integral_constant<int, 1>{}, r > 0 && t + 1 <= NS - 2);
+        for (int t = 0; t < steps; t += 2) {
+            const std::uint32_t st1 = next_stage(st0), st2 = next_stage(st1);
+            step_body(t, st0, st1, r, std::integral_constant<int, 0>{}, r > 0 && t <= NS - 2);
+            step_body(t + 1, st1, st2, r, std::integral_constant<int, 1>{}, r > 0 && t + 1 <= NS - 2);
+            st0 = st2;
         }
         // the reads issued in the last step (the next item's step 0 operands and metadata) land before the registers
         // they target can be given to anything else (after the last item nothing reads them)
