@@ -149,6 +149,31 @@ def timed(torch, quiet, enqueue):
     return e0.elapsed_time(e1)
 
 
+def mfma_ceiling(torch, lib, dev, quiet, stream_ptr, iters=4096):
+    """Sustained int8 MFMA rate of the whole chip (kq_debug_mfma_ceiling: one 8-wave workgroup per CU, two waves per
+    SIMD, only v_mfma_i32_32x32x32_i8 in independent chains, ~1 ms per launch): TOP/s, its fraction of the published
+    dense figure (2.4 GHz x 1024 SIMDs x 65,536 operations per 32-cycle MFMA), and the shader clock that rate implies
+    at 32 cycles per MFMA and SIMD. (The waves' s_memtime counts are not used: that counter does not run at the
+    shader clock on gfx950.)"""
+    wgs = int(lib.kq_debug_mfma_ceiling_workgroups())
+    cycles = torch.zeros((wgs * 8,), dtype=torch.int64, device=dev)
+    sink = torch.zeros((wgs * 8,), dtype=torch.int32, device=dev)
+
+    def run():
+        _ok(lib, lib.kq_debug_mfma_ceiling(iters, cycles.data_ptr(), sink.data_ptr(), stream_ptr()))
+
+    run()
+    torch.cuda.synchronize()
+    ms = min(timed(torch, quiet, run) for _ in range(3))
+    ops = wgs * 8 * iters * 8 * 65536
+    tops = ops / (ms * 1e-3) / 1e12
+    return {"tops": round(tops, 1), "frac_of_peak": round(tops / INT8_PEAK_TOPS, 4),
+            "implied_clock_ghz": round(tops * 1e12 / (wgs * 4 * 65536 / 32) / 1e9, 3),
+            "us_per_launch": round(ms * 1e3, 1),
+            "how": f"kq_debug_mfma_ceiling: {wgs} workgroups x 8 waves, {iters} x 8 independent 32x32x32 int8 MFMAs "
+                   "per wave, nothing else; best of three launches"}
+
+
 def run_steps(torch, projs, start, count, graph_full, graph_rem_fn, stream_ptr_fn):
     """Run `count` projections starting at rotation index `start` (a multiple of len(projs)): whole rotations as
     graph replays, the remainder as one graph of the first count % R projections."""
@@ -457,6 +482,10 @@ def main():
     pre_ok = pre_err <= 2e-3 * float(np.max(np.abs(y_ref)))
     del gp, pre, pre2
 
+    # ---------------- sustained int8 MFMA rate (the ceiling the prefill figure is read against) ----------------
+    ceiling = mfma_ceiling(torch, lib, dev, quiet, stream_ptr)
+    ceiling["prefill_vs_ceiling"] = round(pre_tops / ceiling["tops"], 4)
+
     # ---------------- CPU baseline ----------------
     cpu = None
     if args.cpu_seconds > 0:
@@ -499,6 +528,7 @@ def main():
                     "ms": round(pre_ms, 5), "tops": round(pre_tops, 2),
                     "mfma_frac": round(pre_tops / INT8_PEAK_TOPS, 4), "parity_ok": bool(pre_ok),
                     "max_abs_err": pre_err},
+        "mfma_ceiling": ceiling,
         "cpu_baseline": cpu,
         "extras": extras,
     }

@@ -308,6 +308,15 @@ kq_status kq_debug_read_floor(const void* data, size_t bytes, int32_t* sink, voi
 kq_status kq_debug_read_floor_shape(const void* data, size_t bytes, int32_t threads, int32_t loads, int32_t empty,
                                     int32_t* sink, void* stream);
 
+/* The sustained int8 MFMA rate of the device: one launch of kq_debug_mfma_ceiling_workgroups() workgroups (one per
+ * compute unit) of 8 waves, as the prefill GEMM, each wave issuing `iterations` (1 to 2^24) rounds of eight
+ * independent v_mfma_i32_32x32x32_i8 (65,536 int8 operations each) and nothing else. `cycles` (device, one int64 per
+ * wave: workgroups x 8) receives each wave's s_memtime count over its loop (a timestamp counter, not the shader
+ * clock), `sink` (device, int32, same count) a value that keeps the MFMAs live. Operations per launch: workgroups x 8
+ * x iterations x 8 x 65,536; the rate follows from the launch's device time. */
+int32_t kq_debug_mfma_ceiling_workgroups(void);
+kq_status kq_debug_mfma_ceiling(int32_t iterations, int64_t* cycles, int32_t* sink, void* stream);
+
 /* Host-only (no GPU): the gfx950 tile layout of a Kidi-layout weight and its inverse, for layout tests. */
 size_t kq_layout_bytes(int32_t bits, int32_t group_size, int64_t rows, int64_t cols);
 kq_status kq_layout_encode_host(int32_t bits, int64_t rows, int64_t cols, const uint8_t* values, uint8_t* tiles);

@@ -28,6 +28,7 @@ EXPORTS = (
     "kq_greedy_workspace_size", "kq_greedy_token", "kq_greedy_linear_workspace_size", "kq_packed_linear_greedy",
     "kq_weight_export_size", "kq_weight_export", "kq_weight_import", "kq_rms_norm", "kq_rms_linear_workspace_size",
     "kq_packed_linear_rms", "kq_quantize_weight", "kq_debug_read_floor", "kq_debug_read_floor_shape",
+    "kq_debug_mfma_ceiling_workgroups", "kq_debug_mfma_ceiling",
     "kq_debug_route", "kq_debug_route_shape",
     "kq_lowbit_parity_linear", "kq_packed_linear_noalloc", "kq_gelu_multiply", "kq_silu_multiply",
 )
@@ -183,6 +184,10 @@ def load() -> ctypes.CDLL:
     L.kq_debug_read_floor.restype = ctypes.c_int
     L.kq_debug_read_floor_shape.argtypes = [vp, ctypes.c_size_t, i32, i32, i32, vp, vp]
     L.kq_debug_read_floor_shape.restype = ctypes.c_int
+    L.kq_debug_mfma_ceiling_workgroups.argtypes = []
+    L.kq_debug_mfma_ceiling_workgroups.restype = ctypes.c_int32
+    L.kq_debug_mfma_ceiling.argtypes = [i32, vp, vp, vp]
+    L.kq_debug_mfma_ceiling.restype = ctypes.c_int
     L.kq_packed_linear_noalloc.argtypes = [vp, ctypes.POINTER(LinearArgs), vp]
     L.kq_packed_linear_noalloc.restype = ctypes.c_int
     L.kq_lowbit_parity_linear.argtypes = [vp, ctypes.POINTER(LinearArgs), vp]

@@ -1366,6 +1366,17 @@ kq_status kq_debug_read_floor_shape(const void* data, size_t bytes, int32_t thre
     return KQ_OK;
 }
 
+int32_t kq_debug_mfma_ceiling_workgroups(void) { return kq::mfma_ceiling_workgroups(); }
+
+kq_status kq_debug_mfma_ceiling(int32_t iterations, int64_t* cycles, int32_t* sink, void* stream) {
+    if (!cycles || !sink || iterations <= 0 || iterations > (1 << 24))
+        return fail(KQ_INVALID_ARGUMENT, "mfma ceiling: device cycles and sink buffers, 1 to 2^24 iterations");
+    if (hipError_t e = kq::launch_mfma_ceiling(iterations, reinterpret_cast<long long*>(cycles), sink, static_cast<hipStream_t>(stream));
+        e != hipSuccess)
+        return hip_fail(e, "mfma ceiling launch");
+    return KQ_OK;
+}
+
 size_t kq_layout_bytes(int32_t bits, int32_t group_size, int64_t rows, int64_t cols) {
     if ((bits != 2 && bits != 4 && bits != 8) || rows <= 0 || cols <= 0) return 0;
     return static_cast<size_t>(kq::Geometry::make(bits, group_size, rows, cols).tile_bytes_total());

@@ -982,6 +982,37 @@ __global__ __launch_bounds__(kThreads) void gemm8_reduce_kernel(Gemm8Args a) {
     else store8d<STAT>(a, acc, mb * kBM, wm, gc, lane);
 }
 
+// Measurement: the sustained int8 MFMA rate of the whole chip. Every wave of a fully resident grid (one 8-wave
+// workgroup per CU, two waves per SIMD, as gemm8_kernel) issues `iters` rounds of eight independent
+// v_mfma_i32_32x32x32_i8 chains (each chain's next MFMA is eight MFMAs later, so no round waits on a result) and
+// nothing else; lane 0 of each wave stores its s_memtime count over the loop and the accumulators' sum, so nothing is
+// dead code.
+__global__ __launch_bounds__(kThreads) void mfma_ceiling_kernel(int iters, long long* cycles, int* sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const v4i A = v4i{lane, lane + 1, lane + 2, lane + 3}, B = v4i{3 * lane, 1, 2, lane};
+    v16i C[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int k = 0; k < 16; ++k) C[j][k] = j + k;
+    const long long t0 = __builtin_amdgcn_s_memtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mfma_acc(C[j], A, B);
+    }
+    KQ_ASM("s_nop 15\n\ts_nop 15" ::: "memory");  // the last results written before they are read
+    const long long t1 = __builtin_amdgcn_s_memtime();
+    int r = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int k = 0; k < 16; ++k) r += C[j][k];
+    if (lane == 0) {
+        cycles[blockIdx.x * kWaves + wave] = t1 - t0;
+        sink[blockIdx.x * kWaves + wave] = r;
+    }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -1186,6 +1217,13 @@ hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t 
         if (c.gelu_gate) hipLaunchKernelGGL((gemm8_reduce_kernel<false, true>), dim3(tiles), dim3(kThreads), 0, stream, g);
         else hipLaunchKernelGGL((gemm8_reduce_kernel<false, false>), dim3(tiles), dim3(kThreads), 0, stream, g);
     }
+    return hipGetLastError();
+}
+
+int mfma_ceiling_workgroups() { return device_cus(); }
+
+hipError_t launch_mfma_ceiling(int iters, long long* cycles, int* sink, hipStream_t stream) {
+    hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(static_cast<unsigned>(device_cus())), dim3(kThreads), 0, stream, iters, cycles, sink);
     return hipGetLastError();
 }
 

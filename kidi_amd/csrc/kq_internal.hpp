@@ -177,6 +177,10 @@ bool gemm8_eligible(const Weight& w);  // the geometry a prefill copy is built f
 Gemm8Plan gemm8_plan(const Weight& w, std::int64_t M, bool gelu);
 bool gemm8_fits(const LinearCall& c);
 std::size_t gemm8_partial_bytes(const Weight& w, std::int64_t M, bool gelu);
+// measurement: one 8-wave workgroup per CU issuing only int8 MFMAs (8 chains x iters per wave); cycles[wg * 8 + wave]
+// receives each wave's s_memtime count, sink a value that keeps the MFMAs live
+int mfma_ceiling_workgroups();
+hipError_t launch_mfma_ceiling(int iters, long long* cycles, int* sink, hipStream_t stream);
 // quantize_only: the row quantizer alone (with its parity dumps when d_codes / d_scales / d_sums are set)
 hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t stream, bool quantize_only = false,
                         std::int8_t* d_codes = nullptr, float* d_scales = nullptr, std::int32_t* d_sums = nullptr);
