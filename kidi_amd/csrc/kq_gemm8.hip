@@ -811,6 +811,7 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             mfma_first(P[0], A[1][0], B0[0], bias);
             read_frags(Bn, b_lane1 + st_next);
             read_meta(prv, st_next);
+            read_frags(A[0], a_lane + st_next);  // A row block 0 is free since b1
             mfma_acc(P[0], A[1][1], B0[1]);
             epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
             mfma_acc(P[0], A[1][2], B0[2]);
@@ -819,7 +820,6 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
             // ---- b3
             mfma_first(P[1], A[1][0], Bc[0], bias);
-            read_frags(A[0], a_lane + st_next);
             read_frags(B0, b_lane0 + st_next);
             mfma_acc(P[1], A[1][1], Bc[1]);
             epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
