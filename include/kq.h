@@ -288,7 +288,8 @@ kq_status kq_debug_partials(const kq_weight* weight, const kq_linear_args* args,
  * assert which kernels they cover): 0 none (M = 0), 1 decode_kernel, 2 skinny_kernel, 3 quantize_rows_kernel +
  * gemm_i4_kernel, 4 quantize_rows_g_kernel + gemm_i4g_kernel, 5 quantize_kernel + gemv_kernel, 6 quantize_kernel +
  * gemm_kernel, 7 quantize_rowmajor_kernel + rowmajor_kernel, 8 portable_kernel, 9 quantize_rows8_kernel + gemm8_kernel
- * (from the weight's prefill copy); -1 for invalid arguments.
+ * (from the weight's prefill copy), 10 quantize_rows8_kernel + gemm8w_kernel (the same copy, g = 32 in 128 x 160
+ * tiles where 256 x 128 tiles leave compute units idle); -1 for invalid arguments.
  * kq_debug_route_shape answers for a weight described by its geometry and modes (zero_mode: 0 none, 1 ZP_U8 zero
  * points or additive zeros equal to (8 - zp) * scale, 2 other additive zeros) and touches no device. */
 int32_t kq_debug_route(const kq_weight* weight, const kq_linear_args* args, int32_t gelu_gate);

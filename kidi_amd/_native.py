@@ -35,9 +35,9 @@ EXPORTS = (
 
 # kq_debug_route values: the kernel sequence a projection call runs
 ROUTE_NONE, ROUTE_DECODE, ROUTE_SKINNY, ROUTE_GEMM_I4, ROUTE_GEMM_I4G, ROUTE_GEMV, ROUTE_GEMM, ROUTE_ROWMAJOR, \
-    ROUTE_PORTABLE, ROUTE_GEMM8 = range(10)
+    ROUTE_PORTABLE, ROUTE_GEMM8, ROUTE_GEMM8W = range(11)
 ROUTE_NAMES = ("none", "decode_kernel", "skinny_kernel", "gemm_i4_kernel", "gemm_i4g_kernel", "gemv_kernel",
-               "gemm_kernel", "rowmajor_kernel", "portable_kernel", "gemm8_kernel")
+               "gemm_kernel", "rowmajor_kernel", "portable_kernel", "gemm8_kernel", "gemm8w_kernel")
 
 
 class PackDesc(ctypes.Structure):

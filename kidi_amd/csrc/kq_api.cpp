@@ -495,7 +495,7 @@ kq::Route route_of(const kq::LinearCall& c, kq::SkinnyPlan* plan) {
         if (plan) *plan = p;
         return kq::ROUTE_SKINNY;
     }
-    if (kq::gemm8_fits(c)) return kq::ROUTE_GEMM8;
+    if (kq::gemm8_fits(c)) return kq::gemm8_plan(*c.w, c.M, c.gelu_gate).wide && !c.dump ? kq::ROUTE_GEMM8W : kq::ROUTE_GEMM8;
     if (kq::gemm_i4_fits(c)) return kq::ROUTE_GEMM_I4;
     if (kq::gemm_i4g_fits(c)) return kq::ROUTE_GEMM_I4G;
     if (c.path == kq::PATH_PORTABLE) return kq::ROUTE_PORTABLE;
@@ -530,7 +530,7 @@ kq_status run_call(kq::LinearCall& c, const kq_linear_args* args, std::size_t ws
         c.act = kq::carve_workspace(*c.w, c.M, ws);
     }
     // Prefill, 4-bit g = 128 from the weight's prefill copy: quantizer + int8 GEMM (GELU gate fused).
-    if (route == kq::ROUTE_GEMM8) {
+    if (route == kq::ROUTE_GEMM8 || route == kq::ROUTE_GEMM8W) {
         e = kq::launch_gemm8(c, c.act, stream);
         return e == hipSuccess ? KQ_OK : hip_fail(e, "prefill projection launch");
     }

@@ -982,6 +982,318 @@ __global__ __launch_bounds__(kThreads) void gemm8_reduce_kernel(Gemm8Args a) {
     else store8d<STAT>(a, acc, mb * kBM, wm, gc, lane);
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// 128 x 160 tiles for g = 32 (gemm8w_kernel)
+//
+// A g = 32 projection is bound by its epilogue's VALU (two instructions per element and group, one group per MFMA),
+// so its time follows the blocks a SIMD carries. Where 256 x 128 tiles leave CUs idle (the fused QKV at M = 2048,
+// N = 2560: 160 tiles), 128 x 160 tiles cover the chip (256 tiles): 8 waves, wave w takes row block w % 4 and column
+// blocks 0-2 (w < 4) or 3-4 (w >= 4), so the two waves of a SIMD carry five 32 x 32 blocks per k step against eight.
+// One 64-column k step (two groups) per iteration; a 4-stage ring of 26 KiB stages filled by direct copies only,
+// exactly four per wave and step: copy c = w + 8 j (j = 0..3) is activation fragment c (c < 8: row block c / 2, chunk
+// c % 2), weight fragment c - 8 (c < 18: column block (c - 8) / 2), the activation scales of group c - 18 (c < 20),
+// a 1 KiB run of weight records (c < 26: group (c - 20) / 3, column blocks 2 ((c - 20) % 3) and the next), or a
+// dummy. Operands of step t + 1 are read during step t: the activation fragments and the last block's weight
+// fragments into a second register set (by step parity), the other blocks' weight fragments as soon as their block's
+// MFMAs are issued. Epilogue, stores and numerics are gemm8_kernel's (same operation order per element: y is
+// bit-identical).
+struct GeoW {
+    static constexpr int kAOff = 0;                           // [4 row blocks][2 chunks][1 KiB]
+    static constexpr int kBOff = kAOff + 8 * 1024;            // [5 column blocks][2 chunks][1 KiB]
+    static constexpr int kSOff = kBOff + 10 * 1024;           // [2 groups][256 rows][4 B] (rows 0..127 used)
+    static constexpr int kWOff = kSOff + 2 * 1024;            // [2 groups][6 column blocks][32][16 B] (block 5 unused)
+    static constexpr int kStageBytes = kWOff + 2 * 3 * 1024;  // 26 KiB
+    static constexpr int kStages = 4;
+    static constexpr int kDummyOff = kStages * kStageBytes;
+    static constexpr int kLds = kDummyOff + 1024;             // 105 KiB
+    static constexpr int kCopies = 4;                         // direct copies per wave and step
+};
+// One copy slot of a wave for one item: source, byte offset at step 0 and per step, LDS offset within a stage (or,
+// stage_mask 0, within the whole allocation: the dummy area).
+struct SlotW {
+    __amdgpu_buffer_rsrc_t res;
+    std::uint32_t off0, inc, lds, stage_mask;
+};
+template <int NC>
+struct MetaW {  // one k step's epilogue operands: weight records of the wave's NC column blocks, a_s of its rows
+    v2i rec[NC][2];
+    float as[2];
+};
+
+// Final values of a wave's NC blocks (row block wm, global column blocks gc[]), 4-byte stores as store8d: 16 per
+// block and lane.
+template <bool STAT, int NC>
+__device__ __forceinline__ void store8w(const Gemm8Args& a, const float (&acc)[NC][16], int m0, int wm, const int (&gc)[NC], int lane) {
+    const int n_out = a.N;
+    const int rows = min(a.M - m0, 128);
+    const __amdgpu_buffer_rsrc_t yres = rsrc(a.y + static_cast<std::int64_t>(m0) * n_out, static_cast<std::uint32_t>(rows) * n_out * 4);
+    const std::uint32_t row_bytes = static_cast<std::uint32_t>(n_out) * 4;
+    const bool cal = a.output_scale > 0.F;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int n = 32 * gc[c] + (lane & 31);
+        const std::uint32_t col_off = n < n_out ? static_cast<std::uint32_t>(n) * 4 : 0x80000000u;
+        const std::uint32_t base = col_off + static_cast<std::uint32_t>(32 * wm + 4 * (lane >> 5)) * row_bytes;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            float x = acc[c][k];
+            if (STAT) x = x * a.input_scale;
+            if (cal) x = calibrate_output(x, a.output_scale);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), yres, base + static_cast<std::uint32_t>(8 * (k >> 2) + (k & 3)) * row_bytes,
+                                                  0, 0);
+        }
+    }
+}
+
+// The body of gemm8w_kernel for a wave of NC column blocks (NC = 3: waves 0-3, NC = 2: waves 4-7). Both bodies run
+// the same barriers (one in the prologue, one per step).
+template <int NC, bool SF16, bool STAT>
+__device__ __forceinline__ void gemm8w_body(const Gemm8Args& a, std::uint8_t* lds, int wave, int lane) {
+    using Q = GeoW;
+    constexpr int NS = Q::kStages;
+    constexpr int cb0 = NC == 3 ? 0 : 3;  // the wave's first column block in the tile
+    const int wm = wave & 3;
+    const std::uint32_t lds0 = lds_addr(lds);
+    const int tiles = a.m_blocks * a.n_blocks;
+    const int W = static_cast<int>(gridDim.x);
+    const int bx = static_cast<int>(blockIdx.x);
+    const int items = (tiles - bx + W - 1) / W;
+    const int KC = a.K / 32;
+    const int steps = a.K / 64;
+    auto item_of = [&](int r) __attribute__((always_inline)) {
+        int i = r * W + bx;
+        if (tiles % 8 == 0) i = (i % 8) * (tiles / 8) + i / 8;
+        Item it;
+        it.ks = 0;
+        it.tile = i;
+        it.m0 = (i % a.m_blocks) * 128;
+        it.nbk = i / a.m_blocks;
+        return it;
+    };
+    const std::uint32_t meta_bytes = static_cast<std::uint32_t>(a.groups) * a.NB * 512;
+    auto slot_of = [&](int j, const Item& it) __attribute__((always_inline)) {
+        const int c = wave + 8 * j;
+        SlotW s;
+        s.stage_mask = 0xFFFFFFFFu;
+        if (c < 8) {
+            s.res = rsrc(a.q + static_cast<std::int64_t>(it.m0 / 32) * KC * 1024, 4u * static_cast<std::uint32_t>(KC) * 1024);
+            s.off0 = static_cast<std::uint32_t>((c >> 1) * KC + (c & 1)) * 1024;
+            s.inc = 2048;
+            s.lds = Q::kAOff + c * 1024;
+        } else if (c < 18) {
+            const int f = c - 8, gcb = 5 * it.nbk + (f >> 1);
+            const bool live = gcb < a.NB;
+            s.res = rsrc(a.w + static_cast<std::int64_t>(live ? gcb : 0) * KC * 1024, live ? static_cast<std::uint32_t>(KC) * 1024 : 0u);
+            s.off0 = static_cast<std::uint32_t>(f & 1) * 1024;
+            s.inc = 2048;
+            s.lds = Q::kBOff + f * 1024;
+        } else if (c < 20 && !STAT) {
+            const int gg = c - 18;
+            s.res = rsrc(a.scale_t, static_cast<std::uint32_t>(a.groups) * a.M_p * 4);
+            s.off0 = static_cast<std::uint32_t>(gg * a.M_p + it.m0) * 4;
+            s.inc = static_cast<std::uint32_t>(2 * a.M_p) * 4;
+            s.lds = Q::kSOff + gg * 1024;
+        } else if (c >= 20 && c < 26) {
+            const int gg = (c - 20) / 3, part = (c - 20) % 3;
+            s.res = rsrc(a.wmeta, meta_bytes);
+            s.off0 = static_cast<std::uint32_t>(gg * a.NB + 5 * it.nbk + 2 * part) * 512;
+            s.inc = static_cast<std::uint32_t>(2 * a.NB) * 512;
+            s.lds = Q::kWOff + gg * 3072 + part * 1024;
+        } else {
+            s.res = rsrc(a.wmeta, meta_bytes);
+            s.off0 = 0;
+            s.inc = 0;
+            s.lds = Q::kDummyOff;
+            s.stage_mask = 0;
+        }
+        return s;
+    };
+    auto copy = [&](const SlotW& s, std::uint32_t st, int t) __attribute__((always_inline)) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(s.res, (lds_void*)(lds + (st & s.stage_mask) + s.lds), 16, lane * 16,
+                                                 s.off0 + static_cast<std::uint32_t>(t) * s.inc, 0, 0);
+    };
+    SlotW sl[4];
+    {
+        const Item it0 = item_of(0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sl[j] = slot_of(j, it0);
+    }
+    // issue(st, r, t): the copies of step t of item r into the stage at byte offset st; past the item, the next
+    // item's steps; past the last item, the item's last step again (into a stage nothing reads any more)
+    auto issue = [&](std::uint32_t st, int r, int t) __attribute__((always_inline)) {
+        if (t < steps) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) copy(sl[j], st, t);
+            return;
+        }
+        while (t >= steps) {
+            t -= steps;
+            ++r;
+        }
+        if (r >= items) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) copy(sl[j], st, steps - 1);
+        } else {
+            const Item it = item_of(r);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) copy(slot_of(j, it), st, t);
+        }
+    };
+
+    const int col = lane & 31;
+    const std::uint32_t a_lane = lds0 + Q::kAOff + (wm * 2) * 1024 + lane * 16;
+    const std::uint32_t b_lane = lds0 + Q::kBOff + (cb0 * 2) * 1024 + lane * 16;
+    const std::uint32_t w_lane = lds0 + Q::kWOff + (cb0 * 32 + col) * 16;
+    [[maybe_unused]] const std::uint32_t s_lane = lds0 + Q::kSOff + (32 * wm + bcast_row(lane)) * 4;
+    auto read_meta = [&](MetaW<NC>& m, std::uint32_t stage) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            KQ_ASM("ds_read_b64 %0, %1 offset:%2" : "=v"(m.rec[c][0]) : "v"(w_lane + stage), "n"(c * 512));
+            KQ_ASM("ds_read_b64 %0, %1 offset:%2" : "=v"(m.rec[c][1]) : "v"(w_lane + stage), "n"(3072 + c * 512));
+        }
+        if constexpr (!STAT) {
+            KQ_ASM("ds_read_b32 %0, %1 offset:0" : "=v"(m.as[0]) : "v"(s_lane + stage));
+            KQ_ASM("ds_read_b32 %0, %1 offset:1024" : "=v"(m.as[1]) : "v"(s_lane + stage));
+        }
+    };
+
+    int gc[NC];
+    int m0 = 0;
+    Dump dmp{};
+    constexpr int kStoresAfter = 16 * NC;
+
+    float acc[NC][16];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc[c][k] = 0.F;
+    v16i bias;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) bias[k] = kBiasBits;
+    KQ_ASM("" : "+v"(bias));
+    v16i P[2];
+    P[0] = bias;
+    P[1] = bias;
+    v4i A[2][2], B[NC - 1][2], Bl[2][2];  // A and the last block's B by step parity; the other blocks' B single
+    MetaW<NC> mt[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            mt[1].rec[c][i] = v2i{0, 0};
+        }
+        mt[0].as[i] = 0.F;
+        mt[1].as[i] = 0.F;
+    }
+
+    // prologue: NS stages in flight; step 0's operands in registers
+#pragma unroll
+    for (int i = 0; i < NS; ++i) issue(static_cast<std::uint32_t>(i * Q::kStageBytes), 0, i);
+    KQ_ASM("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    ds_read16<0>(A[0][0], a_lane);
+    ds_read16<1024>(A[0][1], a_lane);
+#pragma unroll
+    for (int c = 0; c < NC - 1; ++c) {
+        ds_read16<0>(B[c][0], b_lane + c * 2048);
+        ds_read16<1024>(B[c][1], b_lane + c * 2048);
+    }
+    ds_read16<(NC - 1) * 2048>(Bl[0][0], b_lane);
+    ds_read16<(NC - 1) * 2048 + 1024>(Bl[0][1], b_lane);
+    read_meta(mt[0], 0);
+
+    // Step t (parity p): units (block c, group g) in the order (0, 0), (0, 1), (1, 0), ...; each unit is one MFMA,
+    // and the epilogue of a unit runs after the next unit's MFMA (the first unit's MFMA is followed by the epilogue of
+    // the previous step's last unit). After unit 1: the mid-step wait and barrier (stage t + 1 complete in every
+    // wave, stage t free), the copies of step t + NS into stage t, then the reads of step t + 1's operands.
+    auto step_body = [&](int t, std::uint32_t st_now, std::uint32_t st_next, int r, auto parity, bool wide) __attribute__((always_inline)) {
+        constexpr int p = decltype(parity)::value;
+        MetaW<NC>& cur = mt[p];
+        MetaW<NC>& prv = mt[p ^ 1];
+        lgkm_wait<0>(A[p], B, Bl[p], cur.rec, cur.as);
+        // ---- block 0
+        mfma_first(P[0], A[p][0], B[0][0], bias);
+        epi_range<0, 16, SF16, STAT, false, false>(acc[NC - 1], P[1], prv.rec[NC - 1][1], 0.F, prv.as[1], 0.F, dmp, 0u, 0);
+        mfma_first(P[1], A[p][1], B[0][1], bias);
+        epi_range<0, 16, SF16, STAT, false, false>(acc[0], P[0], cur.rec[0][0], 0.F, cur.as[0], 0.F, dmp, 0u, 0);
+        if (wide) KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(min63((NS - 2) * Q::kCopies + kStoresAfter)) : "memory");
+        else KQ_ASM("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * Q::kCopies) : "memory");
+        issue(st_now, r, t + NS);
+        ds_read16<0>(A[p ^ 1][0], a_lane + st_next);
+        ds_read16<1024>(A[p ^ 1][1], a_lane + st_next);
+        ds_read16<(NC - 1) * 2048>(Bl[p ^ 1][0], b_lane + st_next);
+        ds_read16<(NC - 1) * 2048 + 1024>(Bl[p ^ 1][1], b_lane + st_next);
+        read_meta(prv, st_next);
+        // ---- block 1 (NC = 2: the last block)
+        const v4i& B10 = NC == 3 ? B[NC == 3 ? 1 : 0][0] : Bl[p][0];
+        const v4i& B11 = NC == 3 ? B[NC == 3 ? 1 : 0][1] : Bl[p][1];
+        mfma_first(P[0], A[p][0], B10, bias);
+        ds_read16<0>(B[0][0], b_lane + st_next);  // block 0's operands are free: its MFMAs were issued before the barrier
+        ds_read16<1024>(B[0][1], b_lane + st_next);
+        epi_range<0, 16, SF16, STAT, false, false>(acc[0], P[1], cur.rec[0][1], 0.F, cur.as[1], 0.F, dmp, 0u, 0);
+        mfma_first(P[1], A[p][1], B11, bias);
+        epi_range<0, 16, SF16, STAT, false, false>(acc[1], P[0], cur.rec[1][0], 0.F, cur.as[0], 0.F, dmp, 0u, 0);
+        if constexpr (NC == 3) {
+            // ---- block 2 (the last block)
+            mfma_first(P[0], A[p][0], Bl[p][0], bias);
+            ds_read16<2048>(B[NC == 3 ? 1 : 0][0], b_lane + st_next);  // block 1's MFMAs were issued 32 VALU ago
+            ds_read16<3072>(B[NC == 3 ? 1 : 0][1], b_lane + st_next);
+            epi_range<0, 16, SF16, STAT, false, false>(acc[1], P[1], cur.rec[1][1], 0.F, cur.as[1], 0.F, dmp, 0u, 0);
+            mfma_first(P[1], A[p][1], Bl[p][1], bias);
+            epi_range<0, 16, SF16, STAT, false, false>(acc[2 < NC ? 2 : 0], P[0], cur.rec[2 < NC ? 2 : 0][0], 0.F, cur.as[0], 0.F, dmp, 0u, 0);
+        }
+    };
+
+    constexpr std::uint32_t kRing = static_cast<std::uint32_t>(NS * Q::kStageBytes);
+    auto next_stage = [](std::uint32_t st) __attribute__((always_inline)) {
+        const std::uint32_t n = st + static_cast<std::uint32_t>(Q::kStageBytes);
+        return n == kRing ? 0u : n;
+    };
+    std::uint32_t st0 = 0;
+    for (int r = 0; r < items; ++r) {
+        const Item it = item_of(r);
+        if (r > 0) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sl[j] = slot_of(j, it);
+        }
+        m0 = it.m0;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) gc[c] = 5 * it.nbk + cb0 + c;
+        for (int t = 0; t < steps; t += 2) {
+            const std::uint32_t st1 = next_stage(st0), st2 = next_stage(st1);
+            step_body(t, st0, st1, r, std::integral_constant<int, 0>{}, r > 0 && t <= NS - 2);
+            step_body(t + 1, st1, st2, r, std::integral_constant<int, 1>{}, r > 0 && t + 1 <= NS - 2);
+            st0 = st2;
+        }
+        // the reads issued in the last step (the next item's step 0 operands) land before their registers are reused
+        lgkm_wait<0>(A, B, Bl, mt[0].rec, mt[0].as);
+        // drain: the epilogue of the item's last unit (last block, group 1 of step steps - 1, parity 1)
+        KQ_ASM("s_nop 11");
+        epi_range<0, 16, SF16, STAT, false, false>(acc[NC - 1], P[1], mt[1].rec[NC - 1][1], 0.F, mt[1].as[1], 0.F, dmp, 0u, 0);
+        store8w<STAT, NC>(a, acc, m0, wm, gc, lane);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int k = 0; k < 16; ++k) acc[c][k] = 0.F;
+        P[1] = bias;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) mt[1].rec[c][i] = v2i{0, 0};
+            mt[1].as[i] = 0.F;
+        }
+    }
+    KQ_ASM("s_waitcnt vmcnt(0)" ::: "memory");  // the copies past the range land before the workgroup ends
+}
+
+template <bool SF16, bool STAT>
+__global__ __launch_bounds__(kThreads) void gemm8w_kernel(Gemm8Args a) {
+    extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    if (wave < 4) gemm8w_body<3, SF16, STAT>(a, lds, wave, lane);
+    else gemm8w_body<2, SF16, STAT>(a, lds, wave, lane);
+}
+
 // Measurement: the sustained int8 MFMA rate of the whole chip. Every wave of a fully resident grid (one 8-wave
 // workgroup per CU, two waves per SIMD, as gemm8_kernel) issues `iters` rounds of eight independent
 // v_mfma_i32_32x32x32_i8 chains (each chain's next MFMA is eight MFMAs later, so no round waits on a result) and
@@ -1048,6 +1360,18 @@ Gemm8Plan gemm8_plan(const Weight& w, std::int64_t M, bool gelu) {
     const int k_steps = static_cast<int>(w.geo.cols / (w.geo.group == 128 ? 128 : 64));
     const int tiles = p.m_blocks * p.n_blocks;
     p.ksplit = 1;
+    // g = 32 (bound by its epilogue's VALU): where 256 x 128 tiles leave CUs idle and 128 x 160 tiles fill at least
+    // three quarters of the 256 CUs without exceeding them (the fused QKV at M = 2048: 160 -> 256 tiles), the wide
+    // tiles: a SIMD then carries five 32 x 32 blocks per k step instead of eight (additive float zeros excluded)
+    if (w.geo.group == 32 && !gelu && w.zero_mode != ZERO_FLOAT && tiles < 256) {
+        const int mw = static_cast<int>((M + 127) / 128), nw = (NB + 4) / 5;
+        if (mw * nw >= 192 && mw * nw <= 256 && mw * nw > tiles) {
+            p.wide = true;
+            p.m_blocks = mw;
+            p.n_blocks = nw;
+            return p;
+        }
+    }
     // fewer 256-row tiles than CUs: 128-row tiles fill the chip without splitting K (no partial tiles, no reduction
     // kernel), where they are enough to
     const int m128 = static_cast<int>((M + 127) / 128);
@@ -1101,6 +1425,18 @@ hipError_t launch8(const Gemm8Args& g, unsigned blocks, hipStream_t stream) {
         configured = true;
     }
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, stream, g);
+    return hipGetLastError();
+}
+template <bool SF16, bool STAT>
+hipError_t launch8w(const Gemm8Args& g, unsigned blocks, hipStream_t stream) {
+    auto kern = gemm8w_kernel<SF16, STAT>;
+    static bool configured = false;  // per instance: the dynamic LDS limit is raised once
+    if (!configured) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, GeoW::kLds);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), GeoW::kLds, stream, g);
     return hipGetLastError();
 }
 template <int G, bool SF16, bool STAT, bool ZF, bool GELU>
@@ -1179,7 +1515,14 @@ hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t 
         if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
     if (quantize_only) return hipSuccess;
-    const Gemm8Plan p = gemm8_plan(w, c.M, c.gelu_gate);
+    Gemm8Plan p = gemm8_plan(w, c.M, c.gelu_gate);
+    const bool dbg = c.dump != nullptr;
+    if (p.wide && dbg) {  // the parity dump runs the 256 x 128 instance (same epilogue order, so the same y)
+        p.wide = false;
+        p.m_blocks = static_cast<int>((c.M + kBM - 1) / kBM);
+        p.n_blocks = static_cast<int>((w.geo.rows + 31) / 32 + 3) / 4;
+        p.ksplit = 1;
+    }
     Gemm8Args g{};
     g.q = act.q;
     g.scale_t = act.scale;
@@ -1200,9 +1543,13 @@ hipError_t launch_gemm8(const LinearCall& c, const ActBuffers& act, hipStream_t 
     g.ksplit = p.ksplit;
     g.input_scale = c.input_scale;
     g.output_scale = c.output_scale;
-    const bool split = p.ksplit > 1, dbg = c.dump != nullptr, sf16 = w.scale_type == META_F16;
+    const bool split = p.ksplit > 1, sf16 = w.scale_type == META_F16;
     const int total = p.m_blocks * p.n_blocks * p.ksplit;
     const unsigned blocks = static_cast<unsigned>(std::min(total, device_cus()));  // persistent: items loop in the kernel
+    if (p.wide) {
+        if (sf16) return stat ? launch8w<true, true>(g, blocks, stream) : launch8w<true, false>(g, blocks, stream);
+        return stat ? launch8w<false, true>(g, blocks, stream) : launch8w<false, false>(g, blocks, stream);
+    }
     hipError_t e;
     const bool rb1 = p.rb == 1;
     if (G == 128) e = launch8_modes<128>(g, blocks, sf16, stat, zf, c.gelu_gate, split, dbg, rb1, stream);

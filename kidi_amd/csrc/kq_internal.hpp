@@ -53,7 +53,8 @@ enum Route : int {
     ROUTE_GEMM = 6,      // quantize_kernel + gemm_kernel (kq_kernels.hip)
     ROUTE_ROWMAJOR = 7,  // quantize_rowmajor_kernel + rowmajor_kernel (kq_kernels.hip)
     ROUTE_PORTABLE = 8,  // portable_kernel (kq_kernels.hip)
-    ROUTE_GEMM8 = 9      // quantize_rows8_kernel + gemm8_kernel (kq_gemm8.hip)
+    ROUTE_GEMM8 = 9,     // quantize_rows8_kernel + gemm8_kernel (kq_gemm8.hip)
+    ROUTE_GEMM8W = 10    // quantize_rows8_kernel + gemm8w_kernel (kq_gemm8.hip: 128 x 160 tiles, g = 32)
 };
 
 // Activation workspace carved out of one device buffer.
@@ -172,6 +173,7 @@ int set_error(int code, const char* message);
 struct Gemm8Plan {
     int m_blocks = 0, n_blocks = 0, ksplit = 1;
     int rb = 2;  // 32-row blocks per wave: 2 (256-row tiles) or 1 (128-row tiles, plain g = 128 projections)
+    bool wide = false;  // g = 32: 128 x 160 tiles (gemm8w_kernel; n_blocks counts 5-column-block tiles)
 };
 bool gemm8_eligible(const Weight& w);  // the geometry a prefill copy is built for
 Gemm8Plan gemm8_plan(const Weight& w, std::int64_t M, bool gelu);

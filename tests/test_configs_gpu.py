@@ -107,7 +107,7 @@ def test_config2_prefill(dev, ref, M):
 @pytest.mark.parametrize("M", [1, 2048])
 def test_config3_fused_qkv(dev, ref, M):
     run_config(ref, dev, f"configs[3] QKV M={M}", 4, 32, M, 2048, 2048 + 256 + 256, False, 0.0, 130 + M,
-               "decode_kernel" if M == 1 else "gemm8_kernel")
+               "decode_kernel" if M == 1 else "gemm8w_kernel")
 
 
 @pytest.mark.parametrize("M", [1, 2048])

@@ -120,7 +120,7 @@ def test_truncated_blob(lib):
 
 
 # kq_debug_route values
-NONE, DECODE, SKINNY, GEMM_I4, GEMM_I4G, GEMV, GEMM, ROWMAJOR, PORTABLE, GEMM8 = range(10)
+NONE, DECODE, SKINNY, GEMM_I4, GEMM_I4G, GEMV, GEMM, ROWMAJOR, PORTABLE, GEMM8, GEMM8W = range(11)
 F32, BF16 = 0, 2
 
 
@@ -134,7 +134,7 @@ def test_routes_of_baseline_shapes(lib):
     assert route(lib, 4, 32, 8192, 2048, 0, 1) == DECODE           # configs[0]
     assert route(lib, 4, 128, 8192, 2048, 1, 2048) == GEMM8        # configs[2]
     assert route(lib, 4, 128, 8192, 2048, 1, 512) == GEMM8
-    assert route(lib, 4, 32, 2560, 2048, 0, 2048) == GEMM8         # configs[3] fused QKV
+    assert route(lib, 4, 32, 2560, 2048, 0, 2048) == GEMM8W        # configs[3] fused QKV (128 x 160 tiles)
     assert route(lib, 4, 128, 16384, 2048, 1, 2048, gelu=1) == GEMM8
     assert route(lib, 4, 128, 2048, 8192, 1, 2048) == GEMM8        # configs[3] down
     assert route(lib, 4, 128, 8192, 2048, 2, 2048) == GEMM8        # additive float zeros
@@ -147,6 +147,12 @@ def test_routes_of_baseline_shapes(lib):
 def test_routes_of_other_shapes(lib):
     assert route(lib, 4, 64, 2560, 2048, 1, 300) == GEMM8          # g = 64 prefill
     assert route(lib, 4, 32, 2560, 2048, 2, 300) == GEMM8          # g = 32 with additive float zeros
+    # g = 32 in 128 x 160 tiles only where 256 x 128 tiles leave CUs idle and the wide tiles fill 192-256 of them
+    assert route(lib, 4, 32, 2560, 2048, 0, 1536) == GEMM8W        # 120 -> 192 tiles
+    assert route(lib, 4, 32, 2560, 2048, 0, 1408) == GEMM8         # 11 x 16 = 176 wide tiles: fewer than 192
+    assert route(lib, 4, 32, 2560, 2048, 0, 2049) == GEMM8         # 17 x 16 = 272 wide tiles: more than the CUs
+    assert route(lib, 4, 32, 2560, 2048, 2, 2048) == GEMM8         # additive float zeros stay on 256 x 128
+    assert route(lib, 4, 32, 8192, 2048, 0, 2048) == GEMM8         # 512 tiles of 256 x 128 already fill the CUs
     assert route(lib, 4, 32, 2562, 2048, 0, 300) == GEMM_I4G       # N % 4 != 0: no 16-byte output stores
     assert route(lib, 4, 32, 2560, 2048, 0, 300, gelu=1) == GEMM   # gate/up pairing is for g = 128 weights
     assert route(lib, 4, 128, 256, 512, 1, 12) == SKINNY

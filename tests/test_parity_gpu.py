@@ -407,6 +407,53 @@ def test_fused_qkv_prefill_rows(dev, ref):
     check_close(y[torch.from_numpy(rows).to(dev)], y_ref)
 
 
+# g = 32 prefill in 128 x 160 tiles (gemm8w_kernel: where 256 x 128 tiles leave CUs idle): M, K, N, zeros, input
+# scale, x as bf16, F32 weight scales
+WIDE_CASES = [
+    (2048, 2048, 2560, None, 0.0, True, False),   # configs[3] fused QKV
+    (2000, 1024, 2496, "zp", 0.0, False, False),  # ragged M (a partial last row tile), two dead column blocks
+    (1536, 512, 2560, None, 0.05, True, False),   # calibrated inputs
+    (2048, 1024, 2400, None, 0.0, True, True),    # F32 weight scales, 15 column tiles
+]
+
+
+@pytest.mark.parametrize("index", range(len(WIDE_CASES)), ids=[f"m{c[0]}k{c[1]}n{c[2]}" for c in WIDE_CASES])
+def test_wide_tile_prefill(dev, ref, index):
+    """The g = 32 prefill in 128 x 160 tiles: routed there, y bit-identical to the parity-dump instance's (256 x 128
+    tiles, whose int32 partials are checked bit-exact against the oracle here on sampled rows and columns, and the
+    same per-element operation order), and sampled rows within tolerance of the oracle."""
+    M, K, N, zeros, in_s, x_bf16, f32_scales = WIDE_CASES[index]
+    print(f"wide case M={M} K={K} N={N} zeros={zeros} in_s={in_s}", flush=True)
+    rng = np.random.default_rng(700 + index)
+    values, scales, zp, codes = weights(rng, N, K, 4, 32, zero_points=zeros == "zp",
+                                        scale_dtype=np.float32 if f32_scales else np.float16)
+    x = activations(rng, M, K, 0.001)
+    dw = device_weight(values, scales, 4, 32, dev, zero_points=zp)
+    xt = to_dev(x, dev)
+    if x_bf16:
+        xt = xt.to(torch.bfloat16)
+    assert dw.route(xt, in_s) == "gemm8w_kernel"
+    y = dw.linear(xt, in_s)
+    y_d, P_d = dw.debug_partials(xt, in_s)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), y_d.cpu().numpy())
+    rows = np.array(sorted({0, 1, 127, 128, 129, M // 2, M - 1}))
+    xr = ref.f32_to_bf16_bits(x[rows]) if x_bf16 else x[rows]
+    y_ref, path = ref.packed_linear(xr, values, scales, 4, 32, in_s, zero_points=zp, x_bf16=x_bf16, threads=8)
+    assert path == (ref.PATH_BLOCKWISE if in_s == 0 else ref.PATH_SYMMETRIC)
+    check_close(y[torch.from_numpy(rows).to(dev)], y_ref)
+    cols = np.array(sorted({0, 31, 32, 159, 160, N - 1, *rng.choice(N, 24, replace=False).tolist()}))
+    xq = (ref.bf16_bits_to_f32(xr) if x_bf16 else xr)
+    if in_s == 0:
+        q, _, _, zpa = ref.quantize_dynamic(xq, 32, 4)
+    else:
+        (q, _), zpa = ref.quantize_static(xq, 32, in_s), None
+    P = P_d[torch.from_numpy(rows).to(dev)][:, torch.from_numpy(cols).to(dev)].cpu().numpy().astype(np.int64)
+    np.testing.assert_array_equal(P, expected_partials(ref, q, codes[cols], zpa, 4, 32,
+                                                       zero_points=zp[cols] if zp is not None else None,
+                                                       dynamic=in_s == 0))
+
+
 @pytest.mark.parametrize("group", [32, 64, 128])
 @pytest.mark.parametrize("scale_kind", ["f32", "f16_extreme"])
 def test_prefill_scale_forms(dev, ref, group, scale_kind):
