@@ -1360,12 +1360,16 @@ Gemm8Plan gemm8_plan(const Weight& w, std::int64_t M, bool gelu) {
     const int k_steps = static_cast<int>(w.geo.cols / (w.geo.group == 128 ? 128 : 64));
     const int tiles = p.m_blocks * p.n_blocks;
     p.ksplit = 1;
-    // g = 32 (bound by its epilogue's VALU): where 256 x 128 tiles leave CUs idle and 128 x 160 tiles fill at least
-    // three quarters of the 256 CUs without exceeding them (the fused QKV at M = 2048: 160 -> 256 tiles), the wide
-    // tiles: a SIMD then carries five 32 x 32 blocks per k step instead of eight (additive float zeros excluded)
-    if (w.geo.group == 32 && !gelu && w.zero_mode != ZERO_FLOAT && tiles < 256) {
-        const int mw = static_cast<int>((M + 127) / 128), nw = (NB + 4) / 5;
-        if (mw * nw >= 192 && mw * nw <= 256 && mw * nw > tiles) {
+    // g = 32 (bound by its epilogue's VALU): 128 x 160 tiles, where a SIMD carries five 32 x 32 blocks per k step
+    // instead of eight (a tile costs ~0.8 of a 256 x 128 one, measured), when they fill the CUs better: where 256 x 128
+    // tiles leave CUs idle and the wide tiles fill 192-256 of them (the fused QKV at M = 2048: 160 -> 256 tiles), or,
+    // with 256 x 128 tiles in several rounds over the CUs, when 0.8 x the wide tiles' rounds is less (M = 4096: 2
+    // rounds of 320 tiles, the second one a quarter full, against 2 full rounds of 512). Additive float zeros excluded.
+    if (w.geo.group == 32 && !gelu && w.zero_mode != ZERO_FLOAT) {
+        const int mw = static_cast<int>((M + 127) / 128), nw = (NB + 4) / 5, tw = mw * nw;
+        const bool fill = tiles < 256 && tw >= 192 && tw <= 256 && tw > tiles;
+        const bool rounds = tiles >= 256 && 4 * ((tw + 255) / 256) < 5 * ((tiles + 255) / 256);
+        if (fill || rounds) {
             p.wide = true;
             p.m_blocks = mw;
             p.n_blocks = nw;

@@ -151,6 +151,9 @@ def test_routes_of_other_shapes(lib):
     assert route(lib, 4, 32, 2560, 2048, 0, 1536) == GEMM8W        # 120 -> 192 tiles
     assert route(lib, 4, 32, 2560, 2048, 0, 1408) == GEMM8         # 11 x 16 = 176 wide tiles: fewer than 192
     assert route(lib, 4, 32, 2560, 2048, 0, 2049) == GEMM8         # 17 x 16 = 272 wide tiles: more than the CUs
+    assert route(lib, 4, 32, 2560, 2048, 0, 3072) == GEMM8         # 240 tiles in one round against 384 in two
+    assert route(lib, 4, 32, 2560, 2048, 0, 4096) == GEMM8W        # 2 rounds of 512 against 2 of 320 (one a quarter full)
+    assert route(lib, 4, 32, 2560, 2048, 0, 6144) == GEMM8         # 3 rounds of 768 against 2 of 480
     assert route(lib, 4, 32, 2560, 2048, 2, 2048) == GEMM8         # additive float zeros stay on 256 x 128
     assert route(lib, 4, 32, 8192, 2048, 0, 2048) == GEMM8         # 512 tiles of 256 x 128 already fill the CUs
     assert route(lib, 4, 32, 2562, 2048, 0, 300) == GEMM_I4G       # N % 4 != 0: no 16-byte output stores

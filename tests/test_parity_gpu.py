@@ -414,6 +414,7 @@ WIDE_CASES = [
     (2000, 1024, 2496, "zp", 0.0, False, False),  # ragged M (a partial last row tile), two dead column blocks
     (1536, 512, 2560, None, 0.05, True, False),   # calibrated inputs
     (2048, 1024, 2400, None, 0.0, True, True),    # F32 weight scales, 15 column tiles
+    (4096, 512, 2560, None, 0.0, True, False),    # two tiles per workgroup (the copy ring runs across items)
 ]
 
 
