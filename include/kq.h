@@ -281,7 +281,9 @@ kq_status kq_debug_quantize(const kq_weight* weight, const void* x, kq_dtype x_d
 
 /* Runs the projection kernel that kq_packed_linear would run for these arguments and also writes its int32
  * per-group partials [M, N, K/g]: sum over the group of x_code * w_code, where w_code = c (symmetric), u - zp
- * (ZP_U8 zero-points, u = c + 8) or c (additive float zeros), and x_code = q - zp_a for 8-bit dynamic. */
+ * (ZP_U8 zero-points, u = c + 8) or c (additive float zeros), and x_code = q - zp_a for 8-bit dynamic. (Where
+ * kq_packed_linear takes route 10, g = 32 in 128 x 160 tiles, the dump comes from the 256 x 128 instance of the same
+ * GEMM, route 9, whose y is bit-identical: the same operations per element in the same order.) */
 kq_status kq_debug_partials(const kq_weight* weight, const kq_linear_args* args, int32_t* partials, void* stream);
 
 /* The kernel sequence a projection call takes, without running it (no counterpart in the reference; for tests that

@@ -275,7 +275,8 @@ class DeviceWeight:
         return N.ROUTE_NAMES[r]
 
     def debug_partials(self, x: torch.Tensor, input_scale: float = 0.0, output_scale: float = 0.0):
-        """(y, int32 partials [M, N, K/g]) from the same kernel as ``linear``."""
+        """(y, int32 partials [M, N, K/g]) from the same kernel as ``linear`` (for g = 32 in 128 x 160 tiles, its
+        256 x 128 form, whose y is bit-identical)."""
         x2 = x.reshape(-1, self.cols).contiguous()
         m = x2.shape[0]
         y = torch.empty((m, self.rows), dtype=torch.float32, device=x.device)

@@ -455,6 +455,28 @@ def test_wide_tile_prefill(dev, ref, index):
                                                        dynamic=in_s == 0))
 
 
+def test_wide_tile_output_calibration(dev, ref):
+    """Calibrated outputs (output_scale > 0) from the 128 x 160 g = 32 tiles: bit-identical to the dump instance and
+    within one int8 step of the oracle, on sampled rows."""
+    M, K, N, out_s = 2048, 512, 2560, 0.01
+    rng = np.random.default_rng(750)
+    values, scales, _, _ = weights(rng, N, K, 4, 32)
+    x = activations(rng, M, K, 0.0)
+    dw = device_weight(values, scales, 4, 32, dev)
+    xt = to_dev(x, dev).to(torch.bfloat16)
+    assert dw.route(xt) == "gemm8w_kernel"
+    y = dw.linear(xt, 0.0, out_s)
+    y_d, _ = dw.debug_partials(xt, 0.0, out_s)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), y_d.cpu().numpy())
+    rows = np.array([0, 5, 127, 128, 1500, M - 1])
+    y_ref, _ = ref.packed_linear(x[rows], values, scales, 4, 32, 0.0, out_s, threads=8)
+    steps = np.rint((y[torch.from_numpy(rows).to(dev)].cpu().numpy() - y_ref) / out_s)
+    assert np.all(np.abs(steps) <= 1)
+    assert np.mean(steps == 0) > 0.99
+    assert np.any(y_ref != 0)
+
+
 @pytest.mark.parametrize("group", [32, 64, 128])
 @pytest.mark.parametrize("scale_kind", ["f32", "f16_extreme"])
 def test_prefill_scale_forms(dev, ref, group, scale_kind):
