@@ -544,8 +544,11 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < (GELU ? 1 : RT) * M * 16; idx += blockDim.x) {
-        // (greedy: a row's RT x 16 columns on consecutive lanes, in column order)
-        const int r = GREEDY ? (idx / 16) % RT : idx / (M * 16), i = GREEDY ? idx / (RT * 16) : (idx / 16) % M, c = idx % 16;
+        // (greedy: a row's RT x 16 columns on consecutive lanes, in column order; no division by the runtime M: a
+        // unit holds at most two row tiles)
+        const int q16 = idx >> 4, c = idx & 15;
+        const int r = GREEDY ? q16 % RT : (RT == 1 ? 0 : static_cast<int>(q16 >= M));
+        const int i = GREEDY ? q16 / RT : q16 - r * M;
         float v[2] = {0.F, 0.F};
 #pragma unroll
         for (int h = 0; h < (GELU ? 2 : 1); ++h) {
