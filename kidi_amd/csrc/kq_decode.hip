@@ -195,7 +195,9 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
             const std::uint32_t e = static_cast<std::uint32_t>(m * K + kb + 8 * lane);
             const std::uint32_t off = x_f32 ? 4 * e : 2 * e;
             xr[m][0] = ld16(xres, off);
-            xr[m][1] = ld16(xres, x_f32 ? off + 16 : off);
+            // bf16 needs one 16-byte word per piece: the second load goes past the buffer (the range check returns
+            // zeros without a memory request; no branch, so the wait counts stay exact)
+            xr[m][1] = ld16(xres, x_f32 ? off + 16 : 0x80000000u);
         }
     }
     // fused RMS normalization (variants of up to 2048 columns): norm weights and residual rows of this lane's piece
@@ -220,7 +222,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
                         const std::uint32_t e = static_cast<std::uint32_t>(m * K + kb + 8 * lane);
                         const std::uint32_t off = x_f32 ? 4 * e : 2 * e;
                         nr[m][0] = ld16(rres, off);
-                        nr[m][1] = ld16(rres, x_f32 ? off + 16 : off);
+                        nr[m][1] = ld16(rres, x_f32 ? off + 16 : 0x80000000u);  // bf16: past the buffer, as above
                     }
                 }
                 if (a.norm_scale) nscale = a.norm_scale[0];
