@@ -415,6 +415,8 @@ WIDE_CASES = [
     (1536, 512, 2560, None, 0.05, True, False),   # calibrated inputs
     (2048, 1024, 2400, None, 0.0, True, True),    # F32 weight scales, 15 column tiles
     (4096, 512, 2560, None, 0.0, True, False),    # two tiles per workgroup (the copy ring runs across items)
+    (2048, 128, 2560, None, 0.0, True, False),    # two k steps: fewer than the four ring stages
+    (4096, 256, 2560, "zp", 0.0, False, False),   # four k steps per item, two items per workgroup
 ]
 
 
