@@ -39,6 +39,7 @@ using namespace dev;
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));  // fp32 accumulators of a 32 x 32 block (the MFMA output layout)
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 
@@ -338,9 +339,11 @@ __device__ __forceinline__ void epi_converts(v16i& P, const v2i& rec) {
     }
 }
 template <int K0, int K1, bool SF16, bool STAT, bool ZF>
-__device__ __forceinline__ void epi_accumulates(float (&acc)[16], const v16i& P, const v2i& rec, float z, float as, float az) {
+__device__ __forceinline__ void epi_accumulates(v16f& acc, const v16i& P, const v2i& rec, float z, float as, float az) {
     if constexpr (K0 < K1) {
-        epi_accumulate<K0, SF16, STAT, ZF>(acc[K0], P[K0], rec, z, as, az);
+        float x = acc[K0];
+        epi_accumulate<K0, SF16, STAT, ZF>(x, P[K0], rec, z, as, az);
+        acc[K0] = x;
         epi_accumulates<K0 + 1, K1, SF16, STAT, ZF>(acc, P, rec, z, as, az);
     }
 }
@@ -363,7 +366,7 @@ struct Dump {
     std::uint32_t row_bytes;   // N * groups * 4
 };
 template <int K0, int K1, bool SF16, bool STAT, bool ZF, bool DBG>
-__device__ __forceinline__ void epi_range(float (&acc)[16], v16i& P, const v2i& rec, float z, float as, float az, const Dump& d,
+__device__ __forceinline__ void epi_range(v16f& acc, v16i& P, const v2i& rec, float z, float as, float az, const Dump& d,
                                           std::uint32_t voff, int g) {
     if constexpr (DBG) epi_dump<K0, K1, DBG>(P, rsrc(d.base, d.bytes), voff, d.row_bytes, static_cast<std::uint32_t>(g) * 4);
     epi_converts<K0, K1, SF16, STAT>(P, rec);
@@ -375,6 +378,13 @@ __device__ __forceinline__ void mfma_first(v16i& P, const v4i& A, const v4i& B, 
 }
 __device__ __forceinline__ void mfma_acc(v16i& P, const v4i& A, const v4i& B) {
     KQ_ASM("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(P) : "v"(A), "v"(B));
+}
+// Additive float zeros of a block and a pair of groups (g, g + 1) straight into its fp32 accumulators:
+// acc[row][col] += a[row][0] b[0][col] + a[row][1] b[1][col] with a[row][k] = (a_s * Q)[row, g + k] (lane l: row
+// l % 32, k = l / 32) and b[k][col] = z[g + k, col] (lane l: column l % 32, k = l / 32); the result layout is the
+// 32 x 32 layout of the int8 MFMAs. The two wait states cover VALU writes of acc, a and b just before it.
+__device__ __forceinline__ void mfma_zero(v16f& acc, float a, float b) {
+    KQ_ASM("s_nop 1\n\tv_mfma_f32_32x32x2_f32 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
 }
 
 // 4 x 4 transpose inside each lane quad: on entry lane q of the quad holds v[e] = element (row e, column q); on exit
@@ -401,7 +411,7 @@ constexpr int kTileStoresGelu = 8;
 constexpr int min63(int n) { return n < 63 ? n : 63; }
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 template <bool STAT, bool GELU, int RB = 2>
-__device__ __forceinline__ void store8t(const Gemm8Args& a, const float (&acc)[RB][2][16], int m0, int wm, const int (&gc)[2],
+__device__ __forceinline__ void store8t(const Gemm8Args& a, const v16f (&acc)[RB][2], int m0, int wm, const int (&gc)[2],
                                         int lane) {
     const int n_out = GELU ? (a.N >> 1) : a.N;
     const int rows = min(a.M - m0, 128 * RB);
@@ -448,7 +458,7 @@ __device__ __forceinline__ void store8t(const Gemm8Args& a, const float (&acc)[R
 // 128-byte row segments. Every lane issues exactly 32 RB stores; rows past M and columns past N get a per-lane
 // offset beyond the buffer resource, whose range check drops them.
 template <bool STAT, int RB = 2>
-__device__ __forceinline__ void store8d(const Gemm8Args& a, const float (&acc)[RB][2][16], int m0, int wm, const int (&gc)[2],
+__device__ __forceinline__ void store8d(const Gemm8Args& a, const v16f (&acc)[RB][2], int m0, int wm, const int (&gc)[2],
                                         int lane) {
     const int n_out = a.N;
     const int rows = min(a.M - m0, 128 * RB);
@@ -494,6 +504,10 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     using Q = Geo8<G, RB>;
     constexpr int CH = Q::CH, GPS = Q::GPS, NS = Q::kStages, TM = Q::TM;
     static_assert(RB == 2 || (G == 128 && !GELU && !SPLIT), "the 128-row tile serves plain g = 128 projections without split K");
+    // additive float zeros: on an fp32 MFMA per block and pair of steps in the 256 x 128 g = 128 body (ZM), else one
+    // more VALU per element and group in the epilogue (ZFE)
+    constexpr bool ZM = ZF && G == 128 && RB == 2;
+    constexpr bool ZFE = ZF && !ZM;
     extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -623,7 +637,8 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     [[maybe_unused]] const std::uint32_t w_lane0 = lds0 + Q::kWOff + (cb_l0 * 32 + col) * 16;
     [[maybe_unused]] const std::uint32_t w_lane1 = lds0 + Q::kWOff + (cb_l1 * 32 + col) * 16;
     [[maybe_unused]] const std::uint32_t s_lane = lds0 + Q::kSOff + (32 * RB * wm + bcast_row(lane)) * 4;
-    [[maybe_unused]] const std::uint32_t z_lane = lds0 + Q::kZOff + (32 * RB * wm + bcast_row(lane)) * 4;
+    // a_s * Q of row bcast_row(lane) (the epilogue's DPP broadcast), or of row lane % 32 (the MFMA's A operand)
+    [[maybe_unused]] const std::uint32_t z_lane = lds0 + Q::kZOff + (32 * RB * wm + (ZM ? (lane & 31) : bcast_row(lane))) * 4;
     auto read_meta = [&](Meta<GPS>& mt, std::uint32_t stage) __attribute__((always_inline)) {
 #pragma unroll
         for (int gg = 0; gg < GPS; ++gg) {
@@ -692,7 +707,7 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     // (store8d: 32 RB 4-byte stores; store8t: 8 RB 16-byte stores, 8 with GELU; split partials: 16)
     [[maybe_unused]] constexpr int kStoresAfter = SPLIT ? 16 : (GELU ? kTileStoresGelu : (DBG ? 8 * RB : 32 * RB));
 
-    float acc[RB][2][16];
+    v16f acc[RB][2];
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
@@ -710,6 +725,8 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     P[1] = bias;
     v4i A[RB][CH], B0[CH], B1[2][CH];
     Meta<GPS> mt[2];
+    // ZM: lanes 0-31 take the pair's first step's a_s * Q and z, lanes 32-63 the second step's (operand k = lane / 32)
+    [[maybe_unused]] const bool lo = lane < 32;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -793,19 +810,28 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             ds_read16<6144>(A[1][2], a_lane + st_now);
             ds_read16<7168>(A[1][3], a_lane + st_now);
             mfma_acc(P[0], A[0][1], B0[1]);
-            epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[1][0], prv.az[1][0], dmp, dvo_prev, g - 1);
+            epi_range<0, 6, SF16, STAT, ZFE, DBG>(acc[1][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[1][0], prv.az[1][0], dmp, dvo_prev, g - 1);
             mfma_acc(P[0], A[0][2], B0[2]);
-            epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[1][0], prv.az[1][0], dmp, dvo_prev, g - 1);
+            epi_range<6, 11, SF16, STAT, ZFE, DBG>(acc[1][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[1][0], prv.az[1][0], dmp, dvo_prev, g - 1);
             mfma_acc(P[0], A[0][3], B0[3]);
-            epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[1][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[1][0], prv.az[1][0], dmp, dvo_prev, g - 1);
+            epi_range<11, 16, SF16, STAT, ZFE, DBG>(acc[1][1], P[1], prv.rec[1][0], prv.z[1][0], prv.as[1][0], prv.az[1][0], dmp, dvo_prev, g - 1);
+            // ZM, odd step t: the zero terms of the pair (t - 1, t) while both steps' metadata are in registers (prv: t - 1,
+            // cur: t; prv is read again after the mid-step barrier); each MFMA follows the epilogue that last wrote its
+            // block, and the next epilogue of that block comes at least a mid-step barrier later
+            if constexpr (ZM && p == 1) mfma_zero(acc[1][1], lo ? prv.az[1][0] : cur.az[1][0], lo ? prv.z[1][0] : cur.z[1][0]);
             // ---- b1
             mfma_first(P[1], A[0][0], Bc[0], bias);
             mfma_acc(P[1], A[0][1], Bc[1]);
-            epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            epi_range<0, 6, SF16, STAT, ZFE, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
             mfma_acc(P[1], A[0][2], Bc[2]);
-            epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            epi_range<6, 11, SF16, STAT, ZFE, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
             mfma_acc(P[1], A[0][3], Bc[3]);
-            epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            epi_range<11, 16, SF16, STAT, ZFE, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
+            if constexpr (ZM && p == 1) {
+                mfma_zero(acc[0][0], lo ? prv.az[0][0] : cur.az[0][0], lo ? prv.z[0][0] : cur.z[0][0]);
+                mfma_zero(acc[0][1], lo ? prv.az[0][0] : cur.az[0][0], lo ? prv.z[1][0] : cur.z[1][0]);
+                mfma_zero(acc[1][0], lo ? prv.az[1][0] : cur.az[1][0], lo ? prv.z[0][0] : cur.z[0][0]);
+            }
             mid_step();
             // ---- b2
             mfma_first(P[0], A[1][0], B0[0], bias);
@@ -813,20 +839,20 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             read_meta(prv, st_next);
             read_frags(A[0], a_lane + st_next);  // A row block 0 is free since b1
             mfma_acc(P[0], A[1][1], B0[1]);
-            epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
+            epi_range<0, 6, SF16, STAT, ZFE, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
             mfma_acc(P[0], A[1][2], B0[2]);
-            epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
+            epi_range<6, 11, SF16, STAT, ZFE, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
             mfma_acc(P[0], A[1][3], B0[3]);
-            epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
+            epi_range<11, 16, SF16, STAT, ZFE, DBG>(acc[0][1], P[1], cur.rec[1][0], cur.z[1][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][1], g);
             // ---- b3
             mfma_first(P[1], A[1][0], Bc[0], bias);
             read_frags(B0, b_lane0 + st_next);
             mfma_acc(P[1], A[1][1], Bc[1]);
-            epi_range<0, 6, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
+            epi_range<0, 6, SF16, STAT, ZFE, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
             mfma_acc(P[1], A[1][2], Bc[2]);
-            epi_range<6, 11, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
+            epi_range<6, 11, SF16, STAT, ZFE, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
             mfma_acc(P[1], A[1][3], Bc[3]);
-            epi_range<11, 16, SF16, STAT, ZF, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
+            epi_range<11, 16, SF16, STAT, ZFE, DBG>(acc[1][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[1][0], cur.az[1][0], dmp, dvo[1][0], g);
         } else if constexpr (G == 64) {
             // ---- b0
             mfma_first(P[0], A[0][0], B0[0], bias);
@@ -902,9 +928,10 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
         lgkm_wait<0>(A[0], B0, B1, mt[0].rec, mt[0].z, mt[0].as, mt[0].az);
         // drain: the epilogue of the item's last unit (block b3 and the step's last group, step steps - 1, parity 1)
         KQ_ASM("s_nop 11");
-        epi_range<0, 16, SF16, STAT, ZF, DBG>(acc[RB - 1][1], P[1], mt[1].rec[1][GPS - 1], mt[1].z[1][GPS - 1],
-                                              mt[1].as[RB - 1][GPS - 1], mt[1].az[RB - 1][GPS - 1], dmp, dvo[RB - 1][1],
-                                              (ks * steps + steps) * GPS - 1);
+        epi_range<0, 16, SF16, STAT, ZFE, DBG>(acc[RB - 1][1], P[1], mt[1].rec[1][GPS - 1], mt[1].z[1][GPS - 1],
+                                               mt[1].as[RB - 1][GPS - 1], mt[1].az[RB - 1][GPS - 1], dmp, dvo[RB - 1][1],
+                                               (ks * steps + steps) * GPS - 1);
+
         if constexpr (SPLIT) {
             // partial tile [16 chunks][512 threads][4 floats]: chunk j of every thread is one coalesced 8 KiB run
             v4f* dst = reinterpret_cast<v4f*>(a.partial) + (static_cast<std::int64_t>(ks) * tiles + tile) * 16 * kThreads + tid;
@@ -950,7 +977,7 @@ __global__ __launch_bounds__(kThreads) void gemm8_reduce_kernel(Gemm8Args a) {
     const int tile = blockIdx.x;
     const int tiles = a.m_blocks * a.n_blocks;
     const int mb = tile % a.m_blocks, nbk = tile / a.m_blocks;
-    float acc[2][2][16];
+    v16f acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -1023,7 +1050,7 @@ struct MetaW {  // one k step's epilogue operands: weight records of the wave's 
 // Final values of a wave's NC blocks (row block wm, global column blocks gc[]), 4-byte stores as store8d: 16 per
 // block and lane.
 template <bool STAT, int NC>
-__device__ __forceinline__ void store8w(const Gemm8Args& a, const float (&acc)[NC][16], int m0, int wm, const int (&gc)[NC], int lane) {
+__device__ __forceinline__ void store8w(const Gemm8Args& a, const v16f (&acc)[NC], int m0, int wm, const int (&gc)[NC], int lane) {
     const int n_out = a.N;
     const int rows = min(a.M - m0, 128);
     const __amdgpu_buffer_rsrc_t yres = rsrc(a.y + static_cast<std::int64_t>(m0) * n_out, static_cast<std::uint32_t>(rows) * n_out * 4);
@@ -1162,7 +1189,7 @@ __device__ __forceinline__ void gemm8w_body(const Gemm8Args& a, std::uint8_t* ld
     Dump dmp{};
     constexpr int kStoresAfter = 16 * NC;
 
-    float acc[NC][16];
+    v16f acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c)
 #pragma unroll

@@ -107,6 +107,7 @@ CASES = [
     (4, 128, 64, 4096, 256, "zp", 0.0, True, 0.0),
     (4, 128, 300, 8192, 256, None, 0.0, False, 0.001),
     (4, 128, 40, 8192, 144, None, 0.05, False, 0.0),
+    (4, 128, 64, 4096, 256, "f16", 0.0, True, 0.001),  # additive float zeros on the fp32 MFMA, K split in 4
     # 4-bit g = 32 / 64 prefill (gemm8_kernel from the prefill copy: one or two groups per 64-column step):
     # fused-QKV-like K, ragged M and N, zero points, additive float zeros, calibrated inputs, a single item step pair
     (4, 32, 300, 2048, 640, None, 0.0, True, 0.001),
