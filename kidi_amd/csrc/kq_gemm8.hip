@@ -28,6 +28,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 #include "kq_device.hpp"
 #include "kq_internal.hpp"
@@ -338,8 +339,9 @@ __device__ __forceinline__ void epi_converts(v16i& P, const v2i& rec) {
         epi_converts<K0 + 1, K1, SF16, STAT>(P, rec);
     }
 }
-template <int K0, int K1, bool SF16, bool STAT, bool ZF>
-__device__ __forceinline__ void epi_accumulates(v16f& acc, const v16i& P, const v2i& rec, float z, float as, float az) {
+// (AccT: float[16], or v16f where an MFMA also accumulates into the block and needs it as one register tuple)
+template <int K0, int K1, bool SF16, bool STAT, bool ZF, typename AccT>
+__device__ __forceinline__ void epi_accumulates(AccT& acc, const v16i& P, const v2i& rec, float z, float as, float az) {
     if constexpr (K0 < K1) {
         float x = acc[K0];
         epi_accumulate<K0, SF16, STAT, ZF>(x, P[K0], rec, z, as, az);
@@ -365,8 +367,8 @@ struct Dump {
     std::uint32_t bytes;       // the buffer's extent from base
     std::uint32_t row_bytes;   // N * groups * 4
 };
-template <int K0, int K1, bool SF16, bool STAT, bool ZF, bool DBG>
-__device__ __forceinline__ void epi_range(v16f& acc, v16i& P, const v2i& rec, float z, float as, float az, const Dump& d,
+template <int K0, int K1, bool SF16, bool STAT, bool ZF, bool DBG, typename AccT>
+__device__ __forceinline__ void epi_range(AccT& acc, v16i& P, const v2i& rec, float z, float as, float az, const Dump& d,
                                           std::uint32_t voff, int g) {
     if constexpr (DBG) epi_dump<K0, K1, DBG>(P, rsrc(d.base, d.bytes), voff, d.row_bytes, static_cast<std::uint32_t>(g) * 4);
     epi_converts<K0, K1, SF16, STAT>(P, rec);
@@ -410,8 +412,8 @@ __device__ __forceinline__ void quad_transpose(float (&v)[4], int lane) {
 constexpr int kTileStoresGelu = 8;
 constexpr int min63(int n) { return n < 63 ? n : 63; }
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-template <bool STAT, bool GELU, int RB = 2>
-__device__ __forceinline__ void store8t(const Gemm8Args& a, const v16f (&acc)[RB][2], int m0, int wm, const int (&gc)[2],
+template <bool STAT, bool GELU, int RB = 2, typename AccT>
+__device__ __forceinline__ void store8t(const Gemm8Args& a, const AccT (&acc)[RB][2], int m0, int wm, const int (&gc)[2],
                                         int lane) {
     const int n_out = GELU ? (a.N >> 1) : a.N;
     const int rows = min(a.M - m0, 128 * RB);
@@ -457,8 +459,8 @@ __device__ __forceinline__ void store8t(const Gemm8Args& a, const v16f (&acc)[RB
 // 32 RB wm + 32 i + 8 (k / 4) + 4 (lane / 32) + k % 4, column 32 gc[c] + lane % 32: one store instruction writes two
 // 128-byte row segments. Every lane issues exactly 32 RB stores; rows past M and columns past N get a per-lane
 // offset beyond the buffer resource, whose range check drops them.
-template <bool STAT, int RB = 2>
-__device__ __forceinline__ void store8d(const Gemm8Args& a, const v16f (&acc)[RB][2], int m0, int wm, const int (&gc)[2],
+template <bool STAT, int RB = 2, typename AccT>
+__device__ __forceinline__ void store8d(const Gemm8Args& a, const AccT (&acc)[RB][2], int m0, int wm, const int (&gc)[2],
                                         int lane) {
     const int n_out = a.N;
     const int rows = min(a.M - m0, 128 * RB);
@@ -707,7 +709,8 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
     // (store8d: 32 RB 4-byte stores; store8t: 8 RB 16-byte stores, 8 with GELU; split partials: 16)
     [[maybe_unused]] constexpr int kStoresAfter = SPLIT ? 16 : (GELU ? kTileStoresGelu : (DBG ? 8 * RB : 32 * RB));
 
-    v16f acc[RB][2];
+    using AccT = std::conditional_t<ZM, v16f, float[16]>;
+    AccT acc[RB][2];
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
@@ -818,7 +821,9 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             // ZM, odd step t: the zero terms of the pair (t - 1, t) while both steps' metadata are in registers (prv: t - 1,
             // cur: t; prv is read again after the mid-step barrier); each MFMA follows the epilogue that last wrote its
             // block, and the next epilogue of that block comes at least a mid-step barrier later
-            if constexpr (ZM && p == 1) mfma_zero(acc[1][1], lo ? prv.az[1][0] : cur.az[1][0], lo ? prv.z[1][0] : cur.z[1][0]);
+            if constexpr (ZM) {
+                if constexpr (p == 1) mfma_zero(acc[1][1], lo ? prv.az[1][0] : cur.az[1][0], lo ? prv.z[1][0] : cur.z[1][0]);
+            }
             // ---- b1
             mfma_first(P[1], A[0][0], Bc[0], bias);
             mfma_acc(P[1], A[0][1], Bc[1]);
@@ -827,10 +832,12 @@ __global__ __launch_bounds__(kThreads) void gemm8_kernel(Gemm8Args a) {
             epi_range<6, 11, SF16, STAT, ZFE, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
             mfma_acc(P[1], A[0][3], Bc[3]);
             epi_range<11, 16, SF16, STAT, ZFE, DBG>(acc[0][0], P[0], cur.rec[0][0], cur.z[0][0], cur.as[0][0], cur.az[0][0], dmp, dvo[0][0], g);
-            if constexpr (ZM && p == 1) {
-                mfma_zero(acc[0][0], lo ? prv.az[0][0] : cur.az[0][0], lo ? prv.z[0][0] : cur.z[0][0]);
-                mfma_zero(acc[0][1], lo ? prv.az[0][0] : cur.az[0][0], lo ? prv.z[1][0] : cur.z[1][0]);
-                mfma_zero(acc[1][0], lo ? prv.az[1][0] : cur.az[1][0], lo ? prv.z[0][0] : cur.z[0][0]);
+            if constexpr (ZM) {
+                if constexpr (p == 1) {
+                    mfma_zero(acc[0][0], lo ? prv.az[0][0] : cur.az[0][0], lo ? prv.z[0][0] : cur.z[0][0]);
+                    mfma_zero(acc[0][1], lo ? prv.az[0][0] : cur.az[0][0], lo ? prv.z[1][0] : cur.z[1][0]);
+                    mfma_zero(acc[1][0], lo ? prv.az[1][0] : cur.az[1][0], lo ? prv.z[0][0] : cur.z[0][0]);
+                }
             }
             mid_step();
             // ---- b2
@@ -977,7 +984,7 @@ __global__ __launch_bounds__(kThreads) void gemm8_reduce_kernel(Gemm8Args a) {
     const int tile = blockIdx.x;
     const int tiles = a.m_blocks * a.n_blocks;
     const int mb = tile % a.m_blocks, nbk = tile / a.m_blocks;
-    v16f acc[2][2];
+    float acc[2][2][16];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -1050,7 +1057,7 @@ struct MetaW {  // one k step's epilogue operands: weight records of the wave's 
 // Final values of a wave's NC blocks (row block wm, global column blocks gc[]), 4-byte stores as store8d: 16 per
 // block and lane.
 template <bool STAT, int NC>
-__device__ __forceinline__ void store8w(const Gemm8Args& a, const v16f (&acc)[NC], int m0, int wm, const int (&gc)[NC], int lane) {
+__device__ __forceinline__ void store8w(const Gemm8Args& a, const float (&acc)[NC][16], int m0, int wm, const int (&gc)[NC], int lane) {
     const int n_out = a.N;
     const int rows = min(a.M - m0, 128);
     const __amdgpu_buffer_rsrc_t yres = rsrc(a.y + static_cast<std::int64_t>(m0) * n_out, static_cast<std::uint32_t>(rows) * n_out * 4);
@@ -1189,7 +1196,7 @@ __device__ __forceinline__ void gemm8w_body(const Gemm8Args& a, std::uint8_t* ld
     Dump dmp{};
     constexpr int kStoresAfter = 16 * NC;
 
-    v16f acc[NC];
+    float acc[NC][16];
 #pragma unroll
     for (int c = 0; c < NC; ++c)
 #pragma unroll
