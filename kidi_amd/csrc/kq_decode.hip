@@ -128,8 +128,10 @@ __device__ __forceinline__ float segment_sum_squares(const float (&v)[8]) {
 }
 
 // MR: rows of the variant (4 or 8); WMAX: most waves per workgroup (4 for K <= 2048, 16 up to K = 8192), which
-// sets the register budget (512 / (WMAX / 4) VGPRs per lane)
-template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, int MR, int WMAX, bool GREEDY = false, bool NORM = false>
+// sets the register budget (512 / (WMAX / 4) VGPRs per lane); FULL: M = MR, so no row is guarded by a runtime
+// compare and the rows' quantization chains interleave (M = 4: 0.3-0.56 µs per launch)
+template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, int MR, int WMAX, bool GREEDY = false, bool NORM = false,
+          bool FULL = false>
 __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const std::uint8_t* ptiles, const void* pscales,
                                                            const void* paux, int pflags, int pK, int pn_tiles, int ppairs,
                                                            int ptotal, DecodeArgs a) {
@@ -152,7 +154,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int W = blockDim.x >> 6;
     const int nn = lane & 15, L = lane >> 4;
-    const int M = pflags & 0xFF, K = pK, k_tiles = K / (512 / BITS), n_tiles = pn_tiles, x_f32 = (pflags >> 8) & 1;
+    const int M = FULL ? MR : (pflags & 0xFF), K = pK, k_tiles = K / (512 / BITS), n_tiles = pn_tiles, x_f32 = (pflags >> 8) & 1;
     const int scale_half = (pflags >> 9) & 1, aux_half = (pflags >> 10) & 1, groups_p = K / G;
     const int aslot = nn >> 2;  // A-operand row of this lane: activation row (nn & 3) + 4 h, group slot
 
@@ -627,6 +629,13 @@ hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds,
             if (wide) return hipErrorInvalidValue;
             if (a.M <= 4) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 4, false, true>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
             else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 8, 4, false, true>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
+            return hipGetLastError();
+        }
+    }
+    if constexpr (BITS == 4 && G == 128 && QM == dev::QUANT_DYN_SYM && !DBG && !GREEDY) {
+        if (a.M == 4) {  // configs[1]'s M = 4 projections: the row count fixed at compile time
+            if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 16, false, false, true>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
+            else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 4, false, false, true>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
             return hipGetLastError();
         }
     }
