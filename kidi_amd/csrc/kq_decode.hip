@@ -197,9 +197,11 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
             const std::uint32_t e = static_cast<std::uint32_t>(m * K + kb + 8 * lane);
             const std::uint32_t off = x_f32 ? 4 * e : 2 * e;
             xr[m][0] = ld16(xres, off);
-            // bf16 needs one 16-byte word per piece: the second load goes past the buffer (the range check returns
-            // zeros without a memory request; no branch, so the wait counts stay exact)
-            xr[m][1] = ld16(xres, x_f32 ? off + 16 : 0x80000000u);
+            // bf16 needs one 16-byte word per piece. With four rows a second load, even one past the buffer, costs
+            // more than a uniform branch around it (0.14-0.17 µs); at M = 1 the branch costs more (0.04 µs), so
+            // there the second load goes past the buffer (the range check returns zeros without a memory request)
+            if constexpr (FULL) xr[m][1] = x_f32 ? ld16(xres, off + 16) : make_uint4(0, 0, 0, 0);
+            else xr[m][1] = ld16(xres, x_f32 ? off + 16 : 0x80000000u);
         }
     }
     // fused RMS normalization (variants of up to 2048 columns): norm weights and residual rows of this lane's piece
