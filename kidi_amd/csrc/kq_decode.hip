@@ -535,6 +535,18 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
     // sum the four group slots (lanes nn + 16 L) and the waves
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
+        if constexpr (FULL && MR == 4) {
+            // four rows at once: permlane16_swap of rows 0 and 1 leaves, summed, row 0's slots L, L ^ 1 in 16-lane
+            // rows 0 and 2 and row 1's in 1 and 3 (rows 2 and 3 likewise); permlane32_swap of the two then leaves
+            // row L's total in 16-lane row L, added in the same order as below: (slots 0 + 1) + (slots 2 + 3)
+            const auto p01 = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[r][0]), __float_as_uint(acc[r][1]), false, false);
+            const auto p23 = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[r][2]), __float_as_uint(acc[r][3]), false, false);
+            const float u = __uint_as_float(p01[0]) + __uint_as_float(p01[1]);
+            const float w = __uint_as_float(p23[0]) + __uint_as_float(p23[1]);
+            const auto pq = __builtin_amdgcn_permlane32_swap(__float_as_uint(u), __float_as_uint(w), false, false);
+            red[((wave * RT + r) * MR + L) * 16 + nn] = __uint_as_float(pq[0]) + __uint_as_float(pq[1]);
+            continue;
+        }
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
             if (i < M) {
