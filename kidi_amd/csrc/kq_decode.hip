@@ -128,10 +128,11 @@ __device__ __forceinline__ float segment_sum_squares(const float (&v)[8]) {
 }
 
 // MR: rows of the variant (4 or 8); WMAX: most waves per workgroup (4 for K <= 2048, 16 up to K = 8192), which
-// sets the register budget (512 / (WMAX / 4) VGPRs per lane); FULL: M = MR, so no row is guarded by a runtime
-// compare and the rows' quantization chains interleave (M = 4: 0.3-0.56 µs per launch)
+// sets the register budget (512 / (WMAX / 4) VGPRs per lane); MK: the row count fixed at compile time (0: the
+// runtime M), so no row is guarded by a runtime compare: with MK = MR the rows' quantization chains interleave
+// (M = 4: 0.3-0.56 µs per launch), with MK = 1 the code of rows 1 .. MR - 1 is gone
 template <int BITS, int G, bool GELU, int ZM, int QM, bool DBG, int MR, int WMAX, bool GREEDY = false, bool NORM = false,
-          bool FULL = false>
+          int MK = 0>
 __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const std::uint8_t* ptiles, const void* pscales,
                                                            const void* paux, int pflags, int pK, int pn_tiles, int ppairs,
                                                            int ptotal, DecodeArgs a) {
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int W = blockDim.x >> 6;
     const int nn = lane & 15, L = lane >> 4;
-    const int M = FULL ? MR : (pflags & 0xFF), K = pK, k_tiles = K / (512 / BITS), n_tiles = pn_tiles, x_f32 = (pflags >> 8) & 1;
+    const int M = MK > 0 ? MK : (pflags & 0xFF), K = pK, k_tiles = K / (512 / BITS), n_tiles = pn_tiles, x_f32 = (pflags >> 8) & 1;
     const int scale_half = (pflags >> 9) & 1, aux_half = (pflags >> 10) & 1, groups_p = K / G;
     const int aslot = nn >> 2;  // A-operand row of this lane: activation row (nn & 3) + 4 h, group slot
 
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
             // bf16 needs one 16-byte word per piece. With four rows a second load, even one past the buffer, costs
             // more than a uniform branch around it (0.14-0.17 µs); at M = 1 the branch costs more (0.04 µs), so
             // there the second load goes past the buffer (the range check returns zeros without a memory request)
-            if constexpr (FULL) xr[m][1] = x_f32 ? ld16(xres, off + 16) : make_uint4(0, 0, 0, 0);
+            if constexpr (MK == MR) xr[m][1] = x_f32 ? ld16(xres, off + 16) : make_uint4(0, 0, 0, 0);
             else xr[m][1] = ld16(xres, x_f32 ? off + 16 : 0x80000000u);
         }
     }
@@ -535,7 +536,7 @@ __global__ __launch_bounds__(64 * WMAX) void decode_kernel(const void* px, const
     // sum the four group slots (lanes nn + 16 L) and the waves
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
-        if constexpr (FULL && MR == 4) {
+        if constexpr (MK == 4 && MR == 4) {
             // four rows at once: permlane16_swap of rows 0 and 1 leaves, summed, row 0's slots L, L ^ 1 in 16-lane
             // rows 0 and 2 and row 1's in 1 and 3 (rows 2 and 3 likewise); permlane32_swap of the two then leaves
             // row L's total in 16-lane row L, added in the same order as below: (slots 0 + 1) + (slots 2 + 3)
@@ -647,9 +648,14 @@ hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds,
         }
     }
     if constexpr (BITS == 4 && G == 128 && QM == dev::QUANT_DYN_SYM && !DBG && !GREEDY) {
-        if (a.M == 4) {  // configs[1]'s M = 4 projections: the row count fixed at compile time
-            if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 16, false, false, true>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
-            else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 4, false, false, true>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
+        if (a.M == 4) {  // configs[1]'s M = 4 and M = 1 projections: the row count fixed at compile time
+            if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 16, false, false, 4>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
+            else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 4, false, false, 4>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
+            return hipGetLastError();
+        }
+        if (a.M == 1) {
+            if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 16, false, false, 1>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
+            else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 4, false, false, 1>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
             return hipGetLastError();
         }
     }
