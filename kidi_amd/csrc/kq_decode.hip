@@ -647,13 +647,6 @@ hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds,
             return hipGetLastError();
         }
     }
-    if constexpr (BITS == 8 && G == 32 && QM == dev::QUANT_DYN_ASYM && !DBG) {
-        if (a.M == 1) {  // 8-bit at M = 1 (the int8 output head walks 16 units per workgroup: its tail repeats per unit)
-            if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 16, GREEDY, false, 1>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
-            else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 4, GREEDY, false, 1>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
-            return hipGetLastError();
-        }
-    }
     if constexpr (BITS == 4 && G == 128 && QM == dev::QUANT_DYN_SYM && !DBG && !GREEDY) {
         if (a.M == 4) {  // configs[1]'s M = 4 and M = 1 projections: the row count fixed at compile time
             if (wide) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 16, false, false, 4>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
