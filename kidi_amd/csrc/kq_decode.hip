@@ -642,6 +642,12 @@ hipError_t launch_g(const DecodeArgs& a, dim3 grid, dim3 block, std::size_t lds,
     if constexpr (!DBG && !GREEDY) {
         if (a.norm) {  // decode_fits admits the fused normalization only for the 4-wave variants
             if (wide) return hipErrorInvalidValue;
+            if constexpr (BITS == 4 && G == 128 && QM == dev::QUANT_DYN_SYM) {
+                if (a.M == 1) {  // the row count fixed at compile time, as for the unnormalized projections below
+                    hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 4, false, true, 1>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
+                    return hipGetLastError();
+                }
+            }
             if (a.M <= 4) hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 4, 4, false, true>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
             else hipLaunchKernelGGL((decode_kernel<BITS, G, GELU, ZM, QM, false, 8, 4, false, true>), grid, block, lds, stream, KQ_DECODE_ARGS(a));
             return hipGetLastError();
